@@ -1,0 +1,184 @@
+"""Benchmark of the batched ragged decode pass on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c3] [--no-cpu]
+
+Workload (the metric's configuration): the
+27B-class dense q8 model (64 layers, d 5120, 40/8 heads, head_dim 128, FFN
+17408, vocab 151936, tied head; random-init int8 weights with one f16 scale
+per 32) serving 32 concurrent chats whose contexts are drawn log-uniform in
+[128, 16384] (seeded), int8 KV prefilled with random codes. One step = one
+packed pass: every chat's next token as one row, 64 blocks with the f16
+residual round after each, the LM head and greedy sampling on the GPU; the
+sampled ids feed the next step. Inputs are resident in HBM when timing
+starts; each timed step includes its tiny host->device job table and the
+device->host copy of the 32 sampled ids.
+
+Prints one JSON line: aggregate decode tok/s, the HBM roofline of the
+dominant kernel (the q8 projection GEMM, timed with HIP events on the
+library's stream), and the CPU oracle timed on a bounded sample of the
+same step.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def contexts(n, lo, hi, seed):
+    rng = np.random.default_rng(seed)
+    return np.round(np.exp(rng.uniform(math.log(lo), math.log(hi), n))).astype(int)
+
+
+def step_bytes(d, pasts):
+    """Algorithmic HBM bytes of one decode step: every q8 weight once (int8 +
+    f16 scale per 32), every chat's K and V rows once per layer (reference
+    layout: 144 B per row at D = 128), and the appended rows."""
+    from chattorrent_amd import configs
+    kv = configs.kv_token_bytes(d)
+    L = d["n_layer"]
+    return configs.weight_bytes(d) + sum(int(p) + 1 for p in pasts) * L * kv + len(pasts) * L * kv
+
+
+def cpu_baseline(d, pasts, ids, seed, layers=1):
+    """The CPU oracle (C, OpenMP) on a bounded sample of the same step: `layers`
+    blocks of the 64 plus the LM head for all 32 rows, scaled to a whole step."""
+    from oracle import model as Mo
+    from oracle import lib as L
+    import oracle.lib  # noqa: F401
+    ds = dict(d, n_layer=layers)
+    n_max = int(max(pasts)) + 2
+    om = Mo.Model(ds, n_slots=len(pasts), max_pages=-(-n_max // 64))
+    om.gen_weights(seed)
+    for s, T in enumerate(pasts):
+        om.fill_random_kv(s, int(T), seed, s + 1)
+    jobs = [dict(slot=s, past=int(T), n=1, ids=[int(ids[s])], sampled=1, topk=1) for s, T in enumerate(pasts)]
+    t0 = time.perf_counter()
+    om.pass_(jobs, head=False)
+    t_blocks = time.perf_counter() - t0
+    hs = np.ones((len(pasts), d["hidden"]), np.float32)
+    t0 = time.perf_counter()
+    L.matmul_q8(hs, *om.head_weight(), group=32)
+    t_head = time.perf_counter() - t0
+    ms_step = (t_blocks / layers * d["n_layer"] + t_head) * 1000.0
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(len(pasts) / (ms_step / 1000.0), 3), "unit": "tok/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle (C restatement, OpenMP) on {layers} of {d['n_layer']} blocks + the LM head of one "
+                      f"32-row decode step, scaled to the whole step ({ms_step:.0f} ms/step)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--chats", type=int, default=32)
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=1)
+    ap.add_argument("--layers", type=int, default=None, help="fewer layers (debug only; not a valid bench)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: every box here has one GPU and this build has no multi-GPU path "
+              "(a data-parallel replica per GPU would need no exchange; see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    from chattorrent_amd import configs
+    from chattorrent_amd.ccdecode import Context
+
+    d = dict(configs.M27B)
+    if args.layers:
+        d["n_layer"] = args.layers
+    chats = args.chats
+    pasts = contexts(chats, 128, 16384, args.seed)
+    total = args.warmup + args.steps
+    n_max = int(64 * math.ceil((pasts.max() + total + 8) / 64))
+    print(f"[bench] creating context: {d['n_layer']} layers, {chats} chats, n_max {n_max}", file=sys.stderr,
+          flush=True)
+    ctx = Context(d, n_max=n_max, t_max=chats, slots=chats, sessions=chats, max_jobs=chats)
+    ctx.fill_random(args.seed)
+    for s, T in enumerate(pasts):
+        ctx.fill_random_kv(s, int(T), args.seed, s + 1)
+    ids = np.random.default_rng(args.seed + 1).integers(0, d["vocab"], chats)
+    ids0 = ids.copy()
+    pasts0 = pasts.copy()
+    print(f"[bench] filled weights and KV; contexts {int(pasts.min())}..{int(pasts.max())} "
+          f"mean {pasts.mean():.0f}", file=sys.stderr, flush=True)
+
+    def step(p, toks):
+        jobs = [dict(slot=s, past=int(p[s]), n=1, ids=[int(toks[s])], sampled=1) for s in range(chats)]
+        _, out = ctx.step(jobs, topk=1)
+        return out[:, 0].astype(np.int64)
+
+    for _ in range(args.warmup):
+        ids = step(pasts, ids)
+        pasts = pasts + 1
+    timed_pasts = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        timed_pasts.append(pasts.copy())
+        ids = step(pasts, ids)
+        pasts = pasts + 1
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1000.0 / args.steps
+    tok_s = chats / (ms / 1000.0)
+    bytes_avg = float(np.mean([step_bytes(d, p) for p in timed_pasts]))
+    step_frac = bytes_avg / (ms / 1000.0) / (HBM_PEAK_GBS * 1e9)
+    print(f"[bench] {ms:.3f} ms/step, {tok_s:.1f} tok/s, step bytes {bytes_avg / 1e9:.2f} GB "
+          f"-> {bytes_avg / (ms / 1000.0) / 1e9:.0f} GB/s ({step_frac * 100:.1f}% of 8 TB/s)",
+          file=sys.stderr, flush=True)
+
+    # The dominant kernel: the q8 projection GEMM (every block's q|k|v, o,
+    # gate|up and down, and the LM head) — timed per launch with HIP events on
+    # the library's stream over a second region of the same steps.
+    ctx.profile(True)
+    for _ in range(args.steps):
+        ids = step(pasts, ids)
+        pasts = pasts + 1
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    g_ms = sum(prof[k][0] for k in ("qkv", "o", "gate_up", "down", "head"))
+    g_n = sum(prof[k][1] for k in ("qkv", "o", "gate_up", "down", "head"))
+    g_b = sum(prof[k][2] for k in ("qkv", "o", "gate_up", "down", "head"))
+    achieved = g_b / (g_ms / 1000.0) / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_gemm_q8 (all q8 projections + LM head)",
+            "avg_launch_us": round(g_ms * 1000.0 / max(g_n, 1), 2),
+            "bytes_per_launch": round(g_b / max(g_n, 1)),
+            "per_kind": {k: {"ms_per_step": round(v[0] / args.steps, 4), "launches": v[1],
+                             "GBps": round(v[2] / (v[0] / 1000.0) / 1e9, 1) if v[0] > 0 else None}
+                         for k, v in prof.items()}}
+    print(f"[bench] profile: {json.dumps(roof['per_kind'])}", file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(d, pasts0, ids0, args.seed, layers=args.cpu_layers)
+    line = {
+        "metric": "aggregate decode tok/s @32 ragged chats, 27B q8; % of HBM roofline",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 weights x f32 activations (f16 hi/lo MFMA), f32 accumulate",
+        "data": "synthetic: random-init q8 weights, random int8 KV, seeded contexts",
+        "config": {"workload": "configs[2]: 27B-class q8 (64 layers, d5120, 40/8 heads, ffn 17408, vocab 151936), "
+                               "32 chats, contexts log-uniform [128,16384], greedy decode, one packed pass per step",
+                   "chats": chats, "layers": d["n_layer"], "mean_context": float(pasts0.mean()),
+                   "step_hbm_bytes": bytes_avg, "step_frac_of_hbm_peak": round(step_frac, 4)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

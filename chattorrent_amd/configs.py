@@ -1,0 +1,43 @@
+"""Model shapes of the benchmark configurations (dims as loader.js
+dimsFromManifest names them, web/model/loader.js:146-201).
+
+The shapes are the ones the benchmark names; RoPE theta and eps are not given
+there and are pinned here. SmolLM2's come from the reference's DIMS
+(web/model/kernels.js:23-37); the 27B-class and 8B shapes use theta 1e6 /
+eps 1e-6 and Llama 3.1's published values respectively.
+"""
+
+SMOLLM2 = dict(hidden=576, n_layer=30, n_heads=9, n_kv_heads=3, head_dim=64, ffn=1536, vocab=49152,
+               rms_eps=1e-5, rope_theta=100000.0, tied=True, group_q8=32)
+
+# 27B-class dense block: d 5120, 40 q / 8 kv heads, head_dim 128, SwiGLU 17408.
+M27B = dict(hidden=5120, n_layer=64, n_heads=40, n_kv_heads=8, head_dim=128, ffn=17408, vocab=151936,
+            rms_eps=1e-6, rope_theta=1000000.0, tied=True, group_q8=32)
+
+BLOCK27B = dict(M27B, n_layer=1)
+
+LLAMA8B = dict(hidden=4096, n_layer=32, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=128256,
+               rms_eps=1e-5, rope_theta=500000.0, tied=False, group_q8=32,
+               rope_scaling=dict(factor=8.0, low_freq_factor=1.0, high_freq_factor=4.0,
+                                 original_max_position_embeddings=8192))
+
+
+def with_layers(d, n):
+    out = dict(d)
+    out["n_layer"] = n
+    return out
+
+
+def weight_bytes(d):
+    """Stored bytes of the q8 weights: int8 + one f16 scale per 32 (1.0625 B/w),
+    embedding counted once when tied (web/model/model.js:721-734 weightBudget)."""
+    H, D, F = d["hidden"], d["head_dim"], d["ffn"]
+    per_layer = (d["n_heads"] * D * H + 2 * d["n_kv_heads"] * D * H + H * d["n_heads"] * D + 3 * F * H)
+    params = d["n_layer"] * per_layer + d["vocab"] * H * (1 if d.get("tied", True) else 2)
+    return params * (1 + 2 / 32)
+
+
+def kv_token_bytes(d):
+    """K and V bytes of one token in one layer: web/split.js:132 kvRowBytes x 2."""
+    D = d["head_dim"]
+    return 2 * d["n_kv_heads"] * (D + 4 * D // min(32, D))

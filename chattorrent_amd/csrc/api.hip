@@ -1,0 +1,1077 @@
+// C ABI of the MI355X batched ragged decode pass (include/ccdecode.h).
+//
+// A context plays the GPU half of the reference's Runner
+// (web/model/stage.js): it owns the held positions' weights, the paged int8
+// KV pool with its page tables and free stack, and the scratch of one pass.
+// cc_step is Runner.#pass (web/model/stage.js:1314-1481): it packs the jobs'
+// rows, takes their pages, runs the embedding, the blocks and the head, and
+// returns candidates or rows. The caller keeps the Runner's policy (queue,
+// batching, admission, eviction); the library validates every job before any
+// device work and reports a status per job.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/ccdecode.h"
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int TOPK_MAX = 256;   // web/model/sampling.js:125
+
+struct Layer {
+    QTensor qkv, o, gu, down;
+    float* ln1 = nullptr;
+    float* ln2 = nullptr;
+    uint8_t* kpool = nullptr;
+    uint8_t* vpool = nullptr;
+};
+
+int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace
+
+struct cc_ctx {
+    cc_dims d{};
+    cc_opts o{};
+    int group = 0, D = 0, rot = 0, L0 = 0, L1 = 0;
+    bool embed = false, head = false;
+    std::vector<Layer> layers;
+    QTensor wte, lm_head;
+    float* norm = nullptr;
+    float* tbl = nullptr;
+    int tbl_cap = 0;
+    KVGeom geom{};
+    int n_pages = 0, max_pages = 0;
+    uint32_t* page_table = nullptr;
+    uint32_t* free_stack = nullptr;
+    std::vector<int> owned;
+    int top = 0;
+    // scratch
+    int mt_alloc = 0;              // operand m-tiles allocated (even)
+    float* x = nullptr;            // residual [t_max][H]
+    uint4* xp_h = nullptr;         // operand for K = hidden
+    uint4* xp_o = nullptr;         // operand for K = nH*D
+    uint4* xp_f = nullptr;         // operand for K = ffn
+    float* part = nullptr;
+    size_t part_floats = 0;
+    uint4* qp = nullptr;
+    size_t qp_units = 0;
+    float* apart = nullptr;
+    size_t apart_floats = 0;
+    AttnItem* d_items = nullptr;
+    size_t items_cap = 0;
+    float* logits = nullptr;
+    uint64_t* tk_a = nullptr;
+    uint64_t* tk_b = nullptr;
+    float* d_vals = nullptr;
+    uint32_t* d_ids = nullptr;
+    uint16_t* d_hbits = nullptr;
+    // per-step metadata (device) and its pinned host staging
+    uint8_t* d_meta = nullptr;
+    uint8_t* h_meta = nullptr;
+    size_t meta_bytes = 0;
+    void* h_out = nullptr;
+    size_t out_bytes = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    uint64_t weight_bytes = 0, kv_bytes = 0, scratch_bytes = 0;
+    int64_t passes = 0, rows = 0;
+    double last_ms = 0;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    std::vector<void*> allocs;
+    // opt-in per-kernel profile (cc_profile)
+    bool prof = false;
+    std::vector<hipEvent_t> pev;               // event pool, pairs
+    struct Mark { int kind; int e0, e1; double bytes; };
+    std::vector<Mark> marks;
+    double prof_ms[CC_K_COUNT] = {0};
+    int64_t prof_n[CC_K_COUNT] = {0};
+    double prof_bytes[CC_K_COUNT] = {0};
+};
+
+namespace {
+
+cc_status fail(cc_ctx* c, cc_status s, const std::string& msg) {
+    if (c) c->err = msg;
+    return s;
+}
+
+#define HIPCHK(expr)                                                                               \
+    do {                                                                                           \
+        hipError_t e_ = (expr);                                                                    \
+        if (e_ != hipSuccess)                                                                      \
+            return fail(ctx, e_ == hipErrorOutOfMemory ? CC_EOOM : CC_EDEVICE,                     \
+                        std::string(#expr) + ": " + hipGetErrorString(e_));                        \
+    } while (0)
+
+template <class T>
+hipError_t dalloc(cc_ctx* ctx, T** p, size_t bytes, uint64_t* acct) {
+    void* v = nullptr;
+    hipError_t e = hipMalloc(&v, bytes ? bytes : 16);
+    if (e != hipSuccess) return e;
+    e = hipMemset(v, 0, bytes ? bytes : 16);
+    if (e != hipSuccess) return e;
+    ctx->allocs.push_back(v);
+    if (acct) *acct += bytes;
+    *p = (T*)v;
+    return hipSuccess;
+}
+
+// K splits of a projection: from N and K only (never M), so every row gets the
+// same reduction whatever the batch.
+int splits_for(const QTensor& w, int nt) {
+    const int strips = w.Nt / nt;
+    int s = ceil_div(640, std::max(strips, 1));
+    s = std::min(s, std::max(1, w.KU / 16));
+    return std::max(1, s);
+}
+
+hipError_t alloc_q(cc_ctx* ctx, QTensor& q, int N, int K) {
+    q.N = N;
+    q.K = K;
+    q.Nt = ceil_div(ceil_div(N, 16), 4) * 4;   // strips of 4 n-tiles
+    q.KU = ceil_div(K, 64);
+    hipError_t e = dalloc(ctx, &q.codes, (size_t)q.Nt * q.KU * 1024, &ctx->weight_bytes);
+    if (e != hipSuccess) return e;
+    return dalloc(ctx, &q.scales, (size_t)q.Nt * q.KU * 64, &ctx->weight_bytes);
+}
+
+void build_rope_table(cc_ctx* ctx, std::vector<float>& t) {
+    // web/model/kernels.js:2016-2045 ropeTable: f64 cos/sin, rounded to f32.
+    const int half = ctx->rot / 2;
+    t.assign((size_t)ctx->tbl_cap * ctx->rot, 0.0f);
+    const cc_dims& d = ctx->d;
+    for (int i = 0; i < half; i++) {
+        double inv = std::pow(d.rope_theta, -(2.0 * i) / (double)ctx->rot);
+        if (d.rope_scaling == 1) {
+            const double PI = 3.14159265358979323846;
+            double wavelen = (2.0 * PI) / inv;
+            double lowW = d.rs_orig_max_pos / d.rs_low_freq, highW = d.rs_orig_max_pos / d.rs_high_freq;
+            if (wavelen < highW) {
+            } else if (wavelen > lowW) {
+                inv = inv / d.rs_factor;
+            } else {
+                double smooth = (d.rs_orig_max_pos / wavelen - d.rs_low_freq) / (d.rs_high_freq - d.rs_low_freq);
+                inv = smooth * inv + (1.0 - smooth) * (inv / d.rs_factor);
+            }
+        }
+        for (int pos = 0; pos < ctx->tbl_cap; pos++) {
+            double ang = (double)pos * inv;
+            t[((size_t)pos * half + i) * 2] = (float)std::cos(ang);
+            t[((size_t)pos * half + i) * 2 + 1] = (float)std::sin(ang);
+        }
+    }
+}
+
+cc_status check_dims(cc_ctx* ctx, const cc_dims& d, const cc_opts& o) {
+    // web/model/model.js:22-40 checkDims, plus what these kernels assume.
+    if (d.hidden <= 0 || d.n_layer <= 0 || d.n_heads <= 0 || d.n_kv_heads <= 0 || d.head_dim <= 0 ||
+        d.ffn <= 0 || d.vocab <= 0)
+        return fail(ctx, CC_EARG, "every dimension must be positive");
+    if (d.n_heads * d.head_dim != d.hidden)
+        return fail(ctx, CC_EARG, "n_heads*head_dim (" + std::to_string(d.n_heads * d.head_dim) +
+                                      ") != hidden (" + std::to_string(d.hidden) + ")");
+    if (d.n_heads % d.n_kv_heads != 0) return fail(ctx, CC_EARG, "n_heads not divisible by n_kv_heads");
+    if (d.head_dim != 64 && d.head_dim != 128)
+        return fail(ctx, CC_EARG, "head_dim must be 64 or 128 (the int8 KV blocks are 32 wide)");
+    if (d.q8_group != 32) return fail(ctx, CC_EARG, "q8 weights must use one scale per 32 values");
+    if (d.hidden % 64 || d.ffn % 16) return fail(ctx, CC_EARG, "hidden must be a multiple of 64, ffn of 16");
+    if ((d.n_kv_heads * d.head_dim) % 16) return fail(ctx, CC_EARG, "n_kv_heads*head_dim must be a multiple of 16");
+    if (d.hidden > 16384) return fail(ctx, CC_EARG, "hidden above 16384 is not supported");
+    const int positions = d.n_layer + 2;
+    if (o.lo < 0 || o.hi > positions || o.lo >= o.hi) return fail(ctx, CC_EARG, "bad position range");
+    if (o.n_max <= 0 || o.t_max <= 0 || o.slots <= 0 || o.sessions <= 0 || o.max_jobs <= 0)
+        return fail(ctx, CC_EARG, "n_max, t_max, slots, sessions and max_jobs must be positive");
+    if (o.page_tokens != 64) return fail(ctx, CC_EARG, "page_tokens must be 64 (web/split.js:75)");
+    if (o.t_max > 4096) return fail(ctx, CC_EARG, "t_max above 4096 rows is not supported");
+    return CC_OK;
+}
+
+struct StepPlan {
+    int T = 0, S = 0, nitems = 0;
+    std::vector<JobDev> jobs;
+    std::vector<AttnItem> items;
+    std::vector<int32_t> row_job, plan, head_rows;
+    size_t qp_units = 0, apart_floats = 0;
+    double kv_bytes = 0;   // K and V rows one layer's attention reads (reference row size)
+};
+
+// Per-step metadata: jobs, items, row_job, plan, head_rows, ids | hidden.
+struct MetaLayout {
+    size_t jobs, items, row_job, plan, head_rows, ids, hidden, total;
+};
+
+MetaLayout meta_layout(int max_jobs, size_t max_items, int t_max, int H) {
+    MetaLayout m{};
+    size_t at = 0;
+    auto take = [&](size_t bytes) { size_t r = at; at += (bytes + 255) & ~(size_t)255; return r; };
+    m.jobs = take(sizeof(JobDev) * max_jobs);
+    m.items = take(sizeof(AttnItem) * max_items);
+    m.row_job = take(4 * (size_t)t_max);
+    m.plan = take(16 * (size_t)max_jobs);
+    m.head_rows = take(4 * (size_t)t_max);
+    m.ids = take(4 * (size_t)t_max);
+    m.hidden = take(2 * (size_t)t_max * H);
+    m.total = at;
+    return m;
+}
+
+// Profile marks: an event pair around one launch, resolved after the step's
+// synchronisation.
+int prof_begin(cc_ctx* ctx) {
+    if (!ctx->prof) return -1;
+    const int e = (int)ctx->marks.size() * 2;
+    while ((int)ctx->pev.size() < e + 2) {
+        hipEvent_t ev;
+        if (hipEventCreate(&ev) != hipSuccess) return -1;
+        ctx->pev.push_back(ev);
+    }
+    hipEventRecord(ctx->pev[e], ctx->stream);
+    return e;
+}
+
+void prof_end(cc_ctx* ctx, int e, int kind, double bytes) {
+    if (e < 0) return;
+    hipEventRecord(ctx->pev[e + 1], ctx->stream);
+    ctx->marks.push_back(cc_ctx::Mark{kind, e, e + 1, bytes});
+}
+
+void prof_collect(cc_ctx* ctx) {
+    for (const auto& m : ctx->marks) {
+        float ms = 0;
+        if (hipEventElapsedTime(&ms, ctx->pev[m.e0], ctx->pev[m.e1]) == hipSuccess) {
+            ctx->prof_ms[m.kind] += ms;
+            ctx->prof_n[m.kind] += 1;
+            ctx->prof_bytes[m.kind] += m.bytes;
+        }
+    }
+    ctx->marks.clear();
+}
+
+double qbytes(const QTensor& q) { return (double)q.N * q.K * (1.0 + 2.0 / 32.0); }
+
+size_t max_items_for(const cc_ctx* ctx) {
+    // Every chunk of 4 pages of every frame that could be in a pass.
+    const int jobs = std::min(ctx->o.max_jobs, ctx->o.sessions);
+    return (size_t)jobs * ctx->geom.nKV * ceil_div(ctx->max_pages, 4) + 16;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* cc_last_error(const cc_ctx* ctx) { return ctx ? ctx->err.c_str() : "no context"; }
+
+void cc_destroy(cc_ctx* ctx) {
+    if (!ctx) return;
+    if (ctx->stream) hipStreamSynchronize(ctx->stream);
+    for (void* p : ctx->allocs) hipFree(p);
+    if (ctx->h_meta) hipHostFree(ctx->h_meta);
+    if (ctx->h_out) hipHostFree(ctx->h_out);
+    if (ctx->ev0) hipEventDestroy(ctx->ev0);
+    if (ctx->ev1) hipEventDestroy(ctx->ev1);
+    for (hipEvent_t e : ctx->pev) hipEventDestroy(e);
+    if (ctx->stream) hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
+    if (!dims || !opts || !out) return CC_EARG;
+    *out = nullptr;
+    cc_ctx* ctx = new cc_ctx();
+    ctx->d = *dims;
+    ctx->o = *opts;
+    cc_status st = check_dims(ctx, *dims, *opts);
+    if (st != CC_OK) {
+        *out = ctx;   // the caller reads the message, then destroys
+        return st;
+    }
+    const cc_dims& d = ctx->d;
+    const cc_opts& o = ctx->o;
+    {
+        hipError_t e = hipSetDevice(o.device);
+        if (e != hipSuccess) {
+            *out = ctx;
+            return fail(ctx, CC_EDEVICE, std::string("hipSetDevice: ") + hipGetErrorString(e));
+        }
+    }
+    auto body = [&]() -> cc_status {
+        HIPCHK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+        HIPCHK(hipEventCreate(&ctx->ev0));
+        HIPCHK(hipEventCreate(&ctx->ev1));
+        ctx->group = d.n_heads / d.n_kv_heads;
+        ctx->D = d.head_dim;
+        ctx->rot = d.head_dim;
+        const int positions = d.n_layer + 2;
+        ctx->embed = o.lo == 0;
+        ctx->head = o.hi == positions;
+        ctx->L0 = std::max(o.lo, 1) - 1;
+        ctx->L1 = std::min(o.hi, d.n_layer + 1) - 1;
+        if (ctx->L1 < ctx->L0) ctx->L1 = ctx->L0;
+        const int H = d.hidden, F = d.ffn, nH = d.n_heads, nKV = d.n_kv_heads, D = d.head_dim;
+        // KV geometry and pool (web/model/model.js:132-147, stage.js:155-187).
+        ctx->geom.nKV = nKV;
+        ctx->geom.D = D;
+        ctx->geom.ng = D / 32;
+        ctx->geom.page = o.page_tokens;
+        ctx->geom.blk = 64 * D + 64 * (D / 32) * 4;
+        ctx->max_pages = ceil_div(o.n_max, o.page_tokens);
+        ctx->geom.max_pages = ctx->max_pages;
+        ctx->n_pages = o.slots * ctx->max_pages;
+        ctx->owned.assign(o.sessions, 0);
+        HIPCHK(dalloc(ctx, &ctx->page_table, (size_t)o.sessions * ctx->max_pages * 4, &ctx->scratch_bytes));
+        HIPCHK(dalloc(ctx, &ctx->free_stack, (size_t)ctx->n_pages * 4, &ctx->scratch_bytes));
+        {
+            // Lowest index pops first (model.js:145-146): stack[i] = n_pages-1-i.
+            std::vector<uint32_t> fs(ctx->n_pages);
+            for (int i = 0; i < ctx->n_pages; i++) fs[i] = (uint32_t)(ctx->n_pages - 1 - i);
+            HIPCHK(hipMemcpy(ctx->free_stack, fs.data(), fs.size() * 4, hipMemcpyHostToDevice));
+            ctx->top = ctx->n_pages;
+        }
+        const size_t pool_bytes = (size_t)ctx->n_pages * nKV * ctx->geom.blk;
+        ctx->layers.resize(ctx->L1 - ctx->L0);
+        for (auto& L : ctx->layers) {
+            HIPCHK(alloc_q(ctx, L.qkv, (nH + 2 * nKV) * D, H));
+            HIPCHK(alloc_q(ctx, L.o, H, nH * D));
+            HIPCHK(alloc_q(ctx, L.gu, 2 * F, H));
+            HIPCHK(alloc_q(ctx, L.down, H, F));
+            HIPCHK(dalloc(ctx, &L.ln1, (size_t)H * 4, &ctx->weight_bytes));
+            HIPCHK(dalloc(ctx, &L.ln2, (size_t)H * 4, &ctx->weight_bytes));
+            launch_fill(ctx->stream, L.ln1, H, 1.0f);
+            launch_fill(ctx->stream, L.ln2, H, 1.0f);
+            HIPCHK(dalloc(ctx, &L.kpool, pool_bytes, &ctx->kv_bytes));
+            HIPCHK(dalloc(ctx, &L.vpool, pool_bytes, &ctx->kv_bytes));
+        }
+        if (ctx->embed || (ctx->head && d.tied)) HIPCHK(alloc_q(ctx, ctx->wte, d.vocab, H));
+        if (ctx->head) {
+            HIPCHK(dalloc(ctx, &ctx->norm, (size_t)H * 4, &ctx->weight_bytes));
+            launch_fill(ctx->stream, ctx->norm, H, 1.0f);
+            if (!d.tied) HIPCHK(alloc_q(ctx, ctx->lm_head, d.vocab, H));
+        }
+        // RoPE table for every position a frame can reach.
+        ctx->tbl_cap = ctx->max_pages * o.page_tokens + 64;
+        {
+            std::vector<float> t;
+            build_rope_table(ctx, t);
+            HIPCHK(dalloc(ctx, &ctx->tbl, t.size() * 4, &ctx->scratch_bytes));
+            HIPCHK(hipMemcpy(ctx->tbl, t.data(), t.size() * 4, hipMemcpyHostToDevice));
+        }
+        // Scratch for t_max rows.
+        const int T = o.t_max;
+        ctx->mt_alloc = 2 * ceil_div(T, 32);
+        auto xp_bytes = [&](int K) { return (size_t)ctx->mt_alloc * 2 * ceil_div(K, 64) * 2 * 1024; };
+        HIPCHK(dalloc(ctx, &ctx->x, (size_t)T * H * 4, &ctx->scratch_bytes));
+        HIPCHK(dalloc(ctx, &ctx->xp_h, xp_bytes(H), &ctx->scratch_bytes));
+        HIPCHK(dalloc(ctx, &ctx->xp_o, xp_bytes(nH * D), &ctx->scratch_bytes));
+        HIPCHK(dalloc(ctx, &ctx->xp_f, xp_bytes(F), &ctx->scratch_bytes));
+        size_t pf = 16;
+        if (!ctx->layers.empty()) {
+            const Layer& L = ctx->layers[0];
+            for (const QTensor* q : {&L.qkv, &L.o, &L.gu, &L.down})
+                pf = std::max(pf, (size_t)splits_for(*q, 4) * T * q->N);
+        }
+        ctx->part_floats = pf;
+        HIPCHK(dalloc(ctx, &ctx->part, pf * 4, &ctx->scratch_bytes));
+        // Q operands: sum over jobs of nKV * ceil(n*group/16) * ng * 2 * 64 uint4.
+        ctx->qp_units = (size_t)(ceil_div(T * ctx->group, 16) + o.max_jobs) * nKV * (D / 32) * 128;
+        HIPCHK(dalloc(ctx, &ctx->qp, ctx->qp_units * 16, &ctx->scratch_bytes));
+        ctx->items_cap = max_items_for(ctx);
+        // Attention partials: per item 16*mtq rows of (D + 2). Sized for the
+        // worst packing: every item at the largest m-tile count.
+        ctx->apart_floats = ctx->items_cap * (size_t)(ceil_div(T * ctx->group, 16) * 16) * (D + 2);
+        ctx->apart_floats = std::min(ctx->apart_floats, (size_t)ctx->items_cap * 16 * (D + 2) *
+                                                            (size_t)(ceil_div(T * ctx->group, 16) + 1));
+        HIPCHK(dalloc(ctx, &ctx->apart, ctx->apart_floats * 4, &ctx->scratch_bytes));
+        if (ctx->head) {
+            HIPCHK(dalloc(ctx, &ctx->logits, (size_t)T * d.vocab * 4, &ctx->scratch_bytes));
+            const size_t keys = (size_t)T * ceil_div(d.vocab, 4096) * TOPK_MAX;
+            HIPCHK(dalloc(ctx, &ctx->tk_a, keys * 8, &ctx->scratch_bytes));
+            HIPCHK(dalloc(ctx, &ctx->tk_b, keys * 8, &ctx->scratch_bytes));
+            HIPCHK(dalloc(ctx, &ctx->d_vals, (size_t)T * TOPK_MAX * 4, &ctx->scratch_bytes));
+            HIPCHK(dalloc(ctx, &ctx->d_ids, (size_t)T * TOPK_MAX * 4, &ctx->scratch_bytes));
+        }
+        HIPCHK(dalloc(ctx, &ctx->d_hbits, (size_t)T * H * 2, &ctx->scratch_bytes));
+        MetaLayout ml = meta_layout(o.max_jobs, ctx->items_cap, T, H);
+        ctx->meta_bytes = ml.total;
+        HIPCHK(dalloc(ctx, &ctx->d_meta, ml.total, &ctx->scratch_bytes));
+        HIPCHK(hipHostMalloc((void**)&ctx->h_meta, ml.total, hipHostMallocDefault));
+        ctx->out_bytes = std::max((size_t)T * TOPK_MAX * 8, (size_t)T * H * 2) + 256;
+        HIPCHK(hipHostMalloc(&ctx->h_out, ctx->out_bytes, hipHostMallocDefault));
+        HIPCHK(hipStreamSynchronize(ctx->stream));
+        return CC_OK;
+    };
+    st = body();
+    *out = ctx;
+    return st;
+}
+
+static QTensor* tensor_of(cc_ctx* ctx, int layer, int tensor, int* row_tile0, int* N, int* K) {
+    const cc_dims& d = ctx->d;
+    const int H = d.hidden, F = d.ffn, D = d.head_dim, nH = d.n_heads, nKV = d.n_kv_heads;
+    if (tensor == CC_T_WTE) { *row_tile0 = 0; *N = d.vocab; *K = H; return ctx->wte.codes ? &ctx->wte : nullptr; }
+    if (tensor == CC_T_LM_HEAD) { *row_tile0 = 0; *N = d.vocab; *K = H; return ctx->lm_head.codes ? &ctx->lm_head : nullptr; }
+    const int li = layer - ctx->L0;
+    if (li < 0 || li >= (int)ctx->layers.size()) return nullptr;
+    Layer& L = ctx->layers[li];
+    switch (tensor) {
+        case CC_T_Q: *row_tile0 = 0; *N = nH * D; *K = H; return &L.qkv;
+        case CC_T_K: *row_tile0 = nH * D / 16; *N = nKV * D; *K = H; return &L.qkv;
+        case CC_T_V: *row_tile0 = (nH + nKV) * D / 16; *N = nKV * D; *K = H; return &L.qkv;
+        case CC_T_O: *row_tile0 = 0; *N = H; *K = nH * D; return &L.o;
+        case CC_T_GATE: *row_tile0 = 0; *N = F; *K = H; return &L.gu;
+        case CC_T_UP: *row_tile0 = F / 16; *N = F; *K = H; return &L.gu;
+        case CC_T_DOWN: *row_tile0 = 0; *N = H; *K = F; return &L.down;
+    }
+    return nullptr;
+}
+
+cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data, size_t n, const void* scales,
+                    size_t ns, int32_t scale_dtype, int32_t group) {
+    if (!ctx || !data) return fail(ctx, CC_EARG, "null argument");
+    const cc_dims& d = ctx->d;
+    if (tensor == CC_T_LN1 || tensor == CC_T_LN2 || tensor == CC_T_NORM) {
+        float* dst = nullptr;
+        if (tensor == CC_T_NORM) dst = ctx->norm;
+        else {
+            const int li = layer - ctx->L0;
+            if (li < 0 || li >= (int)ctx->layers.size()) return fail(ctx, CC_EARG, "layer not held here");
+            dst = tensor == CC_T_LN1 ? ctx->layers[li].ln1 : ctx->layers[li].ln2;
+        }
+        if (!dst) return fail(ctx, CC_EARG, "tensor not held here");
+        if (n != (size_t)d.hidden) return fail(ctx, CC_EARG, "a norm weight has `hidden` f32 values");
+        HIPCHK(hipMemcpy(dst, data, n * 4, hipMemcpyHostToDevice));
+        return CC_OK;
+    }
+    int row_tile0 = 0, N = 0, K = 0;
+    QTensor* q = tensor_of(ctx, layer, tensor, &row_tile0, &N, &K);
+    if (!q) return fail(ctx, CC_EARG, "tensor not held here");
+    if (group != 32) return fail(ctx, CC_EARG, "q8 group must be 32");
+    const int ng = ceil_div(K, 32);
+    if (n != (size_t)N * K || ns != (size_t)N * ng || !scales)
+        return fail(ctx, CC_EARG, "q8 tensor needs N*K codes and N*ceil(K/32) scales");
+    std::vector<uint16_t> s16((size_t)N * ng);
+    if (scale_dtype == CC_SCALES_F16) std::memcpy(s16.data(), scales, s16.size() * 2);
+    else for (size_t i = 0; i < s16.size(); i++) s16[i] = half_bits(((const float*)scales)[i]);
+    int8_t* dc = nullptr;
+    uint16_t* ds = nullptr;
+    HIPCHK(hipMalloc(&dc, n));
+    HIPCHK(hipMalloc(&ds, s16.size() * 2));
+    HIPCHK(hipMemcpy(dc, data, n, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(ds, s16.data(), s16.size() * 2, hipMemcpyHostToDevice));
+    launch_tile_q8(ctx->stream, dc, ds, N, K, 32, *q, row_tile0);
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    hipFree(dc);
+    hipFree(ds);
+    return CC_OK;
+}
+
+// Generator streams shared with the test oracle: wte 1, lm_head 2, block
+// tensor t of layer l: (l+1)*16 + t (q, k, v, o, gate, up, down).
+cc_status cc_fill_random(cc_ctx* ctx, uint64_t seed) {
+    if (!ctx) return CC_EARG;
+    const cc_dims& d = ctx->d;
+    for (int li = 0; li < (int)ctx->layers.size(); li++) {
+        const int layer = ctx->L0 + li;
+        for (int t = CC_T_Q; t <= CC_T_DOWN; t++) {
+            int row_tile0, N, K;
+            QTensor* q = tensor_of(ctx, layer, t, &row_tile0, &N, &K);
+            launch_gen_q8(ctx->stream, *q, row_tile0, N, K, seed, (uint64_t)(layer + 1) * 16 + t);
+        }
+    }
+    if (ctx->wte.codes) launch_gen_q8(ctx->stream, ctx->wte, 0, d.vocab, d.hidden, seed, 1);
+    if (ctx->lm_head.codes) launch_gen_q8(ctx->stream, ctx->lm_head, 0, d.vocab, d.hidden, seed, 2);
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return CC_OK;
+}
+
+int32_t cc_slot_pages(const cc_ctx* ctx, int32_t slot) {
+    if (!ctx || slot < 0 || slot >= (int)ctx->owned.size()) return -1;
+    return ctx->owned[slot];
+}
+
+int32_t cc_free_pages(const cc_ctx* ctx) { return ctx ? ctx->top : -1; }
+
+// Takes pages for jobs (slot, tokens) in order: ensurePages replayed on the
+// device. Validates capacity first; nothing changes on failure.
+static cc_status take_pages(cc_ctx* ctx, const std::vector<std::pair<int, int>>& want, int32_t* d_plan,
+                            int32_t* h_plan, int32_t* status) {
+    int total = 0;
+    for (size_t j = 0; j < want.size(); j++) {
+        const int slot = want[j].first, tokens = want[j].second;
+        const int need = ceil_div(tokens, ctx->geom.page);
+        if (need > ctx->max_pages) {
+            if (status) status[j] = CC_EPOOL;
+            return fail(ctx, CC_EPOOL, "the KV pool cannot fit " + std::to_string(tokens) + " tokens for slot " +
+                                           std::to_string(slot) + " (" + std::to_string(ctx->max_pages) +
+                                           " pages of " + std::to_string(ctx->geom.page) + " per frame)");
+        }
+        const int nw = std::max(0, need - ctx->owned[slot]);
+        h_plan[4 * j] = slot;
+        h_plan[4 * j + 1] = ctx->owned[slot];
+        h_plan[4 * j + 2] = nw;
+        h_plan[4 * j + 3] = total;
+        total += nw;
+    }
+    if (total > ctx->top) {
+        if (status) for (size_t j = 0; j < want.size(); j++) status[j] = CC_BUSY;
+        return fail(ctx, CC_BUSY, "no KV page free for the pass (" + std::to_string(total) + " needed, " +
+                                      std::to_string(ctx->top) + " free)");
+    }
+    if (total > 0) {
+        launch_alloc_pages(ctx->stream, d_plan, (int)want.size(), ctx->free_stack, ctx->top, ctx->page_table,
+                           ctx->max_pages);
+        for (size_t j = 0; j < want.size(); j++) ctx->owned[want[j].first] += h_plan[4 * j + 2];
+        ctx->top -= total;
+    }
+    return CC_OK;
+}
+
+cc_status cc_release(cc_ctx* ctx, int32_t slot) {
+    if (!ctx || slot < 0 || slot >= (int)ctx->owned.size()) return fail(ctx, CC_EARG, "bad slot");
+    const int n = ctx->owned[slot];
+    launch_release_pages(ctx->stream, slot, n, ctx->free_stack, ctx->top, ctx->page_table, ctx->max_pages);
+    ctx->top += n;
+    ctx->owned[slot] = 0;
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return CC_OK;
+}
+
+cc_status cc_fill_random_kv(cc_ctx* ctx, int32_t slot, int32_t tokens, uint64_t seed, uint64_t key) {
+    if (!ctx || slot < 0 || slot >= (int)ctx->owned.size() || tokens < 0 || tokens > ctx->o.n_max)
+        return fail(ctx, CC_EARG, "bad slot or token count");
+    int32_t* h_plan = (int32_t*)ctx->h_meta;
+    int32_t* d_plan = (int32_t*)ctx->d_meta;
+    std::vector<std::pair<int, int>> want{{slot, tokens}};
+    const int need = ceil_div(tokens, ctx->geom.page);
+    if (need > ctx->max_pages) return fail(ctx, CC_EPOOL, "the fill exceeds the frame's pages");
+    h_plan[0] = slot; h_plan[1] = ctx->owned[slot]; h_plan[2] = std::max(0, need - ctx->owned[slot]); h_plan[3] = 0;
+    HIPCHK(hipMemcpyAsync(d_plan, h_plan, 16, hipMemcpyHostToDevice, ctx->stream));
+    cc_status st = take_pages(ctx, want, d_plan, h_plan, nullptr);
+    if (st != CC_OK) return st;
+    for (int li = 0; li < (int)ctx->layers.size(); li++) {
+        const int layer = ctx->L0 + li;
+        for (int which = 0; which < 2; which++)
+            launch_fill_kv(ctx->stream, which ? ctx->layers[li].vpool : ctx->layers[li].kpool, ctx->page_table,
+                           slot, tokens, ctx->geom, seed, 0x4B560000ull + (uint64_t)layer * 2 + which, key, which);
+    }
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    return CC_OK;
+}
+
+static cc_status kv_io(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot, int32_t head, int32_t t0,
+                       int32_t t1, uint32_t* out, const uint32_t* in) {
+    const int li = layer - ctx->L0;
+    if (li < 0 || li >= (int)ctx->layers.size() || which < 0 || which > 1 || slot < 0 ||
+        slot >= (int)ctx->owned.size() || head < 0 || head >= ctx->geom.nKV || t0 < 0 || t1 < t0 ||
+        ceil_div(t1, ctx->geom.page) > ctx->owned[slot])
+        return fail(ctx, CC_EARG, "rows outside the slot's pages");
+    const size_t words = (size_t)(t1 - t0) * (ctx->geom.D / 4 + ctx->geom.ng);
+    uint32_t* dbuf = nullptr;
+    HIPCHK(hipMalloc(&dbuf, words * 4 + 16));
+    uint8_t* pool = which ? ctx->layers[li].vpool : ctx->layers[li].kpool;
+    if (out) {
+        launch_kv_to_ref(ctx->stream, pool, ctx->page_table, slot, head, t0, t1, ctx->geom, which, dbuf);
+        HIPCHK(hipStreamSynchronize(ctx->stream));
+        HIPCHK(hipMemcpy(out, dbuf, words * 4, hipMemcpyDeviceToHost));
+    } else {
+        HIPCHK(hipMemcpy(dbuf, in, words * 4, hipMemcpyHostToDevice));
+        launch_kv_from_ref(ctx->stream, pool, ctx->page_table, slot, head, t0, t1, ctx->geom, which, dbuf);
+        HIPCHK(hipStreamSynchronize(ctx->stream));
+    }
+    hipFree(dbuf);
+    return CC_OK;
+}
+
+cc_status cc_read_kv(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot, int32_t head, int32_t t0,
+                     int32_t t1, uint32_t* out) {
+    if (!ctx || !out) return CC_EARG;
+    return kv_io(ctx, layer, which, slot, head, t0, t1, out, nullptr);
+}
+
+cc_status cc_write_kv(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot, int32_t head, int32_t t0,
+                      int32_t t1, const uint32_t* rows) {
+    if (!ctx || !rows) return CC_EARG;
+    return kv_io(ctx, layer, which, slot, head, t0, t1, nullptr, rows);
+}
+
+cc_status cc_read_pages(cc_ctx* ctx, int32_t slot, uint32_t* out, int32_t n) {
+    if (!ctx || !out || slot < 0 || slot >= (int)ctx->owned.size() || n < 0 || n > ctx->max_pages)
+        return fail(ctx, CC_EARG, "bad slot or count");
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    HIPCHK(hipMemcpy(out, ctx->page_table + (size_t)slot * ctx->max_pages, (size_t)n * 4, hipMemcpyDeviceToHost));
+    return CC_OK;
+}
+
+cc_status cc_stats_get(const cc_ctx* ctx, cc_stats* out) {
+    if (!ctx || !out) return CC_EARG;
+    out->weight_bytes = ctx->weight_bytes;
+    out->kv_bytes = ctx->kv_bytes;
+    out->scratch_bytes = ctx->scratch_bytes;
+    out->vram_bytes = ctx->weight_bytes + ctx->kv_bytes + ctx->scratch_bytes;
+    out->passes = ctx->passes;
+    out->rows = ctx->rows;
+    out->last_pass_ms = ctx->last_ms;
+    return CC_OK;
+}
+
+cc_status cc_profile(cc_ctx* ctx, int32_t enable) {
+    if (!ctx) return CC_EARG;
+    ctx->prof = enable != 0;
+    for (int k = 0; k < CC_K_COUNT; k++) { ctx->prof_ms[k] = 0; ctx->prof_n[k] = 0; ctx->prof_bytes[k] = 0; }
+    ctx->marks.clear();
+    return CC_OK;
+}
+
+cc_status cc_profile_read(const cc_ctx* ctx, int32_t kind, double* ms, int64_t* launches, double* bytes) {
+    if (!ctx || kind < 0 || kind >= CC_K_COUNT) return CC_EARG;
+    if (ms) *ms = ctx->prof_ms[kind];
+    if (launches) *launches = ctx->prof_n[kind];
+    if (bytes) *bytes = ctx->prof_bytes[kind];
+    return CC_OK;
+}
+
+// Build the step plan: rows packed in job order (stage.js:1319-1325), the Q
+// operand offsets, the attention work items, head rows.
+static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, bool head) {
+    p.jobs.resize(njobs);
+    p.kv_bytes = 0;
+    p.items.clear();
+    p.row_job.clear();
+    p.head_rows.clear();
+    const int ng = ctx->geom.ng;
+    size_t qp = 0, ap = 0;
+    int row = 0;
+    for (int j = 0; j < njobs; j++) {
+        JobDev& jd = p.jobs[j];
+        jd.slot = jobs[j].slot;
+        jd.past = jobs[j].past;
+        jd.n = jobs[j].n;
+        jd.row0 = row;
+        jd.mtq = ceil_div(jd.n * ctx->group, 16);
+        jd.qp_off = (int32_t)qp;
+        qp += (size_t)ctx->geom.nKV * jd.mtq * ng * 128;
+        const int T_act = jd.past + jd.n;
+        p.kv_bytes += 2.0 * T_act * ctx->geom.nKV * (ctx->D + 4.0 * ctx->geom.ng);
+        jd.nchunk = ceil_div(ceil_div(T_act, 64), 4);
+        jd.item0 = (int32_t)p.items.size();
+        for (int h = 0; h < ctx->geom.nKV; h++)
+            for (int c = 0; c < jd.nchunk; c++) {
+                p.items.push_back(AttnItem{j, h, c, (int32_t)ap});
+                ap += (size_t)jd.mtq * 16 * (ctx->D + 2);
+            }
+        for (int i = 0; i < jd.n; i++) p.row_job.push_back(j);
+        if (head)
+            for (int i = jd.n - jobs[j].sampled; i < jd.n; i++) p.head_rows.push_back(row + i);
+        row += jd.n;
+    }
+    p.T = row;
+    p.S = (int)p.head_rows.size();
+    p.nitems = (int)p.items.size();
+    p.qp_units = qp;
+    p.apart_floats = ap;
+}
+
+static cc_status grow(cc_ctx* ctx, const StepPlan& p) {
+    if (p.qp_units > ctx->qp_units) {
+        uint4* q = nullptr;
+        HIPCHK(dalloc(ctx, &q, p.qp_units * 16, &ctx->scratch_bytes));
+        ctx->qp = q;
+        ctx->qp_units = p.qp_units;
+    }
+    if (p.apart_floats > ctx->apart_floats) {
+        float* a = nullptr;
+        HIPCHK(dalloc(ctx, &a, p.apart_floats * 4, &ctx->scratch_bytes));
+        ctx->apart = a;
+        ctx->apart_floats = p.apart_floats;
+    }
+    return CC_OK;
+}
+
+// The blocks [p0, p1) (model indices) over the packed rows: blockSegs
+// (web/model/model.js:619-624) per layer, with the reference's dispatches
+// fused into: operand prep, q|k|v GEMM, finish (RoPE + KV store + Q operand),
+// attention, combine (o_proj operand), o GEMM, finish (residual + rmsnorm),
+// gate|up GEMM, finish (SwiGLU), down GEMM, finish (residual + round_f16 +
+// the next block's rmsnorm).
+static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int b0, int b1) {
+    const cc_dims& d = ctx->d;
+    hipStream_t st = ctx->stream;
+    const int T = p.T, H = d.hidden, nH = d.n_heads, D = d.head_dim;
+    const int Mpad = 16 * ceil_div(T, 16) + (ceil_div(T, 16) > 1 && (ceil_div(T, 16) & 1) ? 16 : 0);
+    const JobDev* djobs = (const JobDev*)(ctx->d_meta + ml.jobs);
+    const AttnItem* ditems = (const AttnItem*)(ctx->d_meta + ml.items);
+    const int32_t* drow_job = (const int32_t*)(ctx->d_meta + ml.row_job);
+    for (int b = b0; b < b1; b++) {
+        Layer& L = ctx->layers[b - ctx->L0];
+        if (b == b0)
+            launch_rmsnorm_prep(st, ctx->x, nullptr, T, Mpad, H, L.qkv.KU, L.ln1, d.rms_eps, ctx->xp_h, nullptr);
+        const int sq = splits_for(L.qkv, 4);
+        int e = prof_begin(ctx);
+        launch_gemm(st, L.qkv, ctx->xp_h, ctx->part, T, sq, 4);
+        prof_end(ctx, e, CC_K_QKV, qbytes(L.qkv));
+        launch_fin_qkv(st, ctx->part, sq, T, drow_job, djobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
+                       L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 1);
+        e = prof_begin(ctx);
+        launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
+                    ctx->apart);
+        prof_end(ctx, e, CC_K_ATTN, p.kv_bytes);
+        launch_attn_combine(st, djobs, (int)p.jobs.size(), ditems, ctx->apart, ctx->geom, nH, ctx->group, T, Mpad,
+                            L.o.KU, ctx->xp_o, nullptr);
+        const int so = splits_for(L.o, 4);
+        e = prof_begin(ctx);
+        launch_gemm(st, L.o, ctx->xp_o, ctx->part, T, so, 4);
+        prof_end(ctx, e, CC_K_O, qbytes(L.o));
+        launch_fin_residual(st, ctx->x, ctx->part, so, T, H, 0, L.ln2, d.rms_eps, L.gu.KU, ctx->xp_h, Mpad);
+        const int sg = splits_for(L.gu, 4);
+        e = prof_begin(ctx);
+        launch_gemm(st, L.gu, ctx->xp_h, ctx->part, T, sg, 4);
+        prof_end(ctx, e, CC_K_GU, qbytes(L.gu));
+        launch_fin_swiglu(st, ctx->part, sg, T, Mpad, d.ffn, L.down.KU, ctx->xp_f);
+        const int sd = splits_for(L.down, 4);
+        e = prof_begin(ctx);
+        launch_gemm(st, L.down, ctx->xp_f, ctx->part, T, sd, 4);
+        prof_end(ctx, e, CC_K_DOWN, qbytes(L.down));
+        const bool next = b + 1 < b1;
+        launch_fin_residual(st, ctx->x, ctx->part, sd, T, H, 1, next ? ctx->layers[b + 1 - ctx->L0].ln1 : nullptr,
+                            d.rms_eps, next ? ctx->layers[b + 1 - ctx->L0].qkv.KU : 0, next ? ctx->xp_h : nullptr,
+                            Mpad);
+    }
+    (void)D;
+}
+
+cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, int32_t to, int32_t topk,
+                  float* top_vals, uint32_t* top_ids, uint16_t* hidden_out, int32_t* status) {
+    if (!ctx) return CC_EARG;
+    const cc_dims& d = ctx->d;
+    const int positions = d.n_layer + 2;
+    if (status) for (int j = 0; j < njobs; j++) status[j] = CC_OK;
+    auto bad = [&](int j, const std::string& msg) {
+        if (status && j >= 0) status[j] = CC_EARG;
+        return fail(ctx, CC_EARG, msg);
+    };
+    if (!jobs || njobs < 1 || njobs > ctx->o.max_jobs) return bad(-1, "1..max_jobs jobs per pass");
+    if (at < ctx->o.lo || at >= ctx->o.hi || to <= at || to > ctx->o.hi)
+        return bad(-1, "positions " + std::to_string(at) + ".." + std::to_string(to) + " are not held here");
+    const bool gather = at == 0;
+    const bool head = to == positions;
+    if (head && (topk < 1 || topk > TOPK_MAX)) return bad(-1, "topk must be 1..256");
+    if (head && (!top_vals || !top_ids)) return bad(-1, "a pass to the head needs top_vals and top_ids");
+    if (!head && !hidden_out) return bad(-1, "a pass that stops before the head needs hidden_out");
+    int T = 0;
+    std::vector<char> seen(ctx->owned.size(), 0);
+    // #prepare's checks (web/model/stage.js:1225-1259).
+    for (int j = 0; j < njobs; j++) {
+        const cc_job& jb = jobs[j];
+        if (jb.slot < 0 || jb.slot >= (int)ctx->owned.size()) return bad(j, "slot out of range");
+        if (seen[jb.slot]) return bad(j, "one job per session in a pass");
+        seen[jb.slot] = 1;
+        if (jb.n < 1 || jb.n > ctx->o.t_max)
+            return bad(j, "a job of " + std::to_string(jb.n) + " tokens is outside 1-" + std::to_string(ctx->o.t_max));
+        if (jb.past < 0) return bad(j, "past " + std::to_string(jb.past) + " is not a position");
+        if (jb.past + jb.n > ctx->o.n_max)
+            return bad(j, "context " + std::to_string(jb.past + jb.n) + " exceeds " + std::to_string(ctx->o.n_max));
+        if (gather) {
+            if (!jb.ids) return bad(j, "a job at position 0 needs " + std::to_string(jb.n) + " token ids");
+            for (int i = 0; i < jb.n; i++)
+                if (jb.ids[i] < 0 || jb.ids[i] >= d.vocab) return bad(j, "a token id is outside the vocabulary");
+        } else if (!jb.hidden) {
+            return bad(j, "a job past position 0 needs its hidden rows");
+        }
+        if (head && !(jb.sampled == 1 || jb.sampled == jb.n)) return bad(j, "sampled must be 1 or n at the head");
+        T += jb.n;
+    }
+    if (T > ctx->o.t_max) return bad(-1, "the pass has " + std::to_string(T) + " rows, above t_max");
+
+    StepPlan p;
+    build_plan(ctx, jobs, njobs, p, head);
+    if (p.nitems > (int)ctx->items_cap) return bad(-1, "too many attention items");
+    cc_status gs = grow(ctx, p);
+    if (gs != CC_OK) return gs;
+    MetaLayout ml = meta_layout(ctx->o.max_jobs, ctx->items_cap, ctx->o.t_max, d.hidden);
+    uint8_t* hm = ctx->h_meta;
+    std::memcpy(hm + ml.jobs, p.jobs.data(), p.jobs.size() * sizeof(JobDev));
+    std::memcpy(hm + ml.items, p.items.data(), p.items.size() * sizeof(AttnItem));
+    std::memcpy(hm + ml.row_job, p.row_job.data(), p.row_job.size() * 4);
+    std::memcpy(hm + ml.head_rows, p.head_rows.data(), p.head_rows.size() * 4);
+    std::vector<std::pair<int, int>> want;
+    for (int j = 0; j < njobs; j++) want.push_back({jobs[j].slot, jobs[j].past + jobs[j].n});
+    {
+        // Page plan (host counts), written before the copy.
+        int32_t* plan = (int32_t*)(hm + ml.plan);
+        int total = 0;
+        for (int j = 0; j < njobs; j++) {
+            const int need = ceil_div(want[j].second, ctx->geom.page);
+            const int nw = std::max(0, need - ctx->owned[want[j].first]);
+            plan[4 * j] = want[j].first;
+            plan[4 * j + 1] = ctx->owned[want[j].first];
+            plan[4 * j + 2] = nw;
+            plan[4 * j + 3] = total;
+            total += nw;
+        }
+    }
+    size_t copy_bytes = ml.hidden;
+    if (gather) {
+        int32_t* ids = (int32_t*)(hm + ml.ids);
+        int r = 0;
+        for (int j = 0; j < njobs; j++)
+            for (int i = 0; i < jobs[j].n; i++) ids[r++] = jobs[j].ids[i];
+    } else {
+        uint16_t* hid = (uint16_t*)(hm + ml.hidden);
+        size_t r = 0;
+        for (int j = 0; j < njobs; j++) {
+            std::memcpy(hid + r, jobs[j].hidden, (size_t)jobs[j].n * d.hidden * 2);
+            r += (size_t)jobs[j].n * d.hidden;
+        }
+        copy_bytes = ml.hidden + (size_t)T * d.hidden * 2;
+    }
+    hipStream_t st = ctx->stream;
+    HIPCHK(hipEventRecord(ctx->ev0, st));
+    HIPCHK(hipMemcpyAsync(ctx->d_meta, hm, copy_bytes, hipMemcpyHostToDevice, st));
+    cc_status ps = take_pages(ctx, want, (int32_t*)(ctx->d_meta + ml.plan), (int32_t*)(hm + ml.plan), status);
+    if (ps != CC_OK) {
+        hipStreamSynchronize(st);
+        return ps;
+    }
+    // Embedding (position 0) or the rows handed in.
+    QTensor emb = ctx->wte;
+    emb.K = d.hidden;
+    if (gather) launch_embed(st, (const int32_t*)(ctx->d_meta + ml.ids), nullptr, T, emb, ctx->x);
+    else {
+        QTensor shape;
+        shape.K = d.hidden;
+        launch_embed(st, nullptr, (const uint16_t*)(ctx->d_meta + ml.hidden), T, shape, ctx->x);
+    }
+    const int b0 = std::max(at, 1) - 1, b1 = std::min(to, d.n_layer + 1) - 1;
+    if (b1 > b0) run_blocks(ctx, p, ml, b0, b1);
+    void* hout = ctx->h_out;
+    if (head) {
+        const QTensor& hw = d.tied ? ctx->wte : ctx->lm_head;
+        const int S = p.S;
+        const int Mpad = 32 * ceil_div(S, 32);
+        launch_rmsnorm_prep(st, ctx->x, (const int32_t*)(ctx->d_meta + ml.head_rows), S, Mpad, d.hidden, hw.KU,
+                            ctx->norm, d.rms_eps, ctx->xp_h, nullptr);
+        const int e = prof_begin(ctx);
+        launch_gemm(st, hw, ctx->xp_h, ctx->logits, S, 1, 4);
+        prof_end(ctx, e, CC_K_HEAD, qbytes(hw));
+        launch_topk(st, ctx->logits, S, d.vocab, topk, ctx->tk_a, ctx->tk_b, ctx->d_vals, ctx->d_ids);
+        HIPCHK(hipMemcpyAsync(hout, ctx->d_vals, (size_t)S * topk * 4, hipMemcpyDeviceToHost, st));
+        HIPCHK(hipMemcpyAsync((uint8_t*)hout + (size_t)S * topk * 4, ctx->d_ids, (size_t)S * topk * 4,
+                              hipMemcpyDeviceToHost, st));
+    } else {
+        launch_to_half_bits(st, ctx->x, (int64_t)T * d.hidden, ctx->d_hbits);
+        HIPCHK(hipMemcpyAsync(hout, ctx->d_hbits, (size_t)T * d.hidden * 2, hipMemcpyDeviceToHost, st));
+    }
+    HIPCHK(hipEventRecord(ctx->ev1, st));
+    HIPCHK(hipStreamSynchronize(st));
+    float ms = 0;
+    hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1);
+    ctx->last_ms = ms;
+    prof_collect(ctx);
+    ctx->passes++;
+    ctx->rows += T;
+    if (head) {
+        std::memcpy(top_vals, hout, (size_t)p.S * topk * 4);
+        std::memcpy(top_ids, (uint8_t*)hout + (size_t)p.S * topk * 4, (size_t)p.S * topk * 4);
+    } else {
+        std::memcpy(hidden_out, hout, (size_t)T * d.hidden * 2);
+    }
+    return CC_OK;
+}
+
+// ------------------------------------------------------ kernel-level ops ---
+cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K, const int8_t* W,
+                          const uint16_t* scales_f16, int32_t N, float* Y) {
+    if (!ctx || !X || !W || !scales_f16 || !Y || M < 1 || K < 4 || N < 1 || K % 4) return fail(ctx, CC_EARG, "bad matmul");
+    QTensor q{};
+    q.N = N;
+    q.K = K;
+    q.Nt = ceil_div(ceil_div(N, 16), 4) * 4;
+    q.KU = ceil_div(K, 64);
+    const int ng = ceil_div(K, 32);
+    const int Mt = 2 * ceil_div(M, 32);
+    const int sp = splits_for(q, 4);
+    int8_t* dW = nullptr; uint16_t* dS = nullptr; float* dX = nullptr; float* dP = nullptr; float* dY = nullptr;
+    uint4* dXp = nullptr;
+    HIPCHK(hipMalloc(&q.codes, (size_t)q.Nt * q.KU * 1024));
+    HIPCHK(hipMalloc(&q.scales, (size_t)q.Nt * q.KU * 64));
+    HIPCHK(hipMemset(q.scales, 0, (size_t)q.Nt * q.KU * 64));
+    HIPCHK(hipMalloc(&dW, (size_t)N * K));
+    HIPCHK(hipMalloc(&dS, (size_t)N * ng * 2));
+    HIPCHK(hipMalloc(&dX, (size_t)M * K * 4));
+    HIPCHK(hipMalloc(&dXp, (size_t)Mt * 2 * q.KU * 2 * 1024));
+    HIPCHK(hipMalloc(&dP, (size_t)sp * M * N * 4));
+    HIPCHK(hipMalloc(&dY, (size_t)M * N * 4));
+    HIPCHK(hipMemcpy(dW, W, (size_t)N * K, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(dS, scales_f16, (size_t)N * ng * 2, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(dX, X, (size_t)M * K * 4, hipMemcpyHostToDevice));
+    hipStream_t st = ctx->stream;
+    launch_tile_q8(st, dW, dS, N, K, 32, q, 0);
+    launch_prep_rows(st, dX, K, M, Mt * 16, K, q.KU, dXp);
+    launch_gemm(st, q, dXp, dP, M, sp, 4);
+    launch_sum_splits(st, dP, sp, M, N, dY);
+    HIPCHK(hipStreamSynchronize(st));
+    HIPCHK(hipMemcpy(Y, dY, (size_t)M * N * 4, hipMemcpyDeviceToHost));
+    for (void* v : {(void*)q.codes, (void*)q.scales, (void*)dW, (void*)dS, (void*)dX, (void*)dXp, (void*)dP, (void*)dY})
+        hipFree(v);
+    return CC_OK;
+}
+
+cc_status cc_op_round_f16(cc_ctx* ctx, float* a, int64_t n) {
+    if (!ctx || !a || n < 0) return CC_EARG;
+    float* dA = nullptr;
+    HIPCHK(hipMalloc(&dA, (size_t)n * 4 + 16));
+    HIPCHK(hipMemcpy(dA, a, (size_t)n * 4, hipMemcpyHostToDevice));
+    launch_round_f16(ctx->stream, dA, n);
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    HIPCHK(hipMemcpy(a, dA, (size_t)n * 4, hipMemcpyDeviceToHost));
+    hipFree(dA);
+    return CC_OK;
+}
+
+cc_status cc_op_topk(cc_ctx* ctx, const float* logits, int32_t rows, int32_t V, int32_t M, float* vals,
+                     uint32_t* ids) {
+    if (!ctx || !logits || rows < 1 || V < 1 || M < 1 || M > TOPK_MAX || M > V) return fail(ctx, CC_EARG, "bad topk");
+    float* dL = nullptr; uint64_t* a = nullptr; uint64_t* b = nullptr; float* dv = nullptr; uint32_t* di = nullptr;
+    const size_t keys = (size_t)rows * ceil_div(V, 4096) * M + 16;
+    HIPCHK(hipMalloc(&dL, (size_t)rows * V * 4));
+    HIPCHK(hipMalloc(&a, keys * 8));
+    HIPCHK(hipMalloc(&b, keys * 8));
+    HIPCHK(hipMalloc(&dv, (size_t)rows * M * 4));
+    HIPCHK(hipMalloc(&di, (size_t)rows * M * 4));
+    HIPCHK(hipMemcpy(dL, logits, (size_t)rows * V * 4, hipMemcpyHostToDevice));
+    launch_topk(ctx->stream, dL, rows, V, M, a, b, dv, di);
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    HIPCHK(hipMemcpy(vals, dv, (size_t)rows * M * 4, hipMemcpyDeviceToHost));
+    HIPCHK(hipMemcpy(ids, di, (size_t)rows * M * 4, hipMemcpyDeviceToHost));
+    for (void* v : {(void*)dL, (void*)a, (void*)b, (void*)dv, (void*)di}) hipFree(v);
+    return CC_OK;
+}
+
+cc_status cc_op_rmsnorm(cc_ctx* ctx, const float* x, const float* w, int32_t T, int32_t H, float* y) {
+    if (!ctx || !x || !w || !y || T < 1 || H < 1) return CC_EARG;
+    float *dx = nullptr, *dw = nullptr, *dy = nullptr;
+    HIPCHK(hipMalloc(&dx, (size_t)T * H * 4));
+    HIPCHK(hipMalloc(&dw, (size_t)H * 4));
+    HIPCHK(hipMalloc(&dy, (size_t)T * H * 4));
+    HIPCHK(hipMemcpy(dx, x, (size_t)T * H * 4, hipMemcpyHostToDevice));
+    HIPCHK(hipMemcpy(dw, w, (size_t)H * 4, hipMemcpyHostToDevice));
+    launch_rmsnorm_prep(ctx->stream, dx, nullptr, T, T, H, 0, dw, ctx->d.rms_eps, nullptr, dy);
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    HIPCHK(hipMemcpy(y, dy, (size_t)T * H * 4, hipMemcpyDeviceToHost));
+    for (void* v : {(void*)dx, (void*)dw, (void*)dy}) hipFree(v);
+    return CC_OK;
+}
+
+// A one-job plan for the kernel-level attention ops.
+static cc_status one_job(cc_ctx* ctx, int32_t layer, int32_t slot, int32_t n, int32_t past, StepPlan& p,
+                         MetaLayout& ml) {
+    if (layer - ctx->L0 < 0 || layer - ctx->L0 >= (int)ctx->layers.size()) return fail(ctx, CC_EARG, "layer not held");
+    if (slot < 0 || slot >= (int)ctx->owned.size() || n < 1 || n > ctx->o.t_max || past < 0 ||
+        past + n > ctx->o.n_max)
+        return fail(ctx, CC_EARG, "bad job");
+    cc_job j{};
+    j.slot = slot;
+    j.past = past;
+    j.n = n;
+    build_plan(ctx, &j, 1, p, false);
+    cc_status gs = grow(ctx, p);
+    if (gs != CC_OK) return gs;
+    ml = meta_layout(ctx->o.max_jobs, ctx->items_cap, ctx->o.t_max, ctx->d.hidden);
+    uint8_t* hm = ctx->h_meta;
+    std::memcpy(hm + ml.jobs, p.jobs.data(), sizeof(JobDev));
+    std::memcpy(hm + ml.items, p.items.data(), p.items.size() * sizeof(AttnItem));
+    std::memcpy(hm + ml.row_job, p.row_job.data(), p.row_job.size() * 4);
+    int32_t* plan = (int32_t*)(hm + ml.plan);
+    const int need = ceil_div(past + n, ctx->geom.page);
+    plan[0] = slot; plan[1] = ctx->owned[slot]; plan[2] = std::max(0, need - ctx->owned[slot]); plan[3] = 0;
+    HIPCHK(hipMemcpyAsync(ctx->d_meta, hm, ml.ids, hipMemcpyHostToDevice, ctx->stream));
+    std::vector<std::pair<int, int>> want{{slot, past + n}};
+    return take_pages(ctx, want, (int32_t*)(ctx->d_meta + ml.plan), plan, nullptr);
+}
+
+cc_status cc_op_store_kv(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot, const float* src, int32_t T_new,
+                         int32_t T_past) {
+    if (!ctx || !src || which < 0 || which > 1) return CC_EARG;
+    StepPlan p;
+    MetaLayout ml;
+    cc_status s = one_job(ctx, layer, slot, T_new, T_past, p, ml);
+    if (s != CC_OK) return s;
+    const cc_dims& d = ctx->d;
+    const int kv = d.n_kv_heads * d.head_dim;
+    // Rows laid out as q|k|v with only the chosen part meaningful; store both
+    // halves only when asked, by writing the other half from the cache's own
+    // view is not possible, so K and V are stored one at a time through a
+    // row whose other half is the same source (the kernel writes what it is
+    // told to: do_kv stores K and V, so the unused half is re-stored below).
+    const int N = (d.n_heads + 2 * d.n_kv_heads) * d.head_dim;
+    std::vector<float> rows((size_t)T_new * N, 0.0f);
+    for (int t = 0; t < T_new; t++)
+        for (int e = 0; e < kv; e++) rows[(size_t)t * N + d.n_heads * d.head_dim + which * kv + e] = src[(size_t)t * kv + e];
+    // Save the other half's rows so they can be restored.
+    const int other = 1 - which;
+    std::vector<std::vector<uint32_t>> saved(d.n_kv_heads);
+    const int RW = d.head_dim / 4 + d.head_dim / 32;
+    for (int h = 0; h < d.n_kv_heads; h++) {
+        saved[h].resize((size_t)T_new * RW);
+        cc_status r = kv_io(ctx, layer, other, slot, h, T_past, T_past + T_new, saved[h].data(), nullptr);
+        if (r != CC_OK) return r;
+    }
+    float* dr = nullptr;
+    HIPCHK(hipMalloc(&dr, rows.size() * 4));
+    HIPCHK(hipMemcpy(dr, rows.data(), rows.size() * 4, hipMemcpyHostToDevice));
+    Layer& L = ctx->layers[layer - ctx->L0];
+    launch_fin_qkv(ctx->stream, dr, 1, T_new, (const int32_t*)(ctx->d_meta + ml.row_job),
+                   (const JobDev*)(ctx->d_meta + ml.jobs), d.n_heads, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
+                   L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 0, 1);
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    hipFree(dr);
+    for (int h = 0; h < d.n_kv_heads; h++) {
+        cc_status r = kv_io(ctx, layer, other, slot, h, T_past, T_past + T_new, nullptr, saved[h].data());
+        if (r != CC_OK) return r;
+    }
+    return CC_OK;
+}
+
+cc_status cc_op_attend(cc_ctx* ctx, int32_t layer, int32_t slot, const float* q, int32_t n, int32_t past,
+                       float* out) {
+    if (!ctx || !q || !out) return CC_EARG;
+    const cc_dims& d = ctx->d;
+    if (ceil_div(past + n, ctx->geom.page) > ctx->owned[slot]) return fail(ctx, CC_EARG, "K/V rows are not stored");
+    StepPlan p;
+    MetaLayout ml;
+    cc_status s = one_job(ctx, layer, slot, n, past, p, ml);
+    if (s != CC_OK) return s;
+    const int qd = d.n_heads * d.head_dim;
+    const int N = (d.n_heads + 2 * d.n_kv_heads) * d.head_dim;
+    std::vector<float> rows((size_t)n * N, 0.0f);
+    for (int t = 0; t < n; t++)
+        for (int e = 0; e < qd; e++) rows[(size_t)t * N + e] = q[(size_t)t * qd + e];
+    float *dr = nullptr, *dctx = nullptr;
+    uint4* dXp = nullptr;
+    const int Mt = 2 * ceil_div(n, 32);
+    const int KU = ceil_div(qd, 64);
+    HIPCHK(hipMalloc(&dr, rows.size() * 4));
+    HIPCHK(hipMalloc(&dctx, (size_t)n * qd * 4));
+    HIPCHK(hipMalloc(&dXp, (size_t)Mt * 2 * KU * 2 * 1024));
+    HIPCHK(hipMemcpy(dr, rows.data(), rows.size() * 4, hipMemcpyHostToDevice));
+    Layer& L = ctx->layers[layer - ctx->L0];
+    hipStream_t st = ctx->stream;
+    const JobDev* dj = (const JobDev*)(ctx->d_meta + ml.jobs);
+    const AttnItem* di = (const AttnItem*)(ctx->d_meta + ml.items);
+    launch_fin_qkv(st, dr, 1, n, (const int32_t*)(ctx->d_meta + ml.row_job), dj, d.n_heads, ctx->group, ctx->geom,
+                   ctx->tbl, ctx->rot, L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 0);
+    launch_attn(st, di, p.nitems, dj, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->apart);
+    launch_attn_combine(st, dj, 1, di, ctx->apart, ctx->geom, d.n_heads, ctx->group, n, Mt * 16, KU, dXp, dctx);
+    HIPCHK(hipStreamSynchronize(st));
+    HIPCHK(hipMemcpy(out, dctx, (size_t)n * qd * 4, hipMemcpyDeviceToHost));
+    for (void* v : {(void*)dr, (void*)dctx, (void*)dXp}) hipFree(v);
+    return CC_OK;
+}
+
+}  // extern "C"

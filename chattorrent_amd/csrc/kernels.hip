@@ -1,0 +1,1089 @@
+// Device kernels of the MI355X (gfx950) batched ragged decode pass.
+//
+// Reference counterparts (l-wn/ChatTorrent, web/model/kernels.js) are cited
+// per kernel. The design is MI355X-first: q8 projections run on MFMA
+// (v_mfma_f32_16x16x32_f16) with the int8 codes dequantised exactly to f16 in
+// registers and the f32 activations split into an f16 hi/lo pair, so each
+// 32-wide quantisation group is one MFMA pair followed by one scale FMA per
+// output; attention streams each chat's int8 pages once per kv head for the
+// whole GQA group, also on MFMA; element-wise work is fused into the
+// reduction ("finish") kernels that feed the next projection its operand.
+#include "common.h"
+#include "kernels.h"
+
+#define CHECK_LAUNCH() (void)hipGetLastError()
+
+// ===================================================================== GEMM ===
+// Y[M, N] = X[M, K] . W[N, K]^T for a tiled q8 W (kernels.h QTensor) and an
+// activation operand Xp prepared by the prep/finish kernels:
+//   Xp[((mt*G2 + g)*2 + hl)*64 + lane] = 8 f16 of X[16mt + lane%16][32g + 8(lane/16) ..]
+// (hl = 0: hi part, 1: lo part; G2 = 2*KU groups, zero beyond K).
+// Grid: x = strips of NT n-tiles (16 columns each), y = K splits of `ups`
+// units (64 columns of K), z = blocks of MT m-tiles. Four waves share a strip
+// and split its units round-robin; their partial sums are added in LDS in a
+// fixed order, so a result never depends on timing, on M, or on the other
+// rows (each row's MFMA output depends only on that row's operand).
+// Output: out[(split*M + m)*N + n]; the finish kernels add the splits in order.
+// Reference: matmul_gemv_q8 / matmul_gemv_rows_q8 / matmul_rows_q8
+// (web/model/kernels.js:449-751): per group, acc += scale * dot(x, q).
+template <int MT, int NT>
+__global__ __launch_bounds__(256) void k_gemm_q8(const uint4* __restrict__ Wc,
+                                                 const uint32_t* __restrict__ Ws,
+                                                 const uint4* __restrict__ Xp,
+                                                 float* __restrict__ out,
+                                                 int KU, int M, int N, int ups) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nt0 = blockIdx.x * NT;
+    const int split = blockIdx.y;
+    const int mt0 = blockIdx.z * MT;
+    const int G2 = 2 * KU;
+    const int u0 = split * ups;
+    const int u1 = min(KU, u0 + ups);
+
+    float4_t acc[MT][NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    const uint4* wbase = Wc + (size_t)nt0 * KU * 64 + lane;
+    const uint32_t* sbase = Ws + (size_t)nt0 * KU * 16 + (lane & 15);
+
+    int u = u0 + wave;
+    uint4 w[NT];
+    uint32_t s[NT];
+    if (u < u1) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            w[nt] = wbase[((size_t)nt * KU + u) * 64];
+            s[nt] = sbase[((size_t)nt * KU + u) * 16];
+        }
+    }
+    for (; u < u1; u += 4) {
+        uint4 wc[NT];
+        uint32_t sc[NT];
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) { wc[nt] = w[nt]; sc[nt] = s[nt]; }
+        if (u + 4 < u1) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                w[nt] = wbase[((size_t)nt * KU + u + 4) * 64];
+                s[nt] = sbase[((size_t)nt * KU + u + 4) * 16];
+            }
+        }
+        uint4 xh[MT][2], xl[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const size_t at = (((size_t)(mt0 + mt) * G2 + 2 * u + h) * 2) * 64 + lane;
+                xh[mt][h] = Xp[at];
+                xl[mt][h] = Xp[at + 64];
+            }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const half8_t b = h ? dequant8_biased(wc[nt].z, wc[nt].w)
+                                    : dequant8_biased(wc[nt].x, wc[nt].y);
+                const uint16_t sb = h ? (uint16_t)(sc[nt] >> 16) : (uint16_t)(sc[nt] & 0xffffu);
+                const float scale = (float)__builtin_bit_cast(_Float16, sb);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    float4_t p = {0.f, 0.f, 0.f, 0.f};
+                    p = mfma16x16x32(__builtin_bit_cast(half8_t, xh[mt][h]), b, p);
+                    p = mfma16x16x32(__builtin_bit_cast(half8_t, xl[mt][h]), b, p);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[mt][nt][r] = __builtin_fmaf(scale, p[r], acc[mt][nt][r]);
+                }
+            }
+        }
+    }
+
+    __shared__ float4_t red[4 * MT * NT * 64];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) red[(wave * MT * NT + mt * NT + nt) * 64 + lane] = acc[mt][nt];
+    __syncthreads();
+    for (int e = threadIdx.x; e < MT * NT * 64; e += 256) {
+        float4_t v = red[e];
+#pragma unroll
+        for (int wv = 1; wv < 4; wv++) {
+            const float4_t o = red[wv * MT * NT * 64 + e];
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = v[r] + o[r];
+        }
+        const int l = e & 63, tile = e >> 6, mt = tile / NT, nt = tile % NT;
+        const int n = (nt0 + nt) * 16 + (l & 15);
+        if (n >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = (mt0 + mt) * 16 + 4 * (l >> 4) + r;
+            if (m < M) out[((size_t)split * M + m) * N + n] = v[r];
+        }
+    }
+}
+
+void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, int splits,
+                 int nt) {
+    const int ups = (w.KU + splits - 1) / splits;
+    const int mblocks16 = (M + 15) / 16;
+    if (mblocks16 <= 1) {
+        dim3 grid(w.Nt / nt, splits, 1);
+        if (nt == 4) hipLaunchKernelGGL((k_gemm_q8<1, 4>), grid, dim3(256), 0, st, (const uint4*)w.codes,
+                                        (const uint32_t*)w.scales, Xp, out, w.KU, M, w.N, ups);
+        else hipLaunchKernelGGL((k_gemm_q8<1, 2>), grid, dim3(256), 0, st, (const uint4*)w.codes,
+                                (const uint32_t*)w.scales, Xp, out, w.KU, M, w.N, ups);
+    } else {
+        dim3 grid(w.Nt / nt, splits, (mblocks16 + 1) / 2);
+        if (nt == 4) hipLaunchKernelGGL((k_gemm_q8<2, 4>), grid, dim3(256), 0, st, (const uint4*)w.codes,
+                                        (const uint32_t*)w.scales, Xp, out, w.KU, M, w.N, ups);
+        else hipLaunchKernelGGL((k_gemm_q8<2, 2>), grid, dim3(256), 0, st, (const uint4*)w.codes,
+                                (const uint32_t*)w.scales, Xp, out, w.KU, M, w.N, ups);
+    }
+    CHECK_LAUNCH();
+}
+
+// =========================================================== operand prep ===
+// Writes 8 consecutive values of row m (columns 8c .. 8c+7) as the f16 hi/lo
+// operand fragments of the GEMM (layout above).
+__device__ static inline void write_hilo(uint4* Xp, int m, int c, int KU, const float* v) {
+    const int g = c >> 2, kb = c & 3;
+    const int mt = m >> 4, lane = (m & 15) + 16 * kb;
+    half8_t hi, lo;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        _Float16 a, b;
+        split_hilo(v[j], a, b);
+        hi[j] = a;
+        lo[j] = b;
+    }
+    const size_t at = (((size_t)mt * 2 * KU + g) * 2) * 64 + lane;
+    Xp[at] = __builtin_bit_cast(uint4, hi);
+    Xp[at + 64] = __builtin_bit_cast(uint4, lo);
+}
+
+__global__ void k_prep_rows(const float* __restrict__ x, int ldx, int M, int Mpad, int K, int KU,
+                            uint4* __restrict__ Xp) {
+    const int per = 8 * KU;
+    const int total = Mpad * per;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        const int m = i / per, c = i % per;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int k = 8 * c + j;
+            v[j] = (m < M && k < K) ? x[(size_t)m * ldx + k] : 0.0f;
+        }
+        write_hilo(Xp, m, c, KU, v);
+    }
+}
+
+void launch_prep_rows(hipStream_t st, const float* x, int ldx, int M, int Mpad, int K, int KU,
+                      uint4* Xp) {
+    const int total = Mpad * 8 * KU;
+    hipLaunchKernelGGL(k_prep_rows, dim3((total + 255) / 256), dim3(256), 0, st, x, ldx, M, Mpad, K, KU, Xp);
+    CHECK_LAUNCH();
+}
+
+// rmsnorm (web/model/kernels.js:930-976) fused with the operand prep: one
+// workgroup of 256 per row; sum of squares over h = tid, tid+256, ... then a
+// pairwise tree; y = x * (1/sqrt(ss/H + eps)) * w. Rows m >= M write zeros.
+// `rows` (optional) gathers source rows (the head's sampled rows).
+__device__ static inline float block_sum_256(float v, float* red) {
+    red[threadIdx.x] = v;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + s];
+        __syncthreads();
+    }
+    const float r = red[0];
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(256) void k_rmsnorm_prep(const float* __restrict__ x,
+                                                      const int32_t* __restrict__ rows, int M, int H,
+                                                      int KU, const float* __restrict__ w, float eps,
+                                                      uint4* __restrict__ Xp, float* __restrict__ y) {
+    __shared__ float red[256];
+    const int m = blockIdx.x;
+    const int per = 8 * KU;
+    if (m >= M) {
+        const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (Xp) for (int c = threadIdx.x; c < per; c += 256) write_hilo(Xp, m, c, KU, z);
+        return;
+    }
+    const float* xr = x + (size_t)(rows ? rows[m] : m) * H;
+    float ss = 0.0f;
+    for (int h = threadIdx.x; h < H; h += 256) {
+        const float v = xr[h];
+        ss = ss + v * v;
+    }
+    const float tot = block_sum_256(ss, red);
+    const float scale = 1.0f / sqrtf(tot / (float)H + eps);
+    for (int c = threadIdx.x; c < per; c += 256) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int k = 8 * c + j;
+            v[j] = k < H ? xr[k] * scale * w[k] : 0.0f;
+            if (y && k < H) y[(size_t)m * H + k] = v[j];
+        }
+        if (Xp) write_hilo(Xp, m, c, KU, v);
+    }
+}
+
+void launch_rmsnorm_prep(hipStream_t st, const float* x, const int32_t* rows, int M, int Mpad, int H,
+                         int KU, const float* w, float eps, uint4* Xp, float* y) {
+    hipLaunchKernelGGL(k_rmsnorm_prep, dim3(Xp ? Mpad : M), dim3(256), 0, st, x, rows, M, H, KU, w, eps,
+                       Xp, y);
+    CHECK_LAUNCH();
+}
+
+// ========================================================= finish kernels ===
+// Residual add (web/model/kernels.js:1334-1346 add_inplace) of the projection
+// (the K splits summed in order), optionally round_f16 (:1356-1383, the
+// per-block residual round, model.js:619-624), then optionally the next
+// rmsnorm (:930-976) and its operand prep. One workgroup per row; the row is
+// kept in LDS between the steps.
+__global__ __launch_bounds__(256) void k_fin_residual(float* __restrict__ x, const float* __restrict__ part,
+                                                      int splits, int M, int H, int round,
+                                                      const float* __restrict__ w, float eps, int KU,
+                                                      uint4* __restrict__ Xp) {
+    extern __shared__ float rowbuf[];
+    __shared__ float red[256];
+    const int m = blockIdx.x;
+    const int per = 8 * KU;
+    if (m >= M) {
+        const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (Xp) for (int c = threadIdx.x; c < per; c += 256) write_hilo(Xp, m, c, KU, z);
+        return;
+    }
+    float ss = 0.0f;
+    for (int h = threadIdx.x; h < H; h += 256) {
+        float p = part[(size_t)m * H + h];
+        for (int s = 1; s < splits; s++) p = p + part[((size_t)s * M + m) * H + h];
+        float v = x[(size_t)m * H + h] + p;
+        if (round) v = round_f16_value(v);
+        x[(size_t)m * H + h] = v;
+        rowbuf[h] = v;
+        ss = ss + v * v;
+    }
+    if (!Xp) return;
+    const float tot = block_sum_256(ss, red);   // includes the barrier that publishes rowbuf
+    const float scale = 1.0f / sqrtf(tot / (float)H + eps);
+    for (int c = threadIdx.x; c < per; c += 256) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int k = 8 * c + j;
+            v[j] = k < H ? rowbuf[k] * scale * w[k] : 0.0f;
+        }
+        write_hilo(Xp, m, c, KU, v);
+    }
+}
+
+void launch_fin_residual(hipStream_t st, float* x, const float* part, int splits, int M, int H, int round,
+                         const float* w, float eps, int KU, uint4* Xp, int Mpad) {
+    hipLaunchKernelGGL(k_fin_residual, dim3(Xp ? Mpad : M), dim3(256), H * sizeof(float), st, x, part,
+                       splits, M, H, round, w, eps, KU, Xp);
+    CHECK_LAUNCH();
+}
+
+// SwiGLU (web/model/kernels.js:1513-1529 silu_mul): act = g * (1/(1+exp(-g)))
+// * up over the fused gate|up projection, straight into the down operand.
+__global__ void k_fin_swiglu(const float* __restrict__ part, int splits, int M, int Mpad, int F, int KU,
+                             uint4* __restrict__ Xp) {
+    const int per = 8 * KU;
+    const int total = Mpad * per;
+    const size_t N2 = 2 * (size_t)F;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        const int m = i / per, c = i % per;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int k = 8 * c + j;
+            float a = 0.0f;
+            if (m < M && k < F) {
+                float g = part[(size_t)m * N2 + k], u = part[(size_t)m * N2 + F + k];
+                for (int s = 1; s < splits; s++) {
+                    g = g + part[((size_t)s * M + m) * N2 + k];
+                    u = u + part[((size_t)s * M + m) * N2 + F + k];
+                }
+                const float sc = 1.0f / (1.0f + expf(-g));
+                a = g * sc * u;
+            }
+            v[j] = a;
+        }
+        write_hilo(Xp, m, c, KU, v);
+    }
+}
+
+void launch_fin_swiglu(hipStream_t st, const float* part, int splits, int M, int Mpad, int F, int KU,
+                       uint4* Xp) {
+    const int total = Mpad * 8 * KU;
+    hipLaunchKernelGGL(k_fin_swiglu, dim3((total + 255) / 256), dim3(256), 0, st, part, splits, M, Mpad, F,
+                       KU, Xp);
+    CHECK_LAUNCH();
+}
+
+// ============================================================ KV geometry ===
+// One (page, kv head) block of the pool, blk = 64*D + 64*ng*4 bytes:
+//   K: codes [64 tokens][D] with column d at (D/4)*((d%32)/8) + 8*(d/32) + d%8,
+//      so one lane's fragment bytes for every group are contiguous; then f32
+//      scales [64 tokens][ng].
+//   V: codes [D][64] with token s at vpos(s) = 16*((s%16)/4) + 4*(s/16) + s%4,
+//      so a lane's P·V fragments are contiguous; then f32 scales [ng][64] at
+//      the same positions.
+// Codes are the true int8 values (bit-exact with the reference's store_kv).
+__host__ __device__ static inline int kpos(int d, int D) { return (D / 4) * ((d & 31) >> 3) + 8 * (d >> 5) + (d & 7); }
+__host__ __device__ static inline int vpos(int s) { return 16 * ((s & 15) >> 2) + 4 * (s >> 4) + (s & 3); }
+
+// store_kv (web/model/kernels.js:1024-1073) for a row's K and V, plus RoPE on
+// its Q (kernels.js:1093-1129) into the attention operand, after the q|k|v
+// splits are summed. One workgroup per row; the row sits in LDS.
+// Bit-exact with the reference given the same q|k|v row: RoPE a*cs - o*sn
+// (no fused multiply-add: the build passes -ffp-contract=off), amax,
+// scale = amax/127, inv = scale > 0 ? 1/scale : 0, rint, clamp ±127.
+__device__ static inline float rope_at(const float* src, int c, int rot, const float* tbl, int pos) {
+    if (c >= rot) return src[c];
+    const int half = rot >> 1;
+    const int i = c < half ? c : c - half;
+    const size_t k = ((size_t)pos * half + i) * 2;
+    const float cs = tbl[k], sn = tbl[k + 1];
+    if (c < half) {
+        const float a = src[c], o = src[c + half];
+        return a * cs - o * sn;
+    }
+    const float a = src[c - half], o = src[c];
+    return o * cs + a * sn;
+}
+
+__global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part, int splits, int M,
+                                                 const int32_t* __restrict__ row_job,
+                                                 const JobDev* __restrict__ jobs, int nH, int group,
+                                                 KVGeom g, const float* __restrict__ tbl, int rot,
+                                                 uint8_t* __restrict__ kpool, uint8_t* __restrict__ vpool,
+                                                 const uint32_t* __restrict__ page_table,
+                                                 uint4* __restrict__ Qp, float* __restrict__ qkv_out,
+                                                 int do_q, int do_kv) {
+    extern __shared__ float row[];
+    const int m = blockIdx.x;
+    const int D = g.D, nKV = g.nKV;
+    const int N = (nH + 2 * nKV) * D;
+    for (int e = threadIdx.x; e < N; e += 256) {
+        float p = part[(size_t)m * N + e];
+        for (int s = 1; s < splits; s++) p = p + part[((size_t)s * M + m) * N + e];
+        row[e] = p;
+        if (qkv_out) qkv_out[(size_t)m * N + e] = p;
+    }
+    __syncthreads();
+    const JobDev jb = jobs[row_job[m]];
+    const int i = m - jb.row0;
+    const int pos = jb.past + i;
+
+    // Q: RoPE, then hi/lo fragments [kvh][mtq][g][hl][64] of rows rho = i*group + gi.
+    const int chunks = do_q ? nH * D / 8 : 0;
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        const int hq = (8 * c) / D, d0 = (8 * c) % D;
+        const float* src = row + hq * D;
+        half8_t hi, lo;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            _Float16 a, b;
+            split_hilo(rope_at(src, d0 + j, rot, tbl, pos), a, b);
+            hi[j] = a;
+            lo[j] = b;
+        }
+        const int kvh = hq / group, gi = hq % group;
+        const int rho = i * group + gi;
+        const int mtq = rho >> 4, lane = (rho & 15) + 16 * ((d0 & 31) >> 3), grp = d0 >> 5;
+        const size_t at = (size_t)jb.qp_off + ((((size_t)kvh * jb.mtq + mtq) * g.ng + grp) * 2) * 64 + lane;
+        Qp[at] = __builtin_bit_cast(uint4, hi);
+        Qp[at + 64] = __builtin_bit_cast(uint4, lo);
+    }
+
+    // K and V: one wave per (head, which); lane l holds d = l + 64q.
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t page = page_table[(size_t)jb.slot * g.max_pages + pos / g.page];
+    const int s = pos % g.page;
+    for (int task = wave; do_kv && task < 2 * nKV; task += 4) {
+        const int n = task >> 1, which = task & 1;
+        const float* src = row + (nH + which * nKV + n) * D;
+        uint8_t* blk = (which ? vpool : kpool) + ((size_t)page * nKV + n) * g.blk;
+        for (int q0 = 0; q0 < D; q0 += 64) {
+            const int d = q0 + lane;
+            const float v = d < D ? (which ? src[d] : rope_at(src, d, rot, tbl, pos)) : 0.0f;
+            float amax = fabsf(v);
+            for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+            const float scale = amax / 127.0f;
+            const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+            float q = __builtin_rintf(v * inv);
+            q = fminf(fmaxf(q, -127.0f), 127.0f);
+            if (d < D) {
+                const int8_t code = (int8_t)(int)q;
+                const int b = d >> 5;
+                if (which == 0) {
+                    blk[(size_t)s * D + kpos(d, D)] = (uint8_t)code;
+                    if ((d & 31) == 0) *(float*)(blk + 64 * D + ((size_t)s * g.ng + b) * 4) = scale;
+                } else {
+                    blk[(size_t)d * 64 + vpos(s)] = (uint8_t)code;
+                    if ((d & 31) == 0) *(float*)(blk + 64 * D + ((size_t)b * 64 + vpos(s)) * 4) = scale;
+                }
+            }
+        }
+    }
+}
+
+void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const int32_t* row_job,
+                    const JobDev* jobs, int nH, int group, const KVGeom& g, const float* tbl, int rot,
+                    uint8_t* kpool, uint8_t* vpool, const uint32_t* page_table, uint4* Qp, float* qkv_out,
+                    int do_q, int do_kv) {
+    const int N = (nH + 2 * g.nKV) * g.D;
+    hipLaunchKernelGGL(k_fin_qkv, dim3(M), dim3(256), N * sizeof(float), st, part, splits, M, row_job, jobs,
+                       nH, group, g, tbl, rot, kpool, vpool, page_table, Qp, qkv_out, do_q, do_kv);
+    CHECK_LAUNCH();
+}
+
+// ================================================================ attention ===
+// Ragged GQA attention over each chat's own int8 pages
+// (web/model/kernels.js:1140-1310 qk_scores_gqa, causal_softmax, attn_av_gqa,
+// driven per segment by web/model/model.js:321-351). One work item = (job,
+// kv head, chunk of 4 pages); each wave takes one 64-token page and all the
+// job's query rows rho = i*group + gi of that kv head, so every K/V byte is
+// read once per GQA group:
+//   S^T[token][rho] = sum_g sk[token][g] * (K_g . Qhi_g + K_g . Qlo_g) on MFMA,
+//   masked to token < T_act and token <= past + i (causal inside a verify or
+//   prefill run), scaled by 1/sqrt(D);
+//   a page-local softmax (max, exp, sum), then
+//   O^T[d][rho] += V^T[d][token] . (p * sv[token][d/32]) (hi/lo) on MFMA.
+// The four waves' (max, sum, O) merge in LDS; the chunk's partial goes to
+// `part` and k_attn_combine merges chunks (log-sum-exp). The reference's
+// softmax is exact three-pass; this one is online, equal within tolerance.
+template <int NG>
+__global__ __launch_bounds__(256) void k_attn(const AttnItem* __restrict__ items,
+                                              const JobDev* __restrict__ jobs, const uint4* __restrict__ Qp,
+                                              const uint8_t* __restrict__ kpool,
+                                              const uint8_t* __restrict__ vpool,
+                                              const uint32_t* __restrict__ page_table, KVGeom g, int group,
+                                              float* __restrict__ part) {
+    constexpr int D = 32 * NG;
+    constexpr int DT = D / 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j4 = lane >> 4, l16 = lane & 15;
+    const AttnItem it = items[blockIdx.x];
+    const JobDev jb = jobs[it.job];
+    const int T_act = jb.past + jb.n;
+    const int R = jb.n * group;
+    const int pg = it.chunk * 4 + wave;
+    const int npg = (T_act + 63) >> 6;
+    const bool live = pg < npg;
+    const float inv_sqrt_d = 1.0f / sqrtf((float)D);
+
+    __shared__ float sm[4][16], sl[4][16];
+    __shared__ float so[4][16][D + 1];
+
+    const uint8_t* kb = nullptr;
+    const uint8_t* vb = nullptr;
+    if (live) {
+        const uint32_t phys = page_table[(size_t)jb.slot * g.max_pages + pg];
+        kb = kpool + ((size_t)phys * g.nKV + it.kvh) * g.blk;
+        vb = vpool + ((size_t)phys * g.nKV + it.kvh) * g.blk;
+    }
+    // K fragments: token tile tt, lane's 8*NG bytes (NG/2 uint4).
+    uint4 kc[4][NG / 2];
+    uint4 vc[DT];
+    if (live) {
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int q = 0; q < NG / 2; q++)
+                kc[tt][q] = *(const uint4*)(kb + (size_t)(tt * 16 + l16) * D + (D / 4) * j4 + 16 * q);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) vc[dt] = *(const uint4*)(vb + (size_t)(dt * 16 + l16) * 64 + 16 * j4);
+    }
+
+    for (int mtq = 0; mtq < jb.mtq; mtq++) {
+        float pr[4][4];
+        float mrow = -INFINITY, lsum = 0.0f;
+        float4_t o[DT];
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+        if (live) {
+            uint4 qh[NG], ql[NG];
+            const size_t qb = (size_t)jb.qp_off + (((size_t)it.kvh * jb.mtq + mtq) * NG) * 2 * 64 + lane;
+#pragma unroll
+            for (int gg = 0; gg < NG; gg++) {
+                qh[gg] = Qp[qb + (size_t)gg * 128];
+                ql[gg] = Qp[qb + (size_t)gg * 128 + 64];
+            }
+            const int rho = mtq * 16 + l16;
+            const int lim = rho < R ? jb.past + rho / group : -1;   // last visible token
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++) {
+                // K scales of tokens tt*16 + 4*j4 + r, all groups: 4*NG floats.
+                float ks[4 * NG];
+#pragma unroll
+                for (int q = 0; q < NG; q++) {
+                    const float4 f = *(const float4*)(kb + 64 * D + ((size_t)(tt * 16 + 4 * j4) * NG) * 4 + 16 * q);
+                    ks[4 * q] = f.x; ks[4 * q + 1] = f.y; ks[4 * q + 2] = f.z; ks[4 * q + 3] = f.w;
+                }
+                float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int gg = 0; gg < NG; gg++) {
+                    const uint4 c = kc[tt][gg >> 1];
+                    const half8_t kf = (gg & 1) ? dequant8_signed(c.z, c.w) : dequant8_signed(c.x, c.y);
+                    float4_t p = {0.f, 0.f, 0.f, 0.f};
+                    p = mfma16x16x32(kf, __builtin_bit_cast(half8_t, qh[gg]), p);
+                    p = mfma16x16x32(kf, __builtin_bit_cast(half8_t, ql[gg]), p);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(ks[r * NG + gg], p[r], acc[r]);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int tok = pg * 64 + tt * 16 + 4 * j4 + r;
+                    const bool ok = tok < T_act && tok <= lim;
+                    pr[tt][r] = ok ? acc[r] * inv_sqrt_d : -INFINITY;
+                    mrow = fmaxf(mrow, pr[tt][r]);
+                }
+            }
+            mrow = fmaxf(mrow, __shfl_xor(mrow, 16));
+            mrow = fmaxf(mrow, __shfl_xor(mrow, 32));
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float e = (mrow == -INFINITY || pr[tt][r] == -INFINITY) ? 0.0f : expf(pr[tt][r] - mrow);
+                    pr[tt][r] = e;
+                    lsum += e;
+                }
+            lsum += __shfl_xor(lsum, 16);
+            lsum += __shfl_xor(lsum, 32);
+            // P . V, one 32-token k-step at a time.
+#pragma unroll
+            for (int b = 0; b < NG; b++) {
+                float sv[16];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 f = *(const float4*)(vb + 64 * D + ((size_t)b * 64 + 16 * j4) * 4 + 16 * q);
+                    sv[4 * q] = f.x; sv[4 * q + 1] = f.y; sv[4 * q + 2] = f.z; sv[4 * q + 3] = f.w;
+                }
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) {
+                    half8_t ph, pl;
+#pragma unroll
+                    for (int ii = 0; ii < 8; ii++) {
+                        const int tt = 2 * ks + (ii >> 2), r = ii & 3;
+                        const float pv = pr[tt][r] == 0.0f ? 0.0f : pr[tt][r] * sv[4 * tt + r];
+                        _Float16 a, c;
+                        split_hilo(pv, a, c);
+                        ph[ii] = a;
+                        pl[ii] = c;
+                    }
+#pragma unroll
+                    for (int dd = 0; dd < 2; dd++) {
+                        const int dt = 2 * b + dd;
+                        const uint4 c = vc[dt];
+                        const half8_t vf = ks ? dequant8_signed(c.z, c.w) : dequant8_signed(c.x, c.y);
+                        o[dt] = mfma16x16x32(vf, ph, o[dt]);
+                        o[dt] = mfma16x16x32(vf, pl, o[dt]);
+                    }
+                }
+            }
+        }
+        if (j4 == 0) {
+            sm[wave][l16] = mrow;
+            sl[wave][l16] = lsum;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) so[wave][l16][dt * 16 + 4 * j4 + r] = o[dt][r];
+        __syncthreads();
+        for (int e = threadIdx.x; e < 16 * D; e += 256) {
+            const int rho = e / D, d = e % D;
+            float M = -INFINITY;
+#pragma unroll
+            for (int wv = 0; wv < 4; wv++) M = fmaxf(M, sm[wv][rho]);
+            float L = 0.0f, O = 0.0f;
+            if (M != -INFINITY) {
+#pragma unroll
+                for (int wv = 0; wv < 4; wv++) {
+                    const float mw = sm[wv][rho];
+                    if (mw == -INFINITY) continue;
+                    const float f = expf(mw - M);
+                    L += sl[wv][rho] * f;
+                    O += so[wv][rho][d] * f;
+                }
+            }
+            float* dst = part + it.part + (size_t)(mtq * 16 + rho) * (D + 2);
+            dst[2 + d] = O;
+            if (d == 0) {
+                dst[0] = M;
+                dst[1] = L;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
+                 const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g,
+                 int group, float* part) {
+    if (nitems <= 0) return;
+    if (g.ng == 4)
+        hipLaunchKernelGGL((k_attn<4>), dim3(nitems), dim3(256), 0, st, items, jobs, Qp, kpool, vpool,
+                           page_table, g, group, part);
+    else
+        hipLaunchKernelGGL((k_attn<2>), dim3(nitems), dim3(256), 0, st, items, jobs, Qp, kpool, vpool,
+                           page_table, g, group, part);
+    CHECK_LAUNCH();
+}
+
+// Merge a job's chunk partials (log-sum-exp), normalise, and write the
+// merged-heads row (web/model/kernels.js:1315-1329 merge_heads is this
+// indexing) as the o_proj operand. One workgroup per (job, kv head).
+__global__ __launch_bounds__(256) void k_attn_combine(const JobDev* __restrict__ jobs,
+                                                      const AttnItem* __restrict__ items,
+                                                      const float* __restrict__ part, KVGeom g, int nH,
+                                                      int group, int KU, uint4* __restrict__ Xp,
+                                                      float* __restrict__ ctx_out) {
+    const int job = blockIdx.x / g.nKV, kvh = blockIdx.x % g.nKV;
+    const JobDev jb = jobs[job];
+    const int D = g.D;
+    const int R = jb.n * group;
+    const int per = R * (D / 8);
+    for (int e = threadIdx.x; e < per; e += 256) {
+        const int rho = e / (D / 8), d0 = (e % (D / 8)) * 8;
+        float M = -INFINITY;
+        for (int c = 0; c < jb.nchunk; c++) {
+            const AttnItem it = items[jb.item0 + kvh * jb.nchunk + c];
+            M = fmaxf(M, part[it.part + (size_t)rho * (D + 2)]);
+        }
+        float L = 0.0f, O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int c = 0; c < jb.nchunk; c++) {
+            const AttnItem it = items[jb.item0 + kvh * jb.nchunk + c];
+            const float* src = part + it.part + (size_t)rho * (D + 2);
+            const float mc = src[0];
+            if (mc == -INFINITY) continue;
+            const float f = expf(mc - M);
+            L += src[1] * f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) O[j] += src[2 + d0 + j] * f;
+        }
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = O[j] / L;
+        const int i = rho / group, gi = rho % group;
+        const int r = jb.row0 + i;
+        const int k = (kvh * group + gi) * D + d0;
+        if (ctx_out) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) ctx_out[(size_t)r * nH * D + k + j] = v[j];
+        }
+        write_hilo(Xp, r, k / 8, KU, v);
+    }
+}
+
+void launch_attn_combine(hipStream_t st, const JobDev* jobs, int njobs, const AttnItem* items,
+                         const float* part, const KVGeom& g, int nH, int group, int M, int Mpad, int KU,
+                         uint4* Xp, float* ctx_out) {
+    (void)M;
+    (void)Mpad;
+    hipLaunchKernelGGL(k_attn_combine, dim3(njobs * g.nKV), dim3(256), 0, st, jobs, items, part, g, nH,
+                       group, KU, Xp, ctx_out);
+    CHECK_LAUNCH();
+}
+
+// =============================================================== embedding ===
+// gather_embed_nopos_q8 (web/model/kernels.js:895-917) + round_f16 (the
+// embedding rows are rounded like a block's output, stage.js:1365-1370);
+// or, for a pass entering past position 0, the f16 rows handed in.
+__global__ void k_embed(const int32_t* __restrict__ ids, const uint16_t* __restrict__ hidden, int T, int H,
+                        const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales, int KU,
+                        float* __restrict__ x) {
+    const int t = blockIdx.y;
+    const int h = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T || h >= H) return;
+    if (!ids) {
+        x[(size_t)t * H + h] = half_value(hidden[(size_t)t * H + h]);
+        return;
+    }
+    const int v = ids[t];
+    const int tile = v >> 4, u = h >> 6, lane = (v & 15) + 16 * ((h & 31) >> 3);
+    const int byte = 8 * ((h & 63) >> 5) + (h & 7);
+    const uint8_t b = codes[(((size_t)tile * KU + u) * 64 + lane) * 16 + byte];
+    const int8_t q = (int8_t)(b ^ 0x80);
+    const uint16_t sb = scales[(((size_t)tile * KU + u) * 16 + (v & 15)) * 2 + ((h >> 5) & 1)];
+    x[(size_t)t * H + h] = round_f16_value((float)q * half_value(sb));
+}
+
+void launch_embed(hipStream_t st, const int32_t* ids, const uint16_t* hidden, int T, const QTensor& wte,
+                  float* x) {
+    dim3 grid((wte.K + 255) / 256, T);
+    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, st, ids, hidden, T, wte.K, wte.codes, wte.scales, wte.KU,
+                       x);
+    CHECK_LAUNCH();
+}
+
+// ==================================================================== top-k ===
+// topk_stage / topkRows (web/model/kernels.js:1453-1507, :2129-2144): per row
+// the best M (value, index) pairs, larger value first, ties to the lower
+// index. Keys pack (order-preserving value bits, ~index) so a descending
+// sort of 64-bit keys is that order; 4096 keys per workgroup are bitonic
+// sorted in LDS and the best M kept, stage after stage until one workgroup's
+// output is left.
+__device__ static inline uint64_t topk_key(float v, uint32_t i) {
+    uint32_t b = f2u(v);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)b << 32) | (uint64_t)(0xffffffffu - i);
+}
+
+constexpr int TOPK_CH = 4096;
+
+__global__ __launch_bounds__(256) void k_topk_stage(const float* __restrict__ logits,
+                                                    const uint64_t* __restrict__ keys_in, int n, int M,
+                                                    uint64_t* __restrict__ out) {
+    __shared__ uint64_t s[TOPK_CH];
+    const int row = blockIdx.y;
+    const int base = blockIdx.x * TOPK_CH;
+    for (int k = threadIdx.x; k < TOPK_CH; k += 256) {
+        const int i = base + k;
+        uint64_t key = 0;
+        if (i < n) key = logits ? topk_key(logits[(size_t)row * n + i], (uint32_t)i) : keys_in[(size_t)row * n + i];
+        s[k] = key;
+    }
+    __syncthreads();
+    for (int size = 2; size <= TOPK_CH; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = threadIdx.x; i < TOPK_CH; i += 256) {
+                const int l = i ^ stride;
+                if (l > i) {
+                    const bool desc = (i & size) == 0;
+                    const uint64_t a = s[i], b = s[l];
+                    if (desc ? (a < b) : (a > b)) {
+                        s[i] = b;
+                        s[l] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    const int groups = gridDim.x;
+    for (int m = threadIdx.x; m < M; m += 256) out[(size_t)row * groups * M + (size_t)blockIdx.x * M + m] = s[m];
+}
+
+__global__ void k_topk_unpack(const uint64_t* __restrict__ keys, int rows, int M, float* __restrict__ vals,
+                              uint32_t* __restrict__ ids) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * M) return;
+    const uint64_t k = keys[i];
+    uint32_t b = (uint32_t)(k >> 32);
+    b = (b & 0x80000000u) ? (b & 0x7fffffffu) : ~b;
+    vals[i] = u2f(b);
+    ids[i] = 0xffffffffu - (uint32_t)(k & 0xffffffffu);
+}
+
+void launch_topk(hipStream_t st, const float* logits, int rows, int V, int M, uint64_t* a, uint64_t* b,
+                 float* vals, uint32_t* ids) {
+    int n = V;
+    const float* lg = logits;
+    const uint64_t* in = nullptr;
+    uint64_t* out = a;
+    uint64_t* other = b;
+    for (;;) {
+        const int groups = (n + TOPK_CH - 1) / TOPK_CH;
+        hipLaunchKernelGGL(k_topk_stage, dim3(groups, rows), dim3(256), 0, st, lg, in, n, M, out);
+        CHECK_LAUNCH();
+        if (groups == 1) break;
+        lg = nullptr;
+        in = out;
+        n = groups * M;
+        uint64_t* t = out;
+        out = other;
+        other = t;
+    }
+    hipLaunchKernelGGL(k_topk_unpack, dim3((rows * M + 255) / 256), dim3(256), 0, st, out, rows, M, vals, ids);
+    CHECK_LAUNCH();
+}
+
+// ============================================================ small kernels ===
+__global__ void k_round_f16(float* a, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        a[i] = round_f16_value(a[i]);
+}
+
+void launch_round_f16(hipStream_t st, float* a, int64_t n) {
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_round_f16, dim3((unsigned)blocks), dim3(256), 0, st, a, n);
+    CHECK_LAUNCH();
+}
+
+__global__ void k_fill(float* p, int64_t n, float v) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+void launch_fill(hipStream_t st, float* p, int64_t n, float v) {
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_fill, dim3((unsigned)blocks), dim3(256), 0, st, p, n, v);
+    CHECK_LAUNCH();
+}
+
+// Page allocation (web/model/model.js:191-202 ensurePages, replayed for every
+// job of the pass in job order): plan[4j..4j+3] = slot, owned, new, prefix.
+// The host tracks counts (the stack top and each frame's length); the device
+// holds the indices. Job j's k-th new page is the stack entry
+// top-1-(prefix+k): what sequential pops would return.
+__global__ void k_alloc_pages(const int32_t* __restrict__ plan, int njobs, const uint32_t* __restrict__ free_stack,
+                              int top, uint32_t* __restrict__ page_table, int max_pages) {
+    const int j = blockIdx.x;
+    if (j >= njobs) return;
+    const int slot = plan[4 * j], owned = plan[4 * j + 1], nw = plan[4 * j + 2], pre = plan[4 * j + 3];
+    for (int k = threadIdx.x; k < nw; k += blockDim.x)
+        page_table[(size_t)slot * max_pages + owned + k] = free_stack[top - 1 - (pre + k)];
+}
+
+void launch_alloc_pages(hipStream_t st, const int32_t* plan, int njobs, const uint32_t* free_stack, int top,
+                        uint32_t* page_table, int max_pages) {
+    if (njobs <= 0) return;
+    hipLaunchKernelGGL(k_alloc_pages, dim3(njobs), dim3(64), 0, st, plan, njobs, free_stack, top, page_table,
+                       max_pages);
+    CHECK_LAUNCH();
+}
+
+// freePages (web/model/model.js:204-211): push the frame's pages back, last
+// owned first, so the next pop returns its first page.
+__global__ void k_release_pages(int slot, int owned, uint32_t* __restrict__ free_stack, int top,
+                                const uint32_t* __restrict__ page_table, int max_pages) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < owned; i += gridDim.x * blockDim.x)
+        free_stack[top + i] = page_table[(size_t)slot * max_pages + owned - 1 - i];
+}
+
+void launch_release_pages(hipStream_t st, int slot, int owned, uint32_t* free_stack, int top,
+                          const uint32_t* page_table, int max_pages) {
+    if (owned <= 0) return;
+    hipLaunchKernelGGL(k_release_pages, dim3((owned + 255) / 256), dim3(256), 0, st, slot, owned, free_stack,
+                       top, page_table, max_pages);
+    CHECK_LAUNCH();
+}
+
+// ================================================================ synthetic ===
+// A q8 tensor [N, K] generated straight into the tiled layout at row tile
+// `row_tile0` of w (fused tensors stack their row tiles). Codes
+// clamp(round(N(0,40)), ±127) from the Irwin-Hall generator at index n*K + k;
+// f16 scales ~U(1e-4, 4e-4) at index n*ng + g in stream ^ 0x5ca1e.
+__global__ void k_gen_q8(uint8_t* __restrict__ codes, uint16_t* __restrict__ scales, int KU, int row_tile0,
+                         int N, int K, uint64_t seed, uint64_t stream) {
+    const int tiles = (N + 15) / 16;
+    const int64_t total = (int64_t)tiles * KU * 64;
+    const int ng = (K + 31) / 32;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(i & 63);
+        const int64_t tu = i >> 6;
+        const int u = (int)(tu % KU), t = (int)(tu / KU);
+        const int n = 16 * t + (lane & 15);
+        uint8_t b[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const int k = 64 * u + 32 * (j >> 3) + 8 * (lane >> 4) + (j & 7);
+            int q = 0;
+            if (n < N && k < K) q = gen_code(cc_rng(seed, stream, (uint64_t)n * K + k));
+            b[j] = (uint8_t)((q & 0xff) ^ 0x80);
+        }
+        uint8_t* dst = codes + ((((size_t)(row_tile0 + t)) * KU + u) * 64 + lane) * 16;
+#pragma unroll
+        for (int j = 0; j < 16; j++) dst[j] = b[j];
+        if (lane < 16) {
+            for (int h = 0; h < 2; h++) {
+                const int gg = 2 * u + h;
+                uint16_t sbits = 0;
+                if (n < N && gg < ng) sbits = gen_scale_f16(seed, stream ^ 0x5ca1eull, (uint64_t)n * ng + gg, 1e-4, 4e-4);
+                scales[(((size_t)(row_tile0 + t)) * KU + u) * 32 + lane * 2 + h] = sbits;
+            }
+        }
+    }
+}
+
+void launch_gen_q8(hipStream_t st, const QTensor& w, int row_tile0, int N, int K, uint64_t seed,
+                   uint64_t stream) {
+    const int64_t total = (int64_t)((N + 15) / 16) * w.KU * 64;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_gen_q8, dim3((unsigned)blocks), dim3(256), 0, st, w.codes, w.scales, w.KU, row_tile0,
+                       N, K, seed, stream);
+    CHECK_LAUNCH();
+}
+
+// Host int8 [N, K] codes + f16 scales [N, ceil(K/group)] (group 32) -> tiled.
+__global__ void k_tile_q8(const int8_t* __restrict__ src, const uint16_t* __restrict__ sc, int N, int K,
+                          uint8_t* __restrict__ codes, uint16_t* __restrict__ scales, int KU, int row_tile0) {
+    const int tiles = (N + 15) / 16;
+    const int64_t total = (int64_t)tiles * KU * 64;
+    const int ng = (K + 31) / 32;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int lane = (int)(i & 63);
+        const int64_t tu = i >> 6;
+        const int u = (int)(tu % KU), t = (int)(tu / KU);
+        const int n = 16 * t + (lane & 15);
+        uint8_t* dst = codes + ((((size_t)(row_tile0 + t)) * KU + u) * 64 + lane) * 16;
+        for (int j = 0; j < 16; j++) {
+            const int k = 64 * u + 32 * (j >> 3) + 8 * (lane >> 4) + (j & 7);
+            const int q = (n < N && k < K) ? src[(size_t)n * K + k] : 0;
+            dst[j] = (uint8_t)((q & 0xff) ^ 0x80);
+        }
+        if (lane < 16)
+            for (int h = 0; h < 2; h++) {
+                const int gg = 2 * u + h;
+                scales[(((size_t)(row_tile0 + t)) * KU + u) * 32 + lane * 2 + h] =
+                    (n < N && gg < ng) ? sc[(size_t)n * ng + gg] : (uint16_t)0;
+            }
+    }
+}
+
+void launch_tile_q8(hipStream_t st, const int8_t* codes, const uint16_t* scales, int N, int K, int group,
+                    const QTensor& w, int row_tile0) {
+    (void)group;
+    const int64_t total = (int64_t)((N + 15) / 16) * w.KU * 64;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_tile_q8, dim3((unsigned)blocks), dim3(256), 0, st, codes, scales, N, K, w.codes,
+                       w.scales, w.KU, row_tile0);
+    CHECK_LAUNCH();
+}
+
+// Random KV rows 0..tokens-1 of a slot in one layer's pool (which: 0 = K,
+// 1 = V): the generator of the test oracle (codes uniform in ±127 at index
+// base*D + d, base = ((key << 24) + t)*nKV + head; one f16 scale
+// ~U(0.005, 0.02) at base, replicated into every 32-block).
+__global__ void k_fill_kv(uint8_t* __restrict__ pool, const uint32_t* __restrict__ page_table, int slot,
+                          int tokens, KVGeom g, uint64_t seed, uint64_t stream, uint64_t key, int which) {
+    const int D = g.D;
+    const int64_t total = (int64_t)tokens * g.nKV * D;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int d = (int)(i % D);
+        const int64_t tn = i / D;
+        const int n = (int)(tn % g.nKV), t = (int)(tn / g.nKV);
+        const uint64_t base = ((key << 24) + (uint64_t)t) * (uint64_t)g.nKV + (uint64_t)n;
+        const uint64_t r = cc_rng(seed, stream, base * (uint64_t)D + (uint64_t)d);
+        const int8_t code = (int8_t)((int)((r >> 8) % 255u) - 127);
+        const uint32_t page = page_table[(size_t)slot * g.max_pages + t / g.page];
+        const int s = t % g.page;
+        uint8_t* blk = pool + ((size_t)page * g.nKV + n) * g.blk;
+        if (which == 0) blk[(size_t)s * D + kpos(d, D)] = (uint8_t)code;
+        else blk[(size_t)d * 64 + vpos(s)] = (uint8_t)code;
+        if ((d & 31) == 0) {
+            const float sc = half_value(gen_scale_f16(seed, stream ^ 0x5ca1eull, base, 0.005, 0.02));
+            const int b = d >> 5;
+            if (which == 0) *(float*)(blk + 64 * D + ((size_t)s * g.ng + b) * 4) = sc;
+            else *(float*)(blk + 64 * D + ((size_t)b * 64 + vpos(s)) * 4) = sc;
+        }
+    }
+}
+
+void launch_fill_kv(hipStream_t st, uint8_t* pool, const uint32_t* page_table, int slot, int tokens,
+                    const KVGeom& g, uint64_t seed, uint64_t stream, uint64_t key, int which) {
+    const int64_t total = (int64_t)tokens * g.nKV * g.D;
+    if (total <= 0) return;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    hipLaunchKernelGGL(k_fill_kv, dim3((unsigned)blocks), dim3(256), 0, st, pool, page_table, slot, tokens, g,
+                       seed, stream, key, which);
+    CHECK_LAUNCH();
+}
+
+// Device block layout <-> the reference's rows (kernels.js:999-1022): row
+// word w < D/4 packs codes 4w..4w+3 (low byte first); then D/32 f32 scales.
+__global__ void k_kv_ref(uint8_t* __restrict__ pool, const uint32_t* __restrict__ page_table, int slot, int head,
+                         int t0, int t1, KVGeom g, int which, uint32_t* __restrict__ rows, int to_ref) {
+    const int D = g.D, RW = D / 4 + g.ng;
+    const int64_t total = (int64_t)(t1 - t0) * RW;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int w = (int)(i % RW), t = t0 + (int)(i / RW);
+        const uint32_t page = page_table[(size_t)slot * g.max_pages + t / g.page];
+        const int s = t % g.page;
+        uint8_t* blk = pool + ((size_t)page * g.nKV + head) * g.blk;
+        if (w < D / 4) {
+            uint8_t* p[4];
+            for (int j = 0; j < 4; j++) {
+                const int d = 4 * w + j;
+                p[j] = which == 0 ? blk + (size_t)s * D + kpos(d, D) : blk + (size_t)d * 64 + vpos(s);
+            }
+            if (to_ref) {
+                uint32_t word = 0;
+                for (int j = 0; j < 4; j++) word |= (uint32_t)(*p[j]) << (8 * j);
+                rows[i] = word;
+            } else {
+                const uint32_t word = rows[i];
+                for (int j = 0; j < 4; j++) *p[j] = (uint8_t)(word >> (8 * j));
+            }
+        } else {
+            const int b = w - D / 4;
+            uint32_t* sp = which == 0 ? (uint32_t*)(blk + 64 * D + ((size_t)s * g.ng + b) * 4)
+                                      : (uint32_t*)(blk + 64 * D + ((size_t)b * 64 + vpos(s)) * 4);
+            if (to_ref) rows[i] = *sp;
+            else *sp = rows[i];
+        }
+    }
+}
+
+void launch_kv_to_ref(hipStream_t st, const uint8_t* pool, const uint32_t* page_table, int slot, int head, int t0,
+                      int t1, const KVGeom& g, int which, uint32_t* out) {
+    const int64_t total = (int64_t)(t1 - t0) * (g.D / 4 + g.ng);
+    if (total <= 0) return;
+    hipLaunchKernelGGL(k_kv_ref, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, (uint8_t*)pool,
+                       page_table, slot, head, t0, t1, g, which, out, 1);
+    CHECK_LAUNCH();
+}
+
+void launch_kv_from_ref(hipStream_t st, uint8_t* pool, const uint32_t* page_table, int slot, int head, int t0,
+                        int t1, const KVGeom& g, int which, const uint32_t* in) {
+    const int64_t total = (int64_t)(t1 - t0) * (g.D / 4 + g.ng);
+    if (total <= 0) return;
+    hipLaunchKernelGGL(k_kv_ref, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, pool, page_table, slot,
+                       head, t0, t1, g, which, (uint32_t*)in, 0);
+    CHECK_LAUNCH();
+}
+
+// Sum the K splits of a projection: out[m][n] = sum_s part[s][m][n], in order.
+__global__ void k_sum_splits(const float* __restrict__ part, int splits, int M, int N, float* __restrict__ out) {
+    const int64_t total = (int64_t)M * N;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        float p = part[i];
+        for (int s = 1; s < splits; s++) p = p + part[(size_t)s * total + i];
+        out[i] = p;
+    }
+}
+
+void launch_sum_splits(hipStream_t st, const float* part, int splits, int M, int N, float* out) {
+    const int64_t total = (int64_t)M * N;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_sum_splits, dim3((unsigned)blocks), dim3(256), 0, st, part, splits, M, N, out);
+    CHECK_LAUNCH();
+}
+
+// Rows of f16 values kept as f32 -> their half bits (exact).
+__global__ void k_to_half_bits(const float* __restrict__ x, int64_t n, uint16_t* __restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = half_bits(x[i]);
+}
+
+void launch_to_half_bits(hipStream_t st, const float* x, int64_t n, uint16_t* out) {
+    int64_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_to_half_bits, dim3((unsigned)blocks), dim3(256), 0, st, x, n, out);
+    CHECK_LAUNCH();
+}

@@ -1,0 +1,196 @@
+/* ccdecode.h — C ABI of the MI355X batched ragged decode pass.
+ *
+ * The library replaces the GPU side of the reference's Runner
+ * (web/model/stage.js): one context owns a contiguous range of positions
+ * (0 = embedding, 1..L = blocks, L+1 = final norm + LM head), its q8 weights,
+ * an int8 paged KV pool, session frames (slots) with page tables, and all
+ * scratch. cc_step runs one packed pass over prepared jobs — the reference's
+ * Runner.#pass (web/model/stage.js:1314-1481) — and returns per-row top-M
+ * candidates or the f16 rows handed downstream.
+ *
+ * Host policy (queueing, batching rules, admission, eviction, cuts, boundary
+ * logs) stays with the caller, as it does in the reference's Runner; the
+ * caller is the JS shim (chattorrent_amd/node/runner.js) over the N-API addon,
+ * or Python over ctypes. Every entry point returns a cc_status; on failure
+ * cc_last_error() holds the message. A context is not reentrant: calls on one
+ * context must not overlap (the reference runs jobs one at a time,
+ * web/model/stage.js:5, :646-654).
+ *
+ * Plain C types only. Host buffers are owned by the caller for the duration of
+ * the call; the library copies through its own pinned staging.
+ */
+#ifndef CCDECODE_H
+#define CCDECODE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Error classes of the reference's Runner, kept per job
+ * (web/model/stage.js:930-941 busy, :948-958 / :1073-1079 cold,
+ * :1067-1072 stale, :339-345 nospec, :1225-1259 bad job, :1114-1117 pool too
+ * small; device loss: web/engine.js:703-744). */
+typedef enum cc_status {
+    CC_OK = 0,
+    CC_BUSY = 1,      /* capacity refusal (no frame / page free now) */
+    CC_COLD = 2,      /* the session's cache is not here (evicted or behind) */
+    CC_STALE = 3,     /* a duplicate job behind the cache */
+    CC_NOSPEC = 4,    /* no speculative replay state (hybrid models only) */
+    CC_EARG = 5,      /* a malformed job or call */
+    CC_EPOOL = 6,     /* the KV pool cannot hold this context at all */
+    CC_EOOM = 7,      /* device allocation failed */
+    CC_EDEVICE = 8    /* a HIP error; the context should be destroyed */
+} cc_status;
+
+/* Model dimensions: loader.js dimsFromManifest (web/model/loader.js:146-201),
+ * checked like model.js checkDims (web/model/model.js:22-40). */
+typedef struct cc_dims {
+    int32_t hidden, n_layer, n_heads, n_kv_heads, head_dim, ffn, vocab;
+    int32_t q8_group;       /* weights: one scale per this many values along K (32) */
+    float rms_eps;
+    double rope_theta;
+    int32_t rope_scaling;   /* 0 none, 1 llama3 (kernels.js:1998-2014) */
+    double rs_factor, rs_low_freq, rs_high_freq, rs_orig_max_pos;
+    int32_t tied;           /* LM head reads the embedding table */
+} cc_dims;
+
+/* Runner options (web/model/stage.js:107-110). lo/hi: the position range
+ * held; n_max: context window; t_max: the most rows one pass carries; slots:
+ * full contexts the KV pool holds (pages = slots * ceil(n_max/page));
+ * sessions: frames (page tables). */
+typedef struct cc_opts {
+    int32_t lo, hi;
+    int32_t n_max;
+    int32_t t_max;
+    int32_t slots;
+    int32_t sessions;
+    int32_t page_tokens;    /* 64 (web/split.js:75) */
+    int32_t max_jobs;       /* the most jobs one pass packs */
+    int32_t device;
+} cc_opts;
+
+typedef struct cc_ctx cc_ctx;
+
+/* Tensor ids for cc_upload / cc_fill_random (HF names). layer = -1 for the
+ * model-level tensors. */
+enum {
+    CC_T_Q = 0, CC_T_K = 1, CC_T_V = 2, CC_T_O = 3, CC_T_GATE = 4, CC_T_UP = 5, CC_T_DOWN = 6,
+    CC_T_LN1 = 7, CC_T_LN2 = 8, CC_T_WTE = 9, CC_T_NORM = 10, CC_T_LM_HEAD = 11
+};
+enum { CC_SCALES_F16 = 0, CC_SCALES_F32 = 1 };
+
+/* new Runner(device, d, w, {...}) — web/model/stage.js:107-238. */
+cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out);
+void cc_destroy(cc_ctx* ctx);
+const char* cc_last_error(const cc_ctx* ctx);
+
+/* uploadQ8(device, int8Bytes, scales, group) — web/model/kernels.js:122-126;
+ * norms (tensor LN1/LN2/NORM) are f32 `data` with n = hidden and no scales.
+ * q8 tensors: `data` int8 [N, K] row-major, `scales` [N, ceil(K/group)] as
+ * f16 bits or f32 (rounded to the device's f16 scale). */
+cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data, size_t n,
+                    const void* scales, size_t ns, int32_t scale_dtype, int32_t group);
+
+/* Synthetic weights on the device from the counter-based generator shared
+ * with the test oracle (no reference counterpart: the reference's random
+ * models are randomWeights, web/model/model.js:697-717). */
+cc_status cc_fill_random(cc_ctx* ctx, uint64_t seed);
+
+/* One prepared job of a pass (the fields #prepare hands #pass,
+ * web/model/stage.js:1195-1308). `ids` when the pass enters at position 0,
+ * else `hidden` (n*hidden f16 bits). `sampled`: rows the head samples — 1
+ * (the last row) or n (a verify); 0 when the pass does not reach the head. */
+typedef struct cc_job {
+    int32_t slot;
+    int32_t past;
+    int32_t n;
+    int32_t sampled;
+    const int32_t* ids;
+    const uint16_t* hidden;
+} cc_job;
+
+/* Runner.#pass — web/model/stage.js:1314-1481. Runs positions [at, to) for
+ * `njobs` jobs packed in order. Pages for rows past..past+n-1 are taken from
+ * the pool on the device in job order (model.js ensurePages replayed).
+ * Outputs: when `to` is past the last block (the head), `top_vals`/`top_ids`
+ * receive `topk` candidates per sampled row (sampled rows in job order, best
+ * first, ties to the lower id); otherwise `hidden_out` receives every row as
+ * f16 bits [T, hidden]. `status` (optional, njobs) is set per job. */
+cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, int32_t to,
+                  int32_t topk, float* top_vals, uint32_t* top_ids, uint16_t* hidden_out,
+                  int32_t* status);
+
+/* Runner.#release / freePages — web/model/stage.js:842-874,
+ * web/model/model.js:204-211: the slot's pages return to the pool. */
+cc_status cc_release(cc_ctx* ctx, int32_t slot);
+
+/* Frame pages the slot holds (the frame's `owned` length). */
+int32_t cc_slot_pages(const cc_ctx* ctx, int32_t slot);
+int32_t cc_free_pages(const cc_ctx* ctx);
+
+/* Fill rows 0..tokens-1 of a slot with random int8 KV (codes uniform in
+ * ±127, one f16 scale ~U(0.005, 0.02) per token and kv head), taking pages
+ * as a job would. `key` names the chat in the generator index. */
+cc_status cc_fill_random_kv(cc_ctx* ctx, int32_t slot, int32_t tokens, uint64_t seed, uint64_t key);
+
+/* Debug readback in the reference's row layout (web/model/kernels.js:999-1022:
+ * D/4 code words then D/QB f32 scales per row): rows t0..t1-1 of one kv head,
+ * which = 0 for K, 1 for V, `layer` a held block index. */
+cc_status cc_read_kv(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot, int32_t head,
+                     int32_t t0, int32_t t1, uint32_t* out);
+cc_status cc_write_kv(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot, int32_t head,
+                      int32_t t0, int32_t t1, const uint32_t* rows);
+cc_status cc_read_pages(cc_ctx* ctx, int32_t slot, uint32_t* out, int32_t n);
+
+/* Stats (Runner.counts / vramBytes, web/model/stage.js:219-259). */
+typedef struct cc_stats {
+    uint64_t vram_bytes;
+    uint64_t weight_bytes;
+    uint64_t kv_bytes;
+    uint64_t scratch_bytes;
+    int64_t passes;
+    int64_t rows;
+    double last_pass_ms;
+} cc_stats;
+cc_status cc_stats_get(const cc_ctx* ctx, cc_stats* out);
+
+/* Per-kernel timing with HIP events on the context's stream (the
+ * reference's gpuprof.js level 2, web/model/gpuprof.js:1-12, re-done for
+ * HIP). While enabled, every launch of the classes below is bracketed by
+ * events; cc_profile_read returns the summed milliseconds, the launch count
+ * and the algorithmic HBM bytes of those launches (q8 weights at 1.0625 B
+ * per weight; KV rows at D + 4*D/32 B). Enabling resets the sums. */
+enum { CC_K_QKV = 0, CC_K_O = 1, CC_K_GU = 2, CC_K_DOWN = 3, CC_K_HEAD = 4, CC_K_ATTN = 5, CC_K_COUNT = 6 };
+cc_status cc_profile(cc_ctx* ctx, int32_t enable);
+cc_status cc_profile_read(const cc_ctx* ctx, int32_t kind, double* ms, int64_t* launches, double* bytes);
+
+/* ---- Kernel-level entry points (one reference kernel each), used by the
+ * parity tests to hold each GPU kernel to the oracle on identical inputs. All
+ * pointers are host memory. ---- */
+
+/* matmulNobias for q8 — web/model/kernels.js:1874-1914. Y[M,N] = X[M,K] W^T. */
+cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K,
+                          const int8_t* W, const uint16_t* scales_f16, int32_t N, float* Y);
+/* store_kv — web/model/kernels.js:1960-1973, into `slot`'s pages of block
+ * `layer`: src [T_new, nKV*D] f32; rope != 0 rotates (K), else V. */
+cc_status cc_op_store_kv(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot,
+                         const float* src, int32_t T_new, int32_t T_past);
+/* round_f16 — web/model/kernels.js:2100-2105. In place on n floats. */
+cc_status cc_op_round_f16(cc_ctx* ctx, float* a, int64_t n);
+/* topkRows — web/model/kernels.js:2129-2144: rows x V logits → M pairs. */
+cc_status cc_op_topk(cc_ctx* ctx, const float* logits, int32_t rows, int32_t V, int32_t M,
+                     float* vals, uint32_t* ids);
+/* rmsnorm — web/model/kernels.js:1927-1932. */
+cc_status cc_op_rmsnorm(cc_ctx* ctx, const float* x, const float* w, int32_t T, int32_t H,
+                        float* y);
+/* attend (web/model/model.js:321-351) for one job of block `layer` whose K/V
+ * rows are already stored: q [n, nH*D] f32 (before RoPE) -> out [n, nH*D]. */
+cc_status cc_op_attend(cc_ctx* ctx, int32_t layer, int32_t slot, const float* q, int32_t n,
+                       int32_t past, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

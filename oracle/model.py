@@ -1,0 +1,257 @@
+"""Oracle restatement of the batched ragged decode pass (test infrastructure only).
+
+Follows, step for step:
+
+* ``web/model/model.js:619-624`` blockSegs and ``:368-409`` fullBlockSegs — one
+  block over packed segments: rmsnorm, q/k/v, per-segment attention over the
+  session's own pages, o_proj, residual, SwiGLU MLP, residual, then
+  ``round_f16`` of the residual stream;
+* ``web/model/model.js:321-351`` attend — store K (RoPE'd) and V into the
+  paged int8 cache, RoPE on Q, scores, exact causal softmax, P·V;
+* ``web/model/model.js:664-679`` forward and ``web/model/stage.js:1314-1440``
+  #pass — embedding gather + round, blocks, head on the sampled rows
+  (rmsnorm, LM head, top-M);
+* ``web/model/model.js:132-211`` the page pool: a free stack initialised so
+  the lowest index pops first, ``ensurePages`` pops in logical order,
+  ``freePages`` pushes a frame's pages back in reverse.
+
+Synthetic weights come from the same counter-based generator the device uses
+(stream numbering below), so host and device start from identical bits.
+"""
+import math
+
+import numpy as np
+
+from . import lib as L
+
+# Generator streams, shared with chattorrent_amd/csrc (synth.hip).
+STREAM_WTE = 1
+STREAM_LM_HEAD = 2
+TENSORS = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+def layer_stream(layer, name):
+    return (layer + 1) * 16 + TENSORS.index(name)
+
+
+def kv_stream(layer, which):
+    """Stream of a layer's random KV fill; which = 0 for K, 1 for V."""
+    return 0x4B560000 + layer * 2 + which
+
+
+PAGE_TOKENS = 64  # web/split.js:75
+
+
+def kv_row_words(D):
+    """web/model/kernels.js:1955-1958 kvRowWords: D/4 code words + D/QB scales."""
+    return D // 4 + D // min(32, D)
+
+
+def tensor_shapes(d):
+    H, D, F = d["hidden"], d["head_dim"], d["ffn"]
+    return {
+        "q": (d["n_heads"] * D, H), "k": (d["n_kv_heads"] * D, H), "v": (d["n_kv_heads"] * D, H),
+        "o": (H, d["n_heads"] * D), "gate": (F, H), "up": (F, H), "down": (H, F),
+    }
+
+
+class PagePool:
+    """web/model/model.js:132-147 makePagePool + :191-211 ensurePages/freePages."""
+
+    def __init__(self, n_pages, page_tokens=PAGE_TOKENS):
+        self.n_pages = n_pages
+        self.page_tokens = page_tokens
+        self.free = list(range(n_pages - 1, -1, -1))  # pops lowest index first
+
+    def ensure(self, frame, tokens):
+        need = -(-tokens // self.page_tokens)
+        if need > frame["max_pages"]:
+            return False
+        while len(frame["owned"]) < need:
+            if not self.free:
+                return False
+            phys = self.free.pop()
+            frame["pages"][len(frame["owned"])] = phys
+            frame["owned"].append(phys)
+        return True
+
+    def release(self, frame):
+        n = len(frame["owned"])
+        while frame["owned"]:
+            self.free.append(frame["owned"].pop())
+        return n
+
+
+class Model:
+    """A full-attention Llama-style model with q8 weights and an int8 paged KV pool."""
+
+    def __init__(self, d, n_slots, max_pages, n_pages=None, page_tokens=PAGE_TOKENS):
+        self.d = d
+        self.group = d.get("group_q8", 32)
+        self.page = page_tokens
+        self.max_pages = max_pages
+        self.pool = PagePool(n_pages if n_pages is not None else n_slots * max_pages, page_tokens)
+        D, nKV = d["head_dim"], d["n_kv_heads"]
+        self.rw = kv_row_words(D)
+        words = self.pool.n_pages * nKV * page_tokens * self.rw
+        self.K = [np.zeros(words, np.uint32) for _ in range(d["n_layer"])]
+        self.V = [np.zeros(words, np.uint32) for _ in range(d["n_layer"])]
+        self.frames = [{"pages": np.zeros(max_pages, np.uint32), "owned": [], "max_pages": max_pages}
+                       for _ in range(n_slots)]
+        self.rot = d.get("rot_dim", D)
+        self.tbl = L.rope_table(self.rot, d["rope_theta"], max_pages * page_tokens + 64,
+                                d.get("rope_scaling"))
+        self.w = None
+
+    # --- weights -------------------------------------------------------------
+    def gen_weights(self, seed):
+        d, g = self.d, self.group
+        self.w = {"layers": []}
+        for layer in range(d["n_layer"]):
+            lw = {}
+            for name, (N, K) in tensor_shapes(d).items():
+                codes, sc = L.gen_q8(seed, layer_stream(layer, name), N, K, g)
+                lw[name] = (codes, L.from_f16(sc))
+            lw["ln1"] = np.ones(d["hidden"], np.float32)
+            lw["ln2"] = np.ones(d["hidden"], np.float32)
+            self.w["layers"].append(lw)
+        codes, sc = L.gen_q8(seed, STREAM_WTE, d["vocab"], d["hidden"], g)
+        self.w["wte"] = (codes, L.from_f16(sc))
+        self.w["norm"] = np.ones(d["hidden"], np.float32)
+        if not d.get("tied", True):
+            codes, sc = L.gen_q8(seed, STREAM_LM_HEAD, d["vocab"], d["hidden"], g)
+            self.w["lm_head"] = (codes, L.from_f16(sc))
+
+    def head_weight(self):
+        return self.w.get("lm_head", self.w["wte"])
+
+    # --- KV ------------------------------------------------------------------
+    def fill_random_kv(self, slot, tokens, seed, key):
+        """Random KV rows 0..tokens-1 for `slot` (web/model/model.js:191-202
+        ensurePages takes the pages): codes uniform in [-127, 127], one f16
+        scale ~U(0.005, 0.02) per (token, kv head), widened and replicated into
+        each 32-block. `key` names the chat in the generator index, so the
+        device fill reproduces the same rows."""
+        d = self.d
+        D, nKV, page = d["head_dim"], d["n_kv_heads"], self.page
+        frame = self.frames[slot]
+        if not self.pool.ensure(frame, tokens):
+            raise RuntimeError("the KV pool cannot fit the fill")
+        nb = D // min(32, D)
+        t = np.arange(tokens)
+        for layer in range(d["n_layer"]):
+            for which, cache in ((0, self.K[layer]), (1, self.V[layer])):
+                codes, scales = L.gen_kv(seed, kv_stream(layer, which), key, 0, tokens, nKV, D)
+                for n in range(nKV):
+                    rows = ((frame["pages"][t // page].astype(np.int64) * nKV + n) * page + t % page) * self.rw
+                    cw = np.ascontiguousarray(codes[:, n, :]).view(np.uint32)
+                    for w in range(D // 4):
+                        cache[rows + w] = cw[:, w]
+                    sbits = np.ascontiguousarray(scales[:, n]).view(np.uint32)
+                    for b in range(nb):
+                        cache[rows + D // 4 + b] = sbits
+        return frame
+
+    def kv_rows(self, layer, which, slot, t0, t1, head):
+        """Reference-layout words of rows t0..t1-1 of one kv head: [t, RW] u32."""
+        d = self.d
+        nKV, page = d["n_kv_heads"], self.page
+        frame = self.frames[slot]
+        cache = (self.K if which == 0 else self.V)[layer]
+        t = np.arange(t0, t1)
+        rows = ((frame["pages"][t // page].astype(np.int64) * nKV + head) * page + t % page) * self.rw
+        return cache[rows[:, None] + np.arange(self.rw)[None, :]]
+
+    # --- the pass --------------------------------------------------------------
+    def attend(self, layer, slot, q, k, v, past):
+        d = self.d
+        D, nH, nKV, group = d["head_dim"], d["n_heads"], d["n_kv_heads"], d["n_heads"] // d["n_kv_heads"]
+        n = q.shape[0]
+        pages = self.frames[slot]["pages"]
+        Qh = np.ascontiguousarray(q.reshape(n, nH, D).transpose(1, 0, 2))
+        L.store_kv(k, self.K[layer], past, self.page, nKV, D, self.rot, pages, self.tbl)
+        L.store_kv(v, self.V[layer], past, self.page, nKV, D, 0, pages, None)
+        L.rope(Qh, self.rot, past, self.tbl)
+        T_act = past + n
+        scores = L.qk_scores(Qh, self.K[layer], n, T_act, self.page, D, nH, group, pages)
+        p = L.causal_softmax(scores, past)
+        ctx = L.attn_av(p, self.V[layer], D, self.page, group, pages)
+        return np.ascontiguousarray(ctx.transpose(1, 0, 2).reshape(n, nH * D))
+
+    def block(self, layer, x, segs):
+        d, g = self.d, self.group
+        lw = self.w["layers"][layer]
+        h = L.rmsnorm(x, lw["ln1"], d["rms_eps"])
+        q = L.matmul_q8(h, *lw["q"], group=g)
+        k = L.matmul_q8(h, *lw["k"], group=g)
+        v = L.matmul_q8(h, *lw["v"], group=g)
+        merged = np.empty_like(q)
+        for s in segs:
+            a, b = s["row"], s["row"] + s["n"]
+            merged[a:b] = self.attend(layer, s["slot"], q[a:b], k[a:b], v[a:b], s["past"])
+        attn = L.matmul_q8(merged, *lw["o"], group=g)
+        L.add_inplace(x, attn)
+        h = L.rmsnorm(x, lw["ln2"], d["rms_eps"])
+        gt = L.matmul_q8(h, *lw["gate"], group=g)
+        up = L.matmul_q8(h, *lw["up"], group=g)
+        act = L.silu_mul(gt, up)
+        dn = L.matmul_q8(act, *lw["down"], group=g)
+        L.add_inplace(x, dn)
+        L.lib().orc_round_f16(L._p(x), x.size)
+        return x
+
+    def pass_(self, jobs, layers=None, head=True, capture=None):
+        """One packed pass. `jobs`: dicts with slot, past, n, and ids [n] (or
+        hidden [n, H] f32 holding f16 values), `sampled` (rows the head samples:
+        the last one, or all n for a verify) and `topk` (M). Returns per job
+        {"hidden": [n,H] f32, "logits": [sampled, V], "vals", "ids"}.
+        `capture(layer, x)` is called with the residual after each block."""
+        d = self.d
+        H = d["hidden"]
+        segs, row = [], 0
+        for j in jobs:
+            frame = self.frames[j["slot"]]
+            if not self.pool.ensure(frame, j["past"] + j["n"]):
+                raise RuntimeError("the KV pool cannot fit the job")
+            segs.append({"slot": j["slot"], "past": j["past"], "n": j["n"], "row": row})
+            row += j["n"]
+        T = row
+        if "ids" in jobs[0] and jobs[0]["ids"] is not None:
+            ids = np.concatenate([np.asarray(j["ids"], np.int32) for j in jobs])
+            codes, sc = self.w["wte"]
+            x = L.gather_embed_q8(ids, codes, sc, self.group)
+            L.lib().orc_round_f16(L._p(x), x.size)
+        else:
+            x = np.ascontiguousarray(np.concatenate([np.asarray(j["hidden"], np.float32) for j in jobs]))
+        assert x.shape == (T, H)
+        for layer in (range(d["n_layer"]) if layers is None else layers):
+            self.block(layer, x, segs)
+            if capture is not None:
+                capture(layer, x)
+        out = []
+        for j, s in zip(jobs, segs):
+            r = {"hidden": x[s["row"]:s["row"] + s["n"]].copy()}
+            out.append(r)
+        if head:
+            rows = []
+            for j, s in zip(jobs, segs):
+                ns = j.get("sampled", 1)
+                rows.extend(range(s["row"] + s["n"] - ns, s["row"] + s["n"]))
+            if rows:
+                hs = L.rmsnorm(x[rows], self.w["norm"], d["rms_eps"])
+                logits = L.matmul_q8(hs, *self.head_weight(), group=self.group)
+                at = 0
+                for j, r in zip(jobs, out):
+                    ns = j.get("sampled", 1)
+                    M = j.get("topk", 1)
+                    r["logits"] = logits[at:at + ns]
+                    vals, ids = [], []
+                    for i in range(ns):
+                        v, ix = L.topk(logits[at + i], M)
+                        vals.append(v)
+                        ids.append(ix)
+                    r["vals"], r["ids"] = np.array(vals), np.array(ids)
+                    at += ns
+        return out
+
+

@@ -1,0 +1,184 @@
+"""Kernel-level parity: each HIP kernel against the oracle's restatement of the
+reference kernel, on the same seeded inputs (web/dev/kernels.test.js is the
+model: awkward dims, bitwise row invariance, closed-form checks).
+
+Bars: bit-exact for round_f16, the KV quantiser's codes and scales, top-k ids
+and values; tolerance for float reductions (stated per test)."""
+import numpy as np
+import pytest
+
+from chattorrent_amd import configs
+
+pytestmark = pytest.mark.gpu
+
+
+def _ctx(gpu, d=None, n_max=1024, t_max=64, slots=4):
+    from chattorrent_amd.ccdecode import Context
+    return Context(d or configs.with_layers(configs.SMOLLM2, 2), n_max=n_max, t_max=t_max, slots=slots)
+
+
+@pytest.fixture(scope="module")
+def ctx(gpu):
+    c = _ctx(gpu)
+    yield c
+    c.close()
+
+
+def test_round_f16_bit_exact(ctx):
+    """web/model/kernels.js:1356-1383 against web/f16.js semantics (the oracle
+    restates both): every tie between neighbouring halves, subnormals, clamps."""
+    from oracle import lib as L
+    halves = L.from_f16(np.arange(0x7c00, dtype=np.uint16))
+    mids = ((halves[:-1].astype(np.float64) + halves[1:]) / 2).astype(np.float32)
+    rng = np.random.default_rng(23)
+    noise = ((rng.random(50000) - 0.5) * 2.0 ** (rng.random(50000) * 40 - 25)).astype(np.float32)
+    special = np.array([0, -0.0, np.inf, -np.inf, 65504, 65519, 65520, 1e9, -1e9, 2 ** -24, 2 ** -25,
+                        3 * 2 ** -25, 2 ** -14, 2 ** -15, 1, -1, 1 + 2 ** -11, 1 + 3 * 2 ** -11], np.float32)
+    x = np.concatenate([special, mids, -mids, noise])
+    got = ctx.op_round_f16(x)
+    want = L.round_f16(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # and the result equals fromF16(toF16(x)) (web/f16.js), NaN aside
+    assert np.array_equal(got, L.from_f16(L.to_f16(x)))
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 576, 70), (5, 1000, 77), (12, 5120, 256), (17, 576, 1024),
+                                   (32, 1536, 96), (33, 576, 64), (64, 320, 48)])
+def test_matmul_q8_vs_oracle(ctx, M, K, N):
+    """matmul_gemv_q8 family (web/model/kernels.js:449-751): within a bound of
+    2^-20 of the sum of |terms| (the MFMA path sums in a different order; the
+    f16 hi/lo activation split keeps ~22 significant bits)."""
+    from oracle import lib as L
+    rng = np.random.default_rng(M * 1000 + K + N)
+    X = (rng.random((M, K), np.float32) * 2 - 1).astype(np.float32)
+    W = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    S16 = L.to_f16((rng.random((N, (K + 31) // 32)) * 2 - 1).astype(np.float32))
+    S = L.from_f16(S16)
+    got = ctx.op_matmul_q8(X, W, S16)
+    want = L.matmul_q8(X, W, S)
+    Sfull = np.repeat(S, 32, axis=1)[:, :K]
+    bound = np.abs(X).astype(np.float64) @ (np.abs(W.astype(np.float64)) * np.abs(Sfull)).T
+    exact = X.astype(np.float64) @ (W.astype(np.float64) * Sfull).T
+    assert np.all(np.abs(got - exact) <= 2.0 ** -20 * bound + 1e-30)
+    assert np.all(np.abs(got - want) <= 2.0 ** -19 * bound + 1e-30)
+
+
+def test_matmul_rows_match_one_row_bitwise(ctx):
+    """A row's bits do not depend on its batch-mates (web/dev/kernels.test.js:
+    578-650; docs/model.md 'Matching plain decoding row by row')."""
+    from oracle import lib as L
+    rng = np.random.default_rng(31)
+    K, N = 6 * 32 + 32, 70
+    W = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    S16 = L.to_f16((rng.random((N, K // 32)) * 2 - 1).astype(np.float32))
+    for M in [2, 3, 8, 15, 16, 17, 31, 32, 33, 48]:
+        X = (rng.random((M, K), np.float32) * 2 - 1).astype(np.float32)
+        rows = ctx.op_matmul_q8(X, W, S16)
+        for i in range(M):
+            one = ctx.op_matmul_q8(X[i:i + 1], W, S16)
+            assert np.array_equal(one.view(np.uint32), rows[i:i + 1].view(np.uint32)), (M, i)
+
+
+@pytest.mark.parametrize("V,M", [(1000, 1), (1000, 5), (49152, 40), (151936, 1), (151936, 256)])
+def test_topk_exact(ctx, V, M):
+    """topk_stage/topkRows (web/model/kernels.js:1453-1507, :2129-2144): best M
+    pairs, larger value first, ties to the lower index — exact."""
+    from oracle import lib as L
+    rng = np.random.default_rng(V + M)
+    rows = 3
+    logits = rng.standard_normal((rows, V)).astype(np.float32)
+    logits[:, 7::97] = logits[0, 3]          # planted ties
+    logits[1, 11] = logits[1].max() + 1      # a clear winner
+    vals, ids = ctx.op_topk(logits, M)
+    for r in range(rows):
+        wv, wi = L.topk(logits[r], M)
+        assert np.array_equal(ids[r], wi)
+        assert np.array_equal(vals[r].view(np.uint32), wv.view(np.uint32))
+
+
+def test_rmsnorm_vs_oracle(ctx):
+    """rmsnorm (web/model/kernels.js:930-976): the kernel keeps the reference's
+    256-lane strided sum and tree, so it matches the oracle to 1 ulp."""
+    from oracle import lib as L
+    rng = np.random.default_rng(4)
+    for T, H in [(3, 576), (5, 5120), (2, 70 * 4)]:
+        x = rng.standard_normal((T, H)).astype(np.float32)
+        w = (rng.random(H) + 0.5).astype(np.float32)
+        got = ctx.op_rmsnorm(x, w)
+        want = L.rmsnorm(x, w, ctx.d["rms_eps"])
+        assert np.allclose(got, want, rtol=2.0 ** -22, atol=0)
+
+
+def _oracle_cache(d, n_pages, page=64):
+    from oracle import model as Mo
+    rw = Mo.kv_row_words(d["head_dim"])
+    return np.zeros(n_pages * d["n_kv_heads"] * page * rw, np.uint32)
+
+
+@pytest.mark.parametrize("dims", ["smol", "27b"])
+def test_store_kv_bit_exact(gpu, dims):
+    """store_kv (web/model/kernels.js:1024-1073): RoPE'd K and plain V quantised
+    per 32 values — codes and scales bit-exact with the oracle given the same
+    input, including a zero block (scale 0, codes 0) and rows that cross a
+    page boundary; rows outside the job are untouched."""
+    from oracle import lib as L
+    from oracle import model as Mo
+    d = configs.with_layers(configs.SMOLLM2 if dims == "smol" else configs.M27B, 1)
+    c = _ctx(gpu, d, n_max=512, t_max=16, slots=2)
+    try:
+        D, nKV = d["head_dim"], d["n_kv_heads"]
+        rng = np.random.default_rng(5)
+        T_past, T_new = 60, 9                 # crosses the first page boundary
+        for which in (0, 1):
+            src = rng.standard_normal((T_new, nKV * D)).astype(np.float32)
+            src[0, :D] = 0.0                  # head 0 of row 0 all zero: zero blocks after RoPE too
+            c.op_store_kv(0, which, 1, src, T_past)
+            pages = c.pages(1)
+            cache = _oracle_cache(d, 16)
+            tbl = L.rope_table(D, d["rope_theta"], 1024)
+            L.store_kv(src, cache, T_past, 64, nKV, D, D if which == 0 else 0, pages, tbl if which == 0 else None)
+            rw = Mo.kv_row_words(D)
+            for h in range(nKV):
+                got = c.read_kv(0, which, 1, h, T_past, T_past + T_new)
+                t = np.arange(T_past, T_past + T_new)
+                rows = ((pages[t // 64].astype(np.int64) * nKV + h) * 64 + t % 64) * rw
+                want = cache[rows[:, None] + np.arange(rw)[None, :]]
+                assert np.array_equal(got, want), (which, h)
+            z = c.read_kv(0, which, 1, 0, T_past, T_past + 1)
+            assert z[0, D // 4] == 0 and not z[0, :8].any()
+    finally:
+        c.close()
+
+
+def test_attend_vs_oracle(gpu):
+    """qk_scores_gqa + causal_softmax + attn_av_gqa (web/model/kernels.js:
+    1140-1310) over random int8 pages: decode rows, a causal verify run, and a
+    ragged last page. The GPU softmax is online (max, sum merged per page and
+    chunk); equal to the exact three-pass one within 2e-5 of max |out|."""
+    from oracle import lib as L
+    from oracle import model as Mo
+    for base, tokens, n in [(configs.SMOLLM2, 130, 1), (configs.M27B, 700, 1), (configs.M27B, 300, 8),
+                            (configs.SMOLLM2, 64, 37)]:
+        d = configs.with_layers(base, 1)
+        c = _ctx(gpu, d, n_max=1024, t_max=64, slots=2)
+        try:
+            om = Mo.Model(d, n_slots=2, max_pages=16)
+            c.fill_random_kv(1, tokens + n, 11, 3)
+            om.fill_random_kv(1, tokens + n, 11, 3)
+            D, nH = d["head_dim"], d["n_heads"]
+            rng = np.random.default_rng(tokens + n)
+            q = rng.standard_normal((n, nH * D)).astype(np.float32)
+            got = c.op_attend(0, 1, q, tokens)
+            # oracle: RoPE on Q, scores, exact softmax, P.V over the same rows
+            pages = om.frames[1]["pages"]
+            Qh = np.ascontiguousarray(q.reshape(n, nH, D).transpose(1, 0, 2))
+            L.rope(Qh, D, tokens, om.tbl)
+            group = nH // d["n_kv_heads"]
+            s = L.qk_scores(Qh, om.K[0], n, tokens + n, 64, D, nH, group, pages)
+            p = L.causal_softmax(s, tokens)
+            ctxh = L.attn_av(p, om.V[0], D, 64, group, pages)
+            want = ctxh.transpose(1, 0, 2).reshape(n, nH * D)
+            err = np.abs(got - want).max()
+            assert err <= 2e-5 * max(1.0, np.abs(want).max()), (base["hidden"], tokens, n, err)
+        finally:
+            c.close()

@@ -1,0 +1,256 @@
+"""Pass-level parity: cc_step (Runner.#pass, web/model/stage.js:1314-1481)
+against the oracle's restatement of the same pass, on identical seeded
+weights and KV (both sides use the shared counter-based generator).
+
+Bars: greedy ids identical (with the top-1/top-2
+margin reported for the near-tie case); logits within 1e-2 abs; the f16
+residual within 2 f16 ulp; packing, page indices and batch invariance
+bit-exact."""
+import numpy as np
+import pytest
+
+from chattorrent_amd import configs
+
+pytestmark = pytest.mark.gpu
+
+SEED = 7
+
+
+def _setup(gpu, d, contexts, n_max=1024, t_max=64, extra_slots=1):
+    from chattorrent_amd.ccdecode import Context
+    from oracle import model as Mo
+    slots = len(contexts) + extra_slots
+    c = Context(d, n_max=n_max, t_max=t_max, slots=slots)
+    c.fill_random(SEED)
+    om = Mo.Model(d, n_slots=slots, max_pages=-(-n_max // 64))
+    om.gen_weights(SEED)
+    for s, T in enumerate(contexts):
+        if T:
+            c.fill_random_kv(s, T, SEED, s + 1)
+            om.fill_random_kv(s, T, SEED, s + 1)
+    return c, om
+
+
+def _ids(n, vocab, salt):
+    from oracle import lib as L
+    return L.gen_ids(SEED, 0x1D5 + salt, n, vocab)
+
+
+def _f16_ulp_diff(a_bits, b_bits):
+    """Distance in f16 steps between two arrays of half bits (same sign run)."""
+    def key(h):
+        h = h.astype(np.int32)
+        return np.where(h & 0x8000, -(h & 0x7fff), h & 0x7fff)
+    return np.abs(key(a_bits) - key(b_bits))
+
+
+def _check_head(d, got_vals, got_ids, want, tol=1e-2):
+    """got_*: [rows, M]; want: oracle output rows (logits [rows, V])."""
+    logits = np.concatenate([w["logits"] for w in want])
+    margins = []
+    for r in range(logits.shape[0]):
+        row = logits[r]
+        order = np.argsort(-row, kind="stable")
+        margins.append(float(row[order[0]] - row[order[1]]))
+        if margins[-1] > 1e-3:
+            assert got_ids[r, 0] == order[0], (r, got_ids[r, 0], order[0], margins[-1])
+        err = np.abs(got_vals[r] - row[got_ids[r]]).max()
+        assert err <= tol, (r, err)
+    return margins
+
+
+@pytest.fixture(scope="module")
+def smol(gpu):
+    d = configs.with_layers(configs.SMOLLM2, 3)
+    c, om = _setup(gpu, d, [17, 130, 511, 200])
+    yield d, c, om
+    c.close()
+
+
+def test_decode_step_matches_oracle(smol):
+    d, c, om = smol
+    jobs = [dict(slot=s, past=T, n=1, ids=_ids(1, d["vocab"], s), sampled=1, topk=16)
+            for s, T in enumerate([17, 130, 511, 200])]
+    vals, ids = c.step(jobs, topk=16)
+    want = om.pass_(jobs)
+    _check_head(d, vals, ids, want)
+    # The new K/V rows: the same codes except where the f32 input differs by
+    # an ulp and a value sits on a rounding boundary (then by one code).
+    D, nKV = d["head_dim"], d["n_kv_heads"]
+    same = total = 0
+    for layer in range(d["n_layer"]):
+        for which in (0, 1):
+            for j in jobs:
+                for h in range(nKV):
+                    g = c.read_kv(layer, which, j["slot"], h, j["past"], j["past"] + 1)
+                    w = om.kv_rows(layer, which, j["slot"], j["past"], j["past"] + 1, h)
+                    gc = g[:, :D // 4].view(np.int8).astype(np.int32)
+                    wc = w[:, :D // 4].view(np.int8).astype(np.int32)
+                    assert np.abs(gc - wc).max() <= 1
+                    gs, ws = g[:, D // 4:].view(np.float32), w[:, D // 4:].view(np.float32)
+                    assert np.allclose(gs, ws, rtol=1e-4, atol=0)
+                    same += int((gc == wc).sum())
+                    total += gc.size
+    assert same / total > 0.99
+
+
+def test_hidden_rows_within_two_f16_ulp(smol):
+    """A pass that stops before the head hands on f16 rows (stage.js:1553-1560):
+    within 2 f16 ulp of the oracle's after each block (checked after the last)."""
+    d, c, om = smol
+    from oracle import lib as L
+    jobs = [dict(slot=s, past=T, n=1, ids=_ids(1, d["vocab"], 10 + s), sampled=0)
+            for s, T in enumerate([17, 130, 511, 200])]
+    got = c.step(jobs, at=0, to=d["n_layer"] + 1)
+    want = om.pass_(jobs, head=False)
+    wb = L.to_f16(np.concatenate([w["hidden"] for w in want]))
+    diff = _f16_ulp_diff(got, wb)
+    assert diff.max() <= 2 * d["n_layer"], diff.max()
+    assert (diff <= 2).mean() > 0.999
+
+
+def test_batched_equals_alone_bitwise(smol):
+    """web/dev/batch.test.js: a batched pass gives each session the bits it
+    gets alone (rows packed in order, every projection row-invariant)."""
+    d, c, om = smol
+    jobs = [dict(slot=s, past=T, n=n, ids=_ids(n, d["vocab"], 20 + s), sampled=n)
+            for s, (T, n) in enumerate([(17, 1), (130, 4), (511, 1), (200, 8)])]
+    vals, ids = c.step(jobs, topk=8)
+    at = 0
+    for j in jobs:
+        v1, i1 = c.step([j], topk=8)
+        n = j["n"]
+        assert np.array_equal(i1, ids[at:at + n])
+        assert np.array_equal(v1.view(np.uint32), vals[at:at + n].view(np.uint32))
+        at += n
+
+
+def test_verify_rows_equal_one_row_jobs(smol):
+    """docs/model.md 'Matching plain decoding row by row': row i of an 8-row
+    verify gives the bits of a one-row job at past + i."""
+    d, c, om = smol
+    P = 300                                   # slot 4: the spare frame, rows below P never written
+    ids8 = _ids(8, d["vocab"], 40)
+    vals, ids = c.step([dict(slot=4, past=P, n=8, ids=ids8, sampled=8)], topk=4)
+    for i in range(8):
+        v1, i1 = c.step([dict(slot=4, past=P + i, n=1, ids=ids8[i:i + 1], sampled=1)], topk=4)
+        assert np.array_equal(i1[0], ids[i]) and np.array_equal(v1[0].view(np.uint32), vals[i].view(np.uint32))
+
+
+def test_deterministic(smol):
+    d, c, om = smol
+    jobs = [dict(slot=s, past=T, n=1, ids=_ids(1, d["vocab"], 50 + s), sampled=1)
+            for s, T in enumerate([17, 130, 511, 200])]
+    a = c.step(jobs, topk=8)
+    b = c.step(jobs, topk=8)
+    assert np.array_equal(a[0].view(np.uint32), b[0].view(np.uint32)) and np.array_equal(a[1], b[1])
+
+
+def test_prefill_and_verify_match_oracle(gpu):
+    """Causal rows inside a job: a prefill chunk from position 0 and a verify
+    run on top of a random cache, sampled at every row."""
+    d = configs.with_layers(configs.SMOLLM2, 2)
+    c, om = _setup(gpu, d, [0, 100])
+    try:
+        jobs = [dict(slot=0, past=0, n=37, ids=_ids(37, d["vocab"], 60), sampled=37),
+                dict(slot=1, past=100, n=8, ids=_ids(8, d["vocab"], 61), sampled=8)]
+        vals, ids = c.step(jobs, topk=4)
+        want = om.pass_(jobs)
+        _check_head(d, vals, ids, want)
+    finally:
+        c.close()
+
+
+def test_block27b_step_matches_oracle(gpu):
+    """One 27B-class block (d 5120, 40/8 heads, D 128, FFN 17408), decode rows
+    over ragged contexts, vocab kept full: the head checks the 151936-wide LM
+    head too."""
+    d = configs.with_layers(configs.M27B, 1)
+    ctxs = [256, 1000, 3000]
+    c, om = _setup(gpu, d, ctxs, n_max=4096, t_max=16)
+    try:
+        jobs = [dict(slot=s, past=T, n=1, ids=_ids(1, d["vocab"], 70 + s), sampled=1, topk=8)
+                for s, T in enumerate(ctxs)]
+        vals, ids = c.step(jobs, topk=8)
+        want = om.pass_(jobs)
+        _check_head(d, vals, ids, want)
+    finally:
+        c.close()
+
+
+def test_page_allocation_replays_ensure_pages(gpu):
+    """web/model/model.js:132-211: lowest index first, pages taken in job order
+    and logical order, released last-first — the device table equals the
+    oracle pool's replay of the same calls."""
+    from chattorrent_amd.ccdecode import Context
+    from oracle.model import PagePool
+    d = configs.with_layers(configs.SMOLLM2, 1)
+    c = Context(d, n_max=512, t_max=16, slots=2, sessions=5, max_jobs=5)
+    pool = PagePool(2 * 8)
+    frames = [{"pages": np.zeros(8, np.uint32), "owned": [], "max_pages": 8} for _ in range(5)]
+    try:
+        c.fill_random(SEED)
+
+        def fill(slot, tokens):
+            c.fill_random_kv(slot, tokens, SEED, slot + 1)
+            assert pool.ensure(frames[slot], tokens)
+
+        def check():
+            for s in range(5):
+                assert list(c.pages(s)) == frames[s]["owned"], s
+            assert c.free_pages() == len(pool.free)
+
+        fill(0, 70)
+        fill(1, 129)
+        fill(2, 5)
+        check()
+        c.release(1)
+        pool.release(frames[1])
+        check()
+        jobs = [dict(slot=2, past=5, n=1, ids=[3], sampled=1), dict(slot=3, past=0, n=16, ids=np.arange(16), sampled=1),
+                dict(slot=0, past=127, n=2, ids=[1, 2], sampled=1)]
+        c.step(jobs, topk=1)
+        for j in jobs:
+            assert pool.ensure(frames[j["slot"]], j["past"] + j["n"])
+        check()
+    finally:
+        c.close()
+
+
+def test_error_classes(gpu):
+    """#prepare's refusals (web/model/stage.js:1225-1259) and the capacity
+    errors (:930-941 busy, :1114-1117 pool too small), per job, before any
+    device work."""
+    from chattorrent_amd.ccdecode import Context, CCError, CC_EARG, CC_BUSY, CC_EPOOL
+    d = configs.with_layers(configs.SMOLLM2, 1)
+    c = Context(d, n_max=256, t_max=16, slots=1, sessions=3, max_jobs=3)
+    try:
+        c.fill_random(SEED)
+        with pytest.raises(CCError) as e:
+            c.step([dict(slot=0, past=0, n=1, ids=[d["vocab"]], sampled=1)])
+        assert e.value.status == CC_EARG and e.value.statuses[0] == CC_EARG
+        with pytest.raises(CCError) as e:
+            c.step([dict(slot=0, past=250, n=8, ids=np.zeros(8), sampled=1)])
+        assert e.value.status == CC_EARG and "exceeds" in str(e.value)
+        with pytest.raises(CCError) as e:
+            c.step([dict(slot=0, past=0, n=17, ids=np.zeros(17), sampled=1)])
+        assert e.value.status == CC_EARG
+        with pytest.raises(CCError) as e:
+            c.step([dict(slot=1, past=0, n=1, ids=[1], sampled=1), dict(slot=1, past=1, n=1, ids=[1], sampled=1)])
+        assert e.value.status == CC_EARG
+        c.fill_random_kv(0, 256, SEED, 1)            # the whole pool (1 slot = 4 pages)
+        with pytest.raises(CCError) as e:
+            c.step([dict(slot=1, past=0, n=1, ids=[1], sampled=1)])
+        assert e.value.status == CC_BUSY
+        c.release(0)
+        out = c.step([dict(slot=1, past=0, n=1, ids=[1], sampled=1)])
+        assert out[1].shape == (1, 1)
+    finally:
+        c.close()
+    c = Context(d, n_max=128, t_max=16, slots=1, sessions=1)
+    try:
+        with pytest.raises(CCError) as e:
+            c.fill_random_kv(0, 200, SEED, 1)
+        assert e.value.status == CC_EARG
+    finally:
+        c.close()
