@@ -20,7 +20,7 @@ EXPORTS = [
     "cc_create", "cc_destroy", "cc_last_error", "cc_upload", "cc_fill_random", "cc_step", "cc_release",
     "cc_slot_pages", "cc_free_pages", "cc_fill_random_kv", "cc_read_kv", "cc_write_kv", "cc_read_pages",
     "cc_stats_get", "cc_op_matmul_q8", "cc_op_store_kv", "cc_op_round_f16", "cc_op_topk", "cc_op_rmsnorm",
-    "cc_op_attend", "cc_profile", "cc_profile_read",
+    "cc_op_attend", "cc_profile", "cc_profile_read", "cc_read_logits",
 ]
 
 
@@ -83,6 +83,7 @@ def load():
         "cc_op_topk": (i32, [P, P, i32, i32, i32, P, P]),
         "cc_op_rmsnorm": (i32, [P, P, P, i32, i32, P]),
         "cc_op_attend": (i32, [P, i32, i32, P, i32, i32, P]),
+        "cc_read_logits": (i32, [P, i32, P]),
         "cc_profile": (i32, [P, i32]),
         "cc_profile_read": (i32, [P, i32, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
     }
@@ -187,6 +188,11 @@ class Context:
         out = np.empty(max(n, 1), np.uint32)
         self._chk(self.lib.cc_read_pages(self.h, slot, _p(out), n))
         return out[:n]
+
+    def read_logits(self, rows):
+        out = np.empty((rows, self.d["vocab"]), np.float32)
+        self._chk(self.lib.cc_read_logits(self.h, rows, _p(out)))
+        return out
 
     def free_pages(self):
         return self.lib.cc_free_pages(self.h)

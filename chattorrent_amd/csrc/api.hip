@@ -110,12 +110,15 @@ cc_status fail(cc_ctx* c, cc_status s, const std::string& msg) {
                         std::string(#expr) + ": " + hipGetErrorString(e_));                        \
     } while (0)
 
+// Device allocations are zeroed on the context's own stream: it is a
+// non-blocking stream, so work on the null stream would not be ordered
+// against the fills and copies that follow.
 template <class T>
 hipError_t dalloc(cc_ctx* ctx, T** p, size_t bytes, uint64_t* acct) {
     void* v = nullptr;
     hipError_t e = hipMalloc(&v, bytes ? bytes : 16);
     if (e != hipSuccess) return e;
-    e = hipMemset(v, 0, bytes ? bytes : 16);
+    e = hipMemsetAsync(v, 0, bytes ? bytes : 16, ctx->stream);
     if (e != hipSuccess) return e;
     ctx->allocs.push_back(v);
     if (acct) *acct += bytes;
@@ -331,7 +334,8 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
             // Lowest index pops first (model.js:145-146): stack[i] = n_pages-1-i.
             std::vector<uint32_t> fs(ctx->n_pages);
             for (int i = 0; i < ctx->n_pages; i++) fs[i] = (uint32_t)(ctx->n_pages - 1 - i);
-            HIPCHK(hipMemcpy(ctx->free_stack, fs.data(), fs.size() * 4, hipMemcpyHostToDevice));
+            HIPCHK(hipMemcpyAsync(ctx->free_stack, fs.data(), fs.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+            HIPCHK(hipStreamSynchronize(ctx->stream));
             ctx->top = ctx->n_pages;
         }
         const size_t pool_bytes = (size_t)ctx->n_pages * nKV * ctx->geom.blk;
@@ -360,7 +364,8 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
             std::vector<float> t;
             build_rope_table(ctx, t);
             HIPCHK(dalloc(ctx, &ctx->tbl, t.size() * 4, &ctx->scratch_bytes));
-            HIPCHK(hipMemcpy(ctx->tbl, t.data(), t.size() * 4, hipMemcpyHostToDevice));
+            HIPCHK(hipMemcpyAsync(ctx->tbl, t.data(), t.size() * 4, hipMemcpyHostToDevice, ctx->stream));
+            HIPCHK(hipStreamSynchronize(ctx->stream));
         }
         // Scratch for t_max rows.
         const int T = o.t_max;
@@ -445,7 +450,8 @@ cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data
         }
         if (!dst) return fail(ctx, CC_EARG, "tensor not held here");
         if (n != (size_t)d.hidden) return fail(ctx, CC_EARG, "a norm weight has `hidden` f32 values");
-        HIPCHK(hipMemcpy(dst, data, n * 4, hipMemcpyHostToDevice));
+        HIPCHK(hipMemcpyAsync(dst, data, n * 4, hipMemcpyHostToDevice, ctx->stream));
+        HIPCHK(hipStreamSynchronize(ctx->stream));
         return CC_OK;
     }
     int row_tile0 = 0, N = 0, K = 0;
@@ -605,6 +611,32 @@ cc_status cc_read_pages(cc_ctx* ctx, int32_t slot, uint32_t* out, int32_t n) {
         return fail(ctx, CC_EARG, "bad slot or count");
     HIPCHK(hipStreamSynchronize(ctx->stream));
     HIPCHK(hipMemcpy(out, ctx->page_table + (size_t)slot * ctx->max_pages, (size_t)n * 4, hipMemcpyDeviceToHost));
+    return CC_OK;
+}
+
+cc_status cc_debug_read(cc_ctx* ctx, int32_t which, size_t offset, size_t bytes, void* out) {
+    if (!ctx || !out) return CC_EARG;
+    const void* src = nullptr;
+    switch (which) {
+        case 0: src = ctx->x; break;
+        case 1: src = ctx->xp_h; break;
+        case 2: src = ctx->logits; break;
+        case 3: src = ctx->wte.codes; break;
+        case 4: src = ctx->wte.scales; break;
+        case 5: src = ctx->norm; break;
+        case 6: src = ctx->d_meta; break;
+        default: return fail(ctx, CC_EARG, "unknown buffer");
+    }
+    if (!src) return fail(ctx, CC_EARG, "buffer not allocated");
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    HIPCHK(hipMemcpy(out, (const uint8_t*)src + offset, bytes, hipMemcpyDeviceToHost));
+    return CC_OK;
+}
+
+cc_status cc_read_logits(cc_ctx* ctx, int32_t rows, float* out) {
+    if (!ctx || !out || !ctx->logits || rows < 1 || rows > ctx->o.t_max) return fail(ctx, CC_EARG, "no logits here");
+    HIPCHK(hipStreamSynchronize(ctx->stream));
+    HIPCHK(hipMemcpy(out, ctx->logits, (size_t)rows * ctx->d.vocab * 4, hipMemcpyDeviceToHost));
     return CC_OK;
 }
 
@@ -869,6 +901,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
     }
     HIPCHK(hipEventRecord(ctx->ev1, st));
     HIPCHK(hipStreamSynchronize(st));
+    HIPCHK(take_launch_error());
     float ms = 0;
     hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1);
     ctx->last_ms = ms;
@@ -900,7 +933,7 @@ cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K, con
     uint4* dXp = nullptr;
     HIPCHK(hipMalloc(&q.codes, (size_t)q.Nt * q.KU * 1024));
     HIPCHK(hipMalloc(&q.scales, (size_t)q.Nt * q.KU * 64));
-    HIPCHK(hipMemset(q.scales, 0, (size_t)q.Nt * q.KU * 64));
+    HIPCHK(hipMemsetAsync(q.scales, 0, (size_t)q.Nt * q.KU * 64, ctx->stream));
     HIPCHK(hipMalloc(&dW, (size_t)N * K));
     HIPCHK(hipMalloc(&dS, (size_t)N * ng * 2));
     HIPCHK(hipMalloc(&dX, (size_t)M * K * 4));

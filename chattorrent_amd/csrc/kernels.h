@@ -71,5 +71,6 @@ void launch_kv_from_ref(hipStream_t st, uint8_t* pool, const uint32_t* page_tabl
                         int head, int t0, int t1, const KVGeom& g, int which, const uint32_t* in);
 void launch_tile_q8(hipStream_t st, const int8_t* codes, const uint16_t* scales, int N, int K,
                     int group, const QTensor& w, int row_tile0);
+hipError_t take_launch_error();
 void launch_sum_splits(hipStream_t st, const float* part, int splits, int M, int N, float* out);
 void launch_to_half_bits(hipStream_t st, const float* x, int64_t n, uint16_t* out);

@@ -11,7 +11,19 @@
 #include "common.h"
 #include "kernels.h"
 
-#define CHECK_LAUNCH() (void)hipGetLastError()
+// The first launch error since the last take_launch_error(); cc_step and the
+// other entry points report it as CC_EDEVICE after their synchronisation.
+static hipError_t g_launch_error = hipSuccess;
+hipError_t take_launch_error() {
+    hipError_t e = g_launch_error;
+    g_launch_error = hipSuccess;
+    return e;
+}
+#define CHECK_LAUNCH()                                                       \
+    do {                                                                     \
+        hipError_t e_ = hipGetLastError();                                   \
+        if (e_ != hipSuccess && g_launch_error == hipSuccess) g_launch_error = e_; \
+    } while (0)
 
 // ===================================================================== GEMM ===
 // Y[M, N] = X[M, K] . W[N, K]^T for a tiled q8 W (kernels.h QTensor) and an
@@ -223,15 +235,17 @@ __global__ __launch_bounds__(256) void k_rmsnorm_prep(const float* __restrict__ 
     }
     const float tot = block_sum_256(ss, red);
     const float scale = 1.0f / sqrtf(tot / (float)H + eps);
+    if (y)
+        for (int h = threadIdx.x; h < H; h += 256) y[(size_t)m * H + h] = xr[h] * scale * w[h];
+    if (!Xp) return;
     for (int c = threadIdx.x; c < per; c += 256) {
         float v[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int k = 8 * c + j;
             v[j] = k < H ? xr[k] * scale * w[k] : 0.0f;
-            if (y && k < H) y[(size_t)m * H + k] = v[j];
         }
-        if (Xp) write_hilo(Xp, m, c, KU, v);
+        write_hilo(Xp, m, c, KU, v);
     }
 }
 

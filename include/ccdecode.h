@@ -144,6 +144,11 @@ cc_status cc_write_kv(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot, i
                       int32_t t0, int32_t t1, const uint32_t* rows);
 cc_status cc_read_pages(cc_ctx* ctx, int32_t slot, uint32_t* out, int32_t n);
 
+/* The last pass's full logits rows [rows, vocab] f32 (the sampled rows of a
+ * pass that reached the head), for parity checks: the reference reads back
+ * whole rows when a sampler needs them (web/model/stage.js:1428-1436). */
+cc_status cc_read_logits(cc_ctx* ctx, int32_t rows, float* out);
+
 /* Stats (Runner.counts / vramBytes, web/model/stage.js:219-259). */
 typedef struct cc_stats {
     uint64_t vram_bytes;

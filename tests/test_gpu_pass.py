@@ -44,11 +44,35 @@ def _f16_ulp_diff(a_bits, b_bits):
     return np.abs(key(a_bits) - key(b_bits))
 
 
-def _check_head(d, got_vals, got_ids, want, tol=1e-2):
-    """got_*: [rows, M]; want: oracle output rows (logits [rows, V])."""
+def _f16_ulp(v):
+    """The f16 step at |v| (2^-24 below the normal range)."""
+    e = np.floor(np.log2(np.maximum(np.abs(v.astype(np.float64)), 2.0 ** -14)))
+    return 2.0 ** (e - 10)
+
+
+def _ulps_at_scale(got_bits, want_bits, entry_bits):
+    """|got - want| in f16 steps at the scale of the values the block handles:
+    max(|want|, |entry|). A residual element that cancels to near zero inside
+    a block (entry -4e-3 -> out -9e-6) has an error set by the terms that
+    cancelled, not by the tiny result, so its step is the entry's."""
+    from oracle import lib as L
+    g, w, e = L.from_f16(got_bits), L.from_f16(want_bits), L.from_f16(entry_bits)
+    scale = np.maximum(np.abs(w), np.abs(e))
+    return np.abs(g.astype(np.float64) - w) / _f16_ulp(scale)
+
+
+def _check_head(d, got_vals, got_ids, want, ctx=None, tol=1e-2):
+    """got_*: [rows, M] candidates; want: oracle output rows. With `ctx`, the
+    whole logits rows are compared too (cc_read_logits). Greedy ids must be
+    equal unless the oracle's top-1/top-2 margin is below 1e-3 (reported)."""
     logits = np.concatenate([w["logits"] for w in want])
+    rows = logits.shape[0]
+    if ctx is not None:
+        full = ctx.read_logits(rows)
+        err = np.abs(full - logits).max()
+        assert err <= tol, err
     margins = []
-    for r in range(logits.shape[0]):
+    for r in range(rows):
         row = logits[r]
         order = np.argsort(-row, kind="stable")
         margins.append(float(row[order[0]] - row[order[1]]))
@@ -73,12 +97,13 @@ def test_decode_step_matches_oracle(smol):
             for s, T in enumerate([17, 130, 511, 200])]
     vals, ids = c.step(jobs, topk=16)
     want = om.pass_(jobs)
-    _check_head(d, vals, ids, want)
-    # The new K/V rows: the same codes except where the f32 input differs by
-    # an ulp and a value sits on a rounding boundary (then by one code).
+    _check_head(d, vals, ids, want, ctx=c)
+    # The new K/V rows of block 0, whose input both sides share bit for bit
+    # (the rounded embedding): the same codes except where the f32 K/V differ
+    # by an ulp and sit on a rounding boundary (then by one code).
     D, nKV = d["head_dim"], d["n_kv_heads"]
     same = total = 0
-    for layer in range(d["n_layer"]):
+    for layer in range(1):
         for which in (0, 1):
             for j in jobs:
                 for h in range(nKV):
@@ -88,25 +113,34 @@ def test_decode_step_matches_oracle(smol):
                     wc = w[:, :D // 4].view(np.int8).astype(np.int32)
                     assert np.abs(gc - wc).max() <= 1
                     gs, ws = g[:, D // 4:].view(np.float32), w[:, D // 4:].view(np.float32)
-                    assert np.allclose(gs, ws, rtol=1e-4, atol=0)
+                    assert np.allclose(gs, ws, rtol=1e-5, atol=0)
                     same += int((gc == wc).sum())
                     total += gc.size
     assert same / total > 0.99
 
 
-def test_hidden_rows_within_two_f16_ulp(smol):
-    """A pass that stops before the head hands on f16 rows (stage.js:1553-1560):
-    within 2 f16 ulp of the oracle's after each block (checked after the last)."""
+def test_hidden_rows_within_two_f16_ulp_per_block(smol):
+    """The f16 residual within 2 f16 ulp per block: each block run alone on
+    the GPU (a pass entering at position b+1 with the oracle's f16 rows, as a
+    downstream peer would, stage.js:1340-1346) against the oracle's rows after
+    that block; the exit rows are f16 (stage.js:1553-1560)."""
     d, c, om = smol
     from oracle import lib as L
-    jobs = [dict(slot=s, past=T, n=1, ids=_ids(1, d["vocab"], 10 + s), sampled=0)
-            for s, T in enumerate([17, 130, 511, 200])]
-    got = c.step(jobs, at=0, to=d["n_layer"] + 1)
-    want = om.pass_(jobs, head=False)
-    wb = L.to_f16(np.concatenate([w["hidden"] for w in want]))
-    diff = _f16_ulp_diff(got, wb)
-    assert diff.max() <= 2 * d["n_layer"], diff.max()
-    assert (diff <= 2).mean() > 0.999
+    pasts = [17, 130, 511, 200]
+    jobs = [dict(slot=s, past=T, n=1, ids=_ids(1, d["vocab"], 10 + s), sampled=0) for s, T in enumerate(pasts)]
+    after = []
+    om.pass_(jobs, head=False, capture=lambda layer, x: after.append(L.to_f16(x.copy())))
+    entry = c.step(jobs, at=0, to=1)                       # the rounded embedding rows
+    for b in range(d["n_layer"]):
+        hj = [dict(j, ids=None, hidden=entry[i:i + 1]) for i, j in enumerate(jobs)]
+        got = c.step(hj, at=b + 1, to=b + 2)
+        steps = _ulps_at_scale(got, after[b], entry)
+        assert steps.max() <= 2, (b, steps.max())
+        assert (_f16_ulp_diff(got, after[b]) <= 1).mean() > 0.99   # and nearly all within one step of themselves
+        entry = after[b]                                   # the next block gets the oracle's rows
+    # and the whole pass end to end stays close (errors compound through blocks)
+    full = c.step(jobs, at=0, to=d["n_layer"] + 1)
+    assert (_f16_ulp_diff(full, after[-1]) <= 2).mean() > 0.99
 
 
 def test_batched_equals_alone_bitwise(smol):
@@ -156,7 +190,7 @@ def test_prefill_and_verify_match_oracle(gpu):
                 dict(slot=1, past=100, n=8, ids=_ids(8, d["vocab"], 61), sampled=8)]
         vals, ids = c.step(jobs, topk=4)
         want = om.pass_(jobs)
-        _check_head(d, vals, ids, want)
+        _check_head(d, vals, ids, want, ctx=c)
     finally:
         c.close()
 
@@ -173,7 +207,7 @@ def test_block27b_step_matches_oracle(gpu):
                 for s, T in enumerate(ctxs)]
         vals, ids = c.step(jobs, topk=8)
         want = om.pass_(jobs)
-        _check_head(d, vals, ids, want)
+        _check_head(d, vals, ids, want, ctx=c)
     finally:
         c.close()
 
@@ -185,7 +219,7 @@ def test_page_allocation_replays_ensure_pages(gpu):
     from chattorrent_amd.ccdecode import Context
     from oracle.model import PagePool
     d = configs.with_layers(configs.SMOLLM2, 1)
-    c = Context(d, n_max=512, t_max=16, slots=2, sessions=5, max_jobs=5)
+    c = Context(d, n_max=512, t_max=32, slots=2, sessions=5, max_jobs=5)
     pool = PagePool(2 * 8)
     frames = [{"pages": np.zeros(8, np.uint32), "owned": [], "max_pages": 8} for _ in range(5)]
     try:
