@@ -64,6 +64,8 @@ struct cc_ctx {
     size_t qp_units = 0;
     float* apart = nullptr;
     size_t apart_floats = 0;
+    float* ssq = nullptr;          // rmsnorm partial sums [t_max][ceil(H/256)]
+    int ppw = 8;                   // pages per attention work item
     AttnItem* d_items = nullptr;
     size_t items_cap = 0;
     float* logits = nullptr;
@@ -197,28 +199,36 @@ cc_status check_dims(cc_ctx* ctx, const cc_dims& d, const cc_opts& o) {
 }
 
 struct StepPlan {
-    int T = 0, S = 0, nitems = 0;
+    int T = 0, S = 0, nitems = 0, ncwg = 0;
     std::vector<JobDev> jobs;
     std::vector<AttnItem> items;
-    std::vector<int32_t> row_job, plan, head_rows;
+    std::vector<int32_t> row_job, plan, head_rows, cwg;
     size_t qp_units = 0, apart_floats = 0;
     double kv_bytes = 0;   // K and V rows one layer's attention reads (reference row size)
 };
 
-// Per-step metadata: jobs, items, row_job, plan, head_rows, ids | hidden.
+// Per-step metadata: jobs, items, row_job, plan, head_rows, combine
+// workgroups (job, kv head, m-tile), ids | hidden.
 struct MetaLayout {
-    size_t jobs, items, row_job, plan, head_rows, ids, hidden, total;
+    size_t jobs, items, row_job, plan, head_rows, cwg, ids, hidden, total;
 };
 
-MetaLayout meta_layout(int max_jobs, size_t max_items, int t_max, int H) {
+// (job, kv head, m-tile) triples a pass can hold.
+size_t max_cwg_for(const cc_ctx* ctx) {
+    return (size_t)ctx->geom.nKV * (ceil_div(ctx->o.t_max * ctx->group, 16) + ctx->o.max_jobs);
+}
+
+MetaLayout meta_layout(const cc_ctx* ctx) {
+    const int max_jobs = ctx->o.max_jobs, t_max = ctx->o.t_max, H = ctx->d.hidden;
     MetaLayout m{};
     size_t at = 0;
     auto take = [&](size_t bytes) { size_t r = at; at += (bytes + 255) & ~(size_t)255; return r; };
     m.jobs = take(sizeof(JobDev) * max_jobs);
-    m.items = take(sizeof(AttnItem) * max_items);
+    m.items = take(sizeof(AttnItem) * ctx->items_cap);
     m.row_job = take(4 * (size_t)t_max);
     m.plan = take(16 * (size_t)max_jobs);
     m.head_rows = take(4 * (size_t)t_max);
+    m.cwg = take(12 * max_cwg_for(ctx));
     m.ids = take(4 * (size_t)t_max);
     m.hidden = take(2 * (size_t)t_max * H);
     m.total = at;
@@ -259,10 +269,10 @@ void prof_collect(cc_ctx* ctx) {
 
 double qbytes(const QTensor& q) { return (double)q.N * q.K * (1.0 + 2.0 / 32.0); }
 
+// Attention work items a pass can hold: every (kv head, m-tile) of every job
+// times the most chunks of `ppw` pages a frame has.
 size_t max_items_for(const cc_ctx* ctx) {
-    // Every chunk of 4 pages of every frame that could be in a pass.
-    const int jobs = std::min(ctx->o.max_jobs, ctx->o.sessions);
-    return (size_t)jobs * ctx->geom.nKV * ceil_div(ctx->max_pages, 4) + 16;
+    return max_cwg_for(ctx) * ceil_div(ctx->max_pages, ctx->ppw) + 16;
 }
 
 }  // namespace
@@ -386,13 +396,14 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         // Q operands: sum over jobs of nKV * ceil(n*group/16) * ng * 2 * 64 uint4.
         ctx->qp_units = (size_t)(ceil_div(T * ctx->group, 16) + o.max_jobs) * nKV * (D / 32) * 128;
         HIPCHK(dalloc(ctx, &ctx->qp, ctx->qp_units * 16, &ctx->scratch_bytes));
+        // Attention work items: `ppw` pages each, at most COMBINE_CMAX chunks a
+        // frame (the combine kernel's LDS).
+        ctx->ppw = std::max(8, ceil_div(ctx->max_pages, 512));
         ctx->items_cap = max_items_for(ctx);
-        // Attention partials: per item 16*mtq rows of (D + 2). Sized for the
-        // worst packing: every item at the largest m-tile count.
-        ctx->apart_floats = ctx->items_cap * (size_t)(ceil_div(T * ctx->group, 16) * 16) * (D + 2);
-        ctx->apart_floats = std::min(ctx->apart_floats, (size_t)ctx->items_cap * 16 * (D + 2) *
-                                                            (size_t)(ceil_div(T * ctx->group, 16) + 1));
+        // Attention partials: 16 rows of (D + 2) floats per item.
+        ctx->apart_floats = ctx->items_cap * 16 * (size_t)(D + 2);
         HIPCHK(dalloc(ctx, &ctx->apart, ctx->apart_floats * 4, &ctx->scratch_bytes));
+        HIPCHK(dalloc(ctx, &ctx->ssq, (size_t)T * ceil_div(H, 256) * 4, &ctx->scratch_bytes));
         if (ctx->head) {
             HIPCHK(dalloc(ctx, &ctx->logits, (size_t)T * d.vocab * 4, &ctx->scratch_bytes));
             const size_t keys = (size_t)T * ceil_div(d.vocab, 4096) * TOPK_MAX;
@@ -402,7 +413,7 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
             HIPCHK(dalloc(ctx, &ctx->d_ids, (size_t)T * TOPK_MAX * 4, &ctx->scratch_bytes));
         }
         HIPCHK(dalloc(ctx, &ctx->d_hbits, (size_t)T * H * 2, &ctx->scratch_bytes));
-        MetaLayout ml = meta_layout(o.max_jobs, ctx->items_cap, T, H);
+        MetaLayout ml = meta_layout(ctx);
         ctx->meta_bytes = ml.total;
         HIPCHK(dalloc(ctx, &ctx->d_meta, ml.total, &ctx->scratch_bytes));
         HIPCHK(hipHostMalloc((void**)&ctx->h_meta, ml.total, hipHostMallocDefault));
@@ -625,6 +636,8 @@ cc_status cc_debug_read(cc_ctx* ctx, int32_t which, size_t offset, size_t bytes,
         case 4: src = ctx->wte.scales; break;
         case 5: src = ctx->norm; break;
         case 6: src = ctx->d_meta; break;
+        case 7: src = ctx->apart; break;
+        case 8: src = ctx->qp; break;
         default: return fail(ctx, CC_EARG, "unknown buffer");
     }
     if (!src) return fail(ctx, CC_EARG, "buffer not allocated");
@@ -676,6 +689,7 @@ static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, 
     p.items.clear();
     p.row_job.clear();
     p.head_rows.clear();
+    p.cwg.clear();
     const int ng = ctx->geom.ng;
     size_t qp = 0, ap = 0;
     int row = 0;
@@ -690,12 +704,19 @@ static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, 
         qp += (size_t)ctx->geom.nKV * jd.mtq * ng * 128;
         const int T_act = jd.past + jd.n;
         p.kv_bytes += 2.0 * T_act * ctx->geom.nKV * (ctx->D + 4.0 * ctx->geom.ng);
-        jd.nchunk = ceil_div(ceil_div(T_act, 64), 4);
+        // Work items: (kv head, m-tile, chunk of ppw pages), chunk fastest,
+        // so item0 + (kvh*mtq + mt)*nchunk + c.
+        jd.nchunk = ceil_div(ceil_div(T_act, 64), ctx->ppw);
         jd.item0 = (int32_t)p.items.size();
         for (int h = 0; h < ctx->geom.nKV; h++)
-            for (int c = 0; c < jd.nchunk; c++) {
-                p.items.push_back(AttnItem{j, h, c, (int32_t)ap});
-                ap += (size_t)jd.mtq * 16 * (ctx->D + 2);
+            for (int mt = 0; mt < jd.mtq; mt++) {
+                for (int c = 0; c < jd.nchunk; c++) {
+                    p.items.push_back(AttnItem{j, h, c, (int32_t)ap, mt});
+                    ap += (size_t)16 * (ctx->D + 2);
+                }
+                p.cwg.push_back(j);
+                p.cwg.push_back(h);
+                p.cwg.push_back(mt);
             }
         for (int i = 0; i < jd.n; i++) p.row_job.push_back(j);
         if (head)
@@ -705,6 +726,7 @@ static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, 
     p.T = row;
     p.S = (int)p.head_rows.size();
     p.nitems = (int)p.items.size();
+    p.ncwg = (int)p.cwg.size() / 3;
     p.qp_units = qp;
     p.apart_floats = ap;
 }
@@ -739,10 +761,12 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
     const JobDev* djobs = (const JobDev*)(ctx->d_meta + ml.jobs);
     const AttnItem* ditems = (const AttnItem*)(ctx->d_meta + ml.items);
     const int32_t* drow_job = (const int32_t*)(ctx->d_meta + ml.row_job);
+    const int32_t* dcwg = (const int32_t*)(ctx->d_meta + ml.cwg);
     for (int b = b0; b < b1; b++) {
         Layer& L = ctx->layers[b - ctx->L0];
         if (b == b0)
-            launch_rmsnorm_prep(st, ctx->x, nullptr, T, Mpad, H, L.qkv.KU, L.ln1, d.rms_eps, ctx->xp_h, nullptr);
+            launch_resid_norm(st, ctx->x, nullptr, nullptr, 0, T, Mpad, H, 0, L.ln1, d.rms_eps, L.qkv.KU, ctx->xp_h,
+                              nullptr, ctx->ssq);
         const int sq = splits_for(L.qkv, 4);
         int e = prof_begin(ctx);
         launch_gemm(st, L.qkv, ctx->xp_h, ctx->part, T, sq, 4);
@@ -750,16 +774,17 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
         launch_fin_qkv(st, ctx->part, sq, T, drow_job, djobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
                        L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 1);
         e = prof_begin(ctx);
-        launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
-                    ctx->apart);
+        launch_attn2(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
+                     ctx->ppw, ctx->apart);
         prof_end(ctx, e, CC_K_ATTN, p.kv_bytes);
-        launch_attn_combine(st, djobs, (int)p.jobs.size(), ditems, ctx->apart, ctx->geom, nH, ctx->group, T, Mpad,
-                            L.o.KU, ctx->xp_o, nullptr);
+        launch_attn_combine2(st, djobs, (int)p.jobs.size(), ditems, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU,
+                             ctx->xp_o, nullptr, dcwg, p.ncwg);
         const int so = splits_for(L.o, 4);
         e = prof_begin(ctx);
         launch_gemm(st, L.o, ctx->xp_o, ctx->part, T, so, 4);
         prof_end(ctx, e, CC_K_O, qbytes(L.o));
-        launch_fin_residual(st, ctx->x, ctx->part, so, T, H, 0, L.ln2, d.rms_eps, L.gu.KU, ctx->xp_h, Mpad);
+        launch_resid_norm(st, ctx->x, nullptr, ctx->part, so, T, Mpad, H, 0, L.ln2, d.rms_eps, L.gu.KU, ctx->xp_h,
+                          nullptr, ctx->ssq);
         const int sg = splits_for(L.gu, 4);
         e = prof_begin(ctx);
         launch_gemm(st, L.gu, ctx->xp_h, ctx->part, T, sg, 4);
@@ -770,9 +795,10 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
         launch_gemm(st, L.down, ctx->xp_f, ctx->part, T, sd, 4);
         prof_end(ctx, e, CC_K_DOWN, qbytes(L.down));
         const bool next = b + 1 < b1;
-        launch_fin_residual(st, ctx->x, ctx->part, sd, T, H, 1, next ? ctx->layers[b + 1 - ctx->L0].ln1 : nullptr,
-                            d.rms_eps, next ? ctx->layers[b + 1 - ctx->L0].qkv.KU : 0, next ? ctx->xp_h : nullptr,
-                            Mpad);
+        launch_resid_norm(st, ctx->x, nullptr, ctx->part, sd, T, Mpad, H, 1,
+                          next ? ctx->layers[b + 1 - ctx->L0].ln1 : nullptr, d.rms_eps,
+                          next ? ctx->layers[b + 1 - ctx->L0].qkv.KU : 0, next ? ctx->xp_h : nullptr, nullptr,
+                          ctx->ssq);
     }
     (void)D;
 }
@@ -822,15 +848,17 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
 
     StepPlan p;
     build_plan(ctx, jobs, njobs, p, head);
-    if (p.nitems > (int)ctx->items_cap) return bad(-1, "too many attention items");
+    if (p.nitems > (int)ctx->items_cap || (size_t)p.ncwg > max_cwg_for(ctx))
+        return bad(-1, "too many attention items");
     cc_status gs = grow(ctx, p);
     if (gs != CC_OK) return gs;
-    MetaLayout ml = meta_layout(ctx->o.max_jobs, ctx->items_cap, ctx->o.t_max, d.hidden);
+    MetaLayout ml = meta_layout(ctx);
     uint8_t* hm = ctx->h_meta;
     std::memcpy(hm + ml.jobs, p.jobs.data(), p.jobs.size() * sizeof(JobDev));
     std::memcpy(hm + ml.items, p.items.data(), p.items.size() * sizeof(AttnItem));
     std::memcpy(hm + ml.row_job, p.row_job.data(), p.row_job.size() * 4);
     std::memcpy(hm + ml.head_rows, p.head_rows.data(), p.head_rows.size() * 4);
+    std::memcpy(hm + ml.cwg, p.cwg.data(), p.cwg.size() * 4);
     std::vector<std::pair<int, int>> want;
     for (int j = 0; j < njobs; j++) want.push_back({jobs[j].slot, jobs[j].past + jobs[j].n});
     {
@@ -886,8 +914,8 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         const QTensor& hw = d.tied ? ctx->wte : ctx->lm_head;
         const int S = p.S;
         const int Mpad = 32 * ceil_div(S, 32);
-        launch_rmsnorm_prep(st, ctx->x, (const int32_t*)(ctx->d_meta + ml.head_rows), S, Mpad, d.hidden, hw.KU,
-                            ctx->norm, d.rms_eps, ctx->xp_h, nullptr);
+        launch_resid_norm(st, ctx->x, (const int32_t*)(ctx->d_meta + ml.head_rows), nullptr, 0, S, Mpad, d.hidden, 0,
+                          ctx->norm, d.rms_eps, hw.KU, ctx->xp_h, nullptr, ctx->ssq);
         const int e = prof_begin(ctx);
         launch_gemm(st, hw, ctx->xp_h, ctx->logits, S, 1, 4);
         prof_end(ctx, e, CC_K_HEAD, qbytes(hw));
@@ -988,16 +1016,18 @@ cc_status cc_op_topk(cc_ctx* ctx, const float* logits, int32_t rows, int32_t V, 
 
 cc_status cc_op_rmsnorm(cc_ctx* ctx, const float* x, const float* w, int32_t T, int32_t H, float* y) {
     if (!ctx || !x || !w || !y || T < 1 || H < 1) return CC_EARG;
-    float *dx = nullptr, *dw = nullptr, *dy = nullptr;
+    float *dx = nullptr, *dw = nullptr, *dy = nullptr, *dss = nullptr;
     HIPCHK(hipMalloc(&dx, (size_t)T * H * 4));
     HIPCHK(hipMalloc(&dw, (size_t)H * 4));
     HIPCHK(hipMalloc(&dy, (size_t)T * H * 4));
+    HIPCHK(hipMalloc(&dss, (size_t)T * ceil_div(H, 256) * 4));
     HIPCHK(hipMemcpy(dx, x, (size_t)T * H * 4, hipMemcpyHostToDevice));
     HIPCHK(hipMemcpy(dw, w, (size_t)H * 4, hipMemcpyHostToDevice));
-    launch_rmsnorm_prep(ctx->stream, dx, nullptr, T, T, H, 0, dw, ctx->d.rms_eps, nullptr, dy);
+    launch_resid_norm(ctx->stream, dx, nullptr, nullptr, 0, T, T, H, 0, dw, ctx->d.rms_eps, 0, nullptr, dy, dss);
     HIPCHK(hipStreamSynchronize(ctx->stream));
+    HIPCHK(take_launch_error());
     HIPCHK(hipMemcpy(y, dy, (size_t)T * H * 4, hipMemcpyDeviceToHost));
-    for (void* v : {(void*)dx, (void*)dw, (void*)dy}) hipFree(v);
+    for (void* v : {(void*)dx, (void*)dw, (void*)dy, (void*)dss}) hipFree(v);
     return CC_OK;
 }
 
@@ -1015,11 +1045,12 @@ static cc_status one_job(cc_ctx* ctx, int32_t layer, int32_t slot, int32_t n, in
     build_plan(ctx, &j, 1, p, false);
     cc_status gs = grow(ctx, p);
     if (gs != CC_OK) return gs;
-    ml = meta_layout(ctx->o.max_jobs, ctx->items_cap, ctx->o.t_max, ctx->d.hidden);
+    ml = meta_layout(ctx);
     uint8_t* hm = ctx->h_meta;
     std::memcpy(hm + ml.jobs, p.jobs.data(), sizeof(JobDev));
     std::memcpy(hm + ml.items, p.items.data(), p.items.size() * sizeof(AttnItem));
     std::memcpy(hm + ml.row_job, p.row_job.data(), p.row_job.size() * 4);
+    std::memcpy(hm + ml.cwg, p.cwg.data(), p.cwg.size() * 4);
     int32_t* plan = (int32_t*)(hm + ml.plan);
     const int need = ceil_div(past + n, ctx->geom.page);
     plan[0] = slot; plan[1] = ctx->owned[slot]; plan[2] = std::max(0, need - ctx->owned[slot]); plan[3] = 0;
@@ -1099,9 +1130,12 @@ cc_status cc_op_attend(cc_ctx* ctx, int32_t layer, int32_t slot, const float* q,
     const AttnItem* di = (const AttnItem*)(ctx->d_meta + ml.items);
     launch_fin_qkv(st, dr, 1, n, (const int32_t*)(ctx->d_meta + ml.row_job), dj, d.n_heads, ctx->group, ctx->geom,
                    ctx->tbl, ctx->rot, L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 0);
-    launch_attn(st, di, p.nitems, dj, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->apart);
-    launch_attn_combine(st, dj, 1, di, ctx->apart, ctx->geom, d.n_heads, ctx->group, n, Mt * 16, KU, dXp, dctx);
+    launch_attn2(st, di, p.nitems, dj, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->ppw,
+                 ctx->apart);
+    launch_attn_combine2(st, dj, 1, di, ctx->apart, ctx->geom, d.n_heads, ctx->group, KU, dXp, dctx,
+                         (const int32_t*)(ctx->d_meta + ml.cwg), p.ncwg);
     HIPCHK(hipStreamSynchronize(st));
+    HIPCHK(take_launch_error());
     HIPCHK(hipMemcpy(out, dctx, (size_t)n * qd * 4, hipMemcpyDeviceToHost));
     for (void* v : {(void*)dr, (void*)dctx, (void*)dXp}) hipFree(v);
     return CC_OK;

@@ -24,6 +24,7 @@ struct JobDev {
 
 struct AttnItem {
     int32_t job, kvh, chunk, part; // part: float offset of the partial block
+    int32_t mt;                    // query m-tile (16 rows rho = i*group + gi)
 };
 
 struct KVGeom {
@@ -72,5 +73,14 @@ void launch_kv_from_ref(hipStream_t st, uint8_t* pool, const uint32_t* page_tabl
 void launch_tile_q8(hipStream_t st, const int8_t* codes, const uint16_t* scales, int N, int K,
                     int group, const QTensor& w, int row_tile0);
 hipError_t take_launch_error();
+void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const float* part, int splits, int M,
+                       int Mpad, int H, int round, const float* w, float eps, int KU, uint4* Xp, float* y,
+                       float* ssq);
+void launch_attn2(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
+                  const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
+                  int ppw, float* part);
+void launch_attn_combine2(hipStream_t st, const JobDev* jobs, int njobs, const AttnItem* items, const float* part,
+                          const KVGeom& g, int nH, int group, int KU, uint4* Xp, float* ctx_out,
+                          const int32_t* wg_job, int nwg);
 void launch_sum_splits(hipStream_t st, const float* part, int splits, int M, int N, float* out);
 void launch_to_half_bits(hipStream_t st, const float* x, int64_t n, uint16_t* out);

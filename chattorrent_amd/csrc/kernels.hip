@@ -306,6 +306,79 @@ void launch_fin_residual(hipStream_t st, float* x, const float* part, int splits
     CHECK_LAUNCH();
 }
 
+// The same residual step spread over the whole chip: grid (column blocks of
+// 256, rows). Each block adds the projection's K splits in order to its 256
+// residual values (add_inplace), optionally rounds them (round_f16), writes
+// them back and stores its partial sum of squares; k_norm_prep then finishes
+// rmsnorm from the partials. With part == nullptr it only computes the
+// partials of x (rows gathered through `rows`), for the first block's norm
+// and the head's.
+__global__ __launch_bounds__(256) void k_resid_ssq(float* __restrict__ x, const int32_t* __restrict__ rows,
+                                                   const float* __restrict__ part, int splits, int M, int H,
+                                                   int round, float* __restrict__ ssq) {
+    __shared__ float red[256];
+    const int m = blockIdx.y;
+    const int h = blockIdx.x * 256 + threadIdx.x;
+    float v = 0.0f;
+    if (h < H) {
+        if (part) {
+            float p = part[(size_t)m * H + h];
+            for (int s = 1; s < splits; s++) p = p + part[((size_t)s * M + m) * H + h];
+            v = x[(size_t)m * H + h] + p;
+            if (round) v = round_f16_value(v);
+            x[(size_t)m * H + h] = v;
+        } else {
+            v = x[(size_t)(rows ? rows[m] : m) * H + h];
+        }
+    }
+    const float t = block_sum_256(v * v, red);
+    if (threadIdx.x == 0) ssq[(size_t)m * gridDim.x + blockIdx.x] = t;
+}
+
+// rmsnorm's scale from the partial sums (added in block order) and the
+// operand prep: y = x * (1/sqrt(ss/H + eps)) * w as f16 hi/lo fragments.
+// Grid (chunk blocks, Mpad); rows m >= M are zero.
+__global__ __launch_bounds__(256) void k_norm_prep(const float* __restrict__ x, const int32_t* __restrict__ rows,
+                                                   const float* __restrict__ ssq, int nb, int M, int H, int KU,
+                                                   const float* __restrict__ w, float eps, uint4* __restrict__ Xp,
+                                                   float* __restrict__ y) {
+    const int m = blockIdx.y;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    const int per = 8 * KU;
+    if (Xp && c >= per) return;
+    if (!Xp && 8 * c >= H) return;
+    float v[8];
+    if (m >= M) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = 0.0f;
+    } else {
+        float tot = 0.0f;
+        for (int b = 0; b < nb; b++) tot = tot + ssq[(size_t)m * nb + b];
+        const float scale = 1.0f / sqrtf(tot / (float)H + eps);
+        const float* xr = x + (size_t)(rows ? rows[m] : m) * H;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int k = 8 * c + j;
+            v[j] = k < H ? xr[k] * scale * w[k] : 0.0f;
+            if (y && k < H) y[(size_t)m * H + k] = v[j];
+        }
+    }
+    if (Xp) write_hilo(Xp, m, c, KU, v);
+}
+
+void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const float* part, int splits, int M,
+                       int Mpad, int H, int round, const float* w, float eps, int KU, uint4* Xp, float* y,
+                       float* ssq) {
+    const int nb = (H + 255) / 256;
+    hipLaunchKernelGGL(k_resid_ssq, dim3(nb, M), dim3(256), 0, st, x, rows, part, splits, M, H, round, ssq);
+    CHECK_LAUNCH();
+    if (!w) return;
+    const int chunks = Xp ? 8 * KU : (H + 7) / 8;
+    hipLaunchKernelGGL(k_norm_prep, dim3((chunks + 255) / 256, Xp ? Mpad : M), dim3(256), 0, st, x, rows, ssq, nb,
+                       M, H, KU, w, eps, Xp, y);
+    CHECK_LAUNCH();
+}
+
 // SwiGLU (web/model/kernels.js:1513-1529 silu_mul): act = g * (1/(1+exp(-g)))
 // * up over the fused gate|up projection, straight into the down operand.
 __global__ void k_fin_swiglu(const float* __restrict__ part, int splits, int M, int Mpad, int F, int KU,
@@ -451,13 +524,108 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
     }
 }
 
+// The same finish spread over (row, head): one wave per head of a row, four
+// heads per workgroup. The head's D values (K splits summed in order) sit in
+// the wave's LDS slice; Q heads are RoPE'd into the attention operand, K heads
+// RoPE'd and quantised into the pool, V heads quantised — each with exactly
+// the arithmetic above.
+template <int D>
+__global__ __launch_bounds__(256) void k_fin_qkv2(const float* __restrict__ part, int splits, int M,
+                                                  const int32_t* __restrict__ row_job,
+                                                  const JobDev* __restrict__ jobs, int nH, int group, KVGeom g,
+                                                  const float* __restrict__ tbl, int rot, uint8_t* __restrict__ kpool,
+                                                  uint8_t* __restrict__ vpool,
+                                                  const uint32_t* __restrict__ page_table, uint4* __restrict__ Qp,
+                                                  int do_q, int do_kv) {
+    __shared__ float buf[4][D];
+    __shared__ float rq[4][D];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int m = blockIdx.y;
+    const int nKV = g.nKV;
+    const int nall = nH + 2 * nKV;
+    const int hidx = blockIdx.x * 4 + wave;
+    const bool live = hidx < nall;
+    const int N = nall * D;
+    if (live)
+        for (int d = lane; d < D; d += 64) {
+            const size_t e = (size_t)hidx * D + d;
+            float p = part[(size_t)m * N + e];
+            for (int s = 1; s < splits; s++) p = p + part[((size_t)s * M + m) * N + e];
+            buf[wave][d] = p;
+        }
+    __syncthreads();
+    const JobDev jb = jobs[row_job[m]];
+    const int i = m - jb.row0;
+    const int pos = jb.past + i;
+    if (live && hidx < nH) {
+        if (do_q) {
+            for (int d = lane; d < D; d += 64) rq[wave][d] = rope_at(buf[wave], d, rot, tbl, pos);
+        }
+    }
+    __syncthreads();
+    if (!live) return;
+    if (hidx < nH) {
+        if (!do_q) return;
+        if (lane < D / 8) {
+            const int d0 = 8 * lane;
+            half8_t hi, lo;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                _Float16 a, b;
+                split_hilo(rq[wave][d0 + j], a, b);
+                hi[j] = a;
+                lo[j] = b;
+            }
+            const int kvh = hidx / group, gi = hidx % group;
+            const int rho = i * group + gi;
+            const int mtq = rho >> 4, ln = (rho & 15) + 16 * ((d0 & 31) >> 3), grp = d0 >> 5;
+            const size_t at = (size_t)jb.qp_off + ((((size_t)kvh * jb.mtq + mtq) * g.ng + grp) * 2) * 64 + ln;
+            Qp[at] = __builtin_bit_cast(uint4, hi);
+            Qp[at + 64] = __builtin_bit_cast(uint4, lo);
+        }
+        return;
+    }
+    if (!do_kv) return;
+    const int which = hidx < nH + nKV ? 0 : 1;
+    const int n = hidx - nH - which * nKV;
+    const uint32_t page = page_table[(size_t)jb.slot * g.max_pages + pos / g.page];
+    const int s = pos % g.page;
+    uint8_t* blk = (which ? vpool : kpool) + ((size_t)page * nKV + n) * g.blk;
+#pragma unroll
+    for (int q0 = 0; q0 < D; q0 += 64) {
+        const int d = q0 + lane;
+        const float v = which ? buf[wave][d] : rope_at(buf[wave], d, rot, tbl, pos);
+        float amax = fabsf(v);
+        for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        const float scale = amax / 127.0f;
+        const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+        float q = __builtin_rintf(v * inv);
+        q = fminf(fmaxf(q, -127.0f), 127.0f);
+        const int8_t code = (int8_t)(int)q;
+        const int b = d >> 5;
+        if (which == 0) {
+            blk[(size_t)s * D + kpos(d, D)] = (uint8_t)code;
+            if ((d & 31) == 0) *(float*)(blk + 64 * D + ((size_t)s * g.ng + b) * 4) = scale;
+        } else {
+            blk[(size_t)d * 64 + vpos(s)] = (uint8_t)code;
+            if ((d & 31) == 0) *(float*)(blk + 64 * D + ((size_t)b * 64 + vpos(s)) * 4) = scale;
+        }
+    }
+}
+
 void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const int32_t* row_job,
                     const JobDev* jobs, int nH, int group, const KVGeom& g, const float* tbl, int rot,
                     uint8_t* kpool, uint8_t* vpool, const uint32_t* page_table, uint4* Qp, float* qkv_out,
                     int do_q, int do_kv) {
-    const int N = (nH + 2 * g.nKV) * g.D;
-    hipLaunchKernelGGL(k_fin_qkv, dim3(M), dim3(256), N * sizeof(float), st, part, splits, M, row_job, jobs,
-                       nH, group, g, tbl, rot, kpool, vpool, page_table, Qp, qkv_out, do_q, do_kv);
+    (void)qkv_out;
+    const int nall = nH + 2 * g.nKV;
+    dim3 grid((nall + 3) / 4, M);
+    if (g.D == 128)
+        hipLaunchKernelGGL(k_fin_qkv2<128>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
+                           rot, kpool, vpool, page_table, Qp, do_q, do_kv);
+    else
+        hipLaunchKernelGGL(k_fin_qkv2<64>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
+                           rot, kpool, vpool, page_table, Qp, do_q, do_kv);
     CHECK_LAUNCH();
 }
 
@@ -642,6 +810,279 @@ __global__ __launch_bounds__(256) void k_attn(const AttnItem* __restrict__ items
     }
 }
 
+// Attention, one wave per work item: (job, kv head, query m-tile, chunk of
+// `ppw` pages). The wave walks its pages in order with the next page's int8
+// K/V fragments already loading while it computes the current one, and keeps
+// an online softmax (running max, sum, rescaled O) across them; its
+// (max, sum, O) partial for the 16 query rows goes to `part` (16 x (D + 2)
+// floats). Per page, the arithmetic is k_attn's: S^T = K . Q^T (hi/lo) scaled
+// per (token, 32-block), masked (token < T_act, token <= past + i) and scaled
+// by 1/sqrt(D); O^T += V^T . (p * sv) (hi/lo).
+template <int NG>
+__global__ __launch_bounds__(256) void k_attn2(const AttnItem* __restrict__ items, int nitems,
+                                               const JobDev* __restrict__ jobs, const uint4* __restrict__ Qp,
+                                               const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
+                                               const uint32_t* __restrict__ page_table, KVGeom g, int group, int ppw,
+                                               float* __restrict__ part) {
+    constexpr int D = 32 * NG;
+    constexpr int DT = D / 16;
+    const int lane = threadIdx.x & 63, j4 = lane >> 4, l16 = lane & 15;
+    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= nitems) return;   // no barriers below: a finished wave may leave
+    const AttnItem it = items[wid];
+    const JobDev jb = jobs[it.job];
+    const int T_act = jb.past + jb.n;
+    const int R = jb.n * group;
+    const int npg = (T_act + 63) >> 6;
+    const int p0 = it.chunk * ppw;
+    const int p1 = min(npg, p0 + ppw);
+    const int mtq = it.mt;
+    const float inv_sqrt_d = 1.0f / sqrtf((float)D);
+
+    uint4 qh[NG], ql[NG];
+    {
+        const size_t qb = (size_t)jb.qp_off + (((size_t)it.kvh * jb.mtq + mtq) * NG) * 128 + lane;
+#pragma unroll
+        for (int gg = 0; gg < NG; gg++) {
+            qh[gg] = Qp[qb + (size_t)gg * 128];
+            ql[gg] = Qp[qb + (size_t)gg * 128 + 64];
+        }
+    }
+    const int rho = mtq * 16 + l16;
+    const int lim = rho < R ? jb.past + rho / group : -1;   // last visible token of this row
+    const uint32_t* pt = page_table + (size_t)jb.slot * g.max_pages;
+    const size_t hoff = (size_t)it.kvh * g.blk;
+    const size_t pstride = (size_t)g.nKV * g.blk;
+
+    float mrow = -INFINITY, lsum = 0.0f;
+    float4_t o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    uint4 kc[4][NG / 2], vc[DT];
+    if (p0 < p1) {
+        const uint8_t* kb = kpool + (size_t)pt[p0] * pstride + hoff;
+        const uint8_t* vb = vpool + (size_t)pt[p0] * pstride + hoff;
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int q = 0; q < NG / 2; q++)
+                kc[tt][q] = *(const uint4*)(kb + (size_t)(tt * 16 + l16) * D + (D / 4) * j4 + 16 * q);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) vc[dt] = *(const uint4*)(vb + (size_t)(dt * 16 + l16) * 64 + 16 * j4);
+    }
+    for (int p = p0; p < p1; p++) {
+        const uint8_t* kb = kpool + (size_t)pt[p] * pstride + hoff;
+        const uint8_t* vb = vpool + (size_t)pt[p] * pstride + hoff;
+        uint4 kn[4][NG / 2], vn[DT];
+        if (p + 1 < p1) {
+            const uint8_t* kb2 = kpool + (size_t)pt[p + 1] * pstride + hoff;
+            const uint8_t* vb2 = vpool + (size_t)pt[p + 1] * pstride + hoff;
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                for (int q = 0; q < NG / 2; q++)
+                    kn[tt][q] = *(const uint4*)(kb2 + (size_t)(tt * 16 + l16) * D + (D / 4) * j4 + 16 * q);
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) vn[dt] = *(const uint4*)(vb2 + (size_t)(dt * 16 + l16) * 64 + 16 * j4);
+        }
+        float pr[4][4];
+        float pm = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) {
+            float ks[4 * NG];
+#pragma unroll
+            for (int q = 0; q < NG; q++) {
+                const float4 f = *(const float4*)(kb + 64 * D + ((size_t)(tt * 16 + 4 * j4) * NG) * 4 + 16 * q);
+                ks[4 * q] = f.x; ks[4 * q + 1] = f.y; ks[4 * q + 2] = f.z; ks[4 * q + 3] = f.w;
+            }
+            float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int gg = 0; gg < NG; gg++) {
+                const uint4 c = kc[tt][gg >> 1];
+                const half8_t kf = (gg & 1) ? dequant8_signed(c.z, c.w) : dequant8_signed(c.x, c.y);
+                float4_t pp = {0.f, 0.f, 0.f, 0.f};
+                pp = mfma16x16x32(kf, __builtin_bit_cast(half8_t, qh[gg]), pp);
+                pp = mfma16x16x32(kf, __builtin_bit_cast(half8_t, ql[gg]), pp);
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(ks[r * NG + gg], pp[r], acc[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int tok = p * 64 + tt * 16 + 4 * j4 + r;
+                const bool ok = tok < T_act && tok <= lim;
+                pr[tt][r] = ok ? acc[r] * inv_sqrt_d : -INFINITY;
+                pm = fmaxf(pm, pr[tt][r]);
+            }
+        }
+        pm = fmaxf(pm, __shfl_xor(pm, 16));
+        pm = fmaxf(pm, __shfl_xor(pm, 32));
+        const float mnew = fmaxf(mrow, pm);
+        // No branch on the row's state here: a row that is still fully masked
+        // (mnew = -inf) takes alpha = 0 and p = 0 through the same code. MFMA
+        // reads every lane's operands whatever the execution mask, so lanes
+        // must not skip building their fragments.
+        {
+            const float alpha = mrow == -INFINITY ? 0.0f : expf(mrow - mnew);
+            lsum *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) o[dt][r] *= alpha;
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float e = pr[tt][r] == -INFINITY ? 0.0f : expf(pr[tt][r] - mnew);
+                    pr[tt][r] = e;
+                    lsum += e;
+                }
+#pragma unroll
+            for (int b = 0; b < NG; b++) {
+                float sv[16];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const float4 f = *(const float4*)(vb + 64 * D + ((size_t)b * 64 + 16 * j4) * 4 + 16 * q);
+                    sv[4 * q] = f.x; sv[4 * q + 1] = f.y; sv[4 * q + 2] = f.z; sv[4 * q + 3] = f.w;
+                }
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) {
+                    half8_t ph, pl;
+#pragma unroll
+                    for (int ii = 0; ii < 8; ii++) {
+                        const int tt = 2 * ks + (ii >> 2), r = ii & 3;
+                        const float pv = pr[tt][r] == 0.0f ? 0.0f : pr[tt][r] * sv[4 * tt + r];
+                        _Float16 a, c;
+                        split_hilo(pv, a, c);
+                        ph[ii] = a;
+                        pl[ii] = c;
+                    }
+#pragma unroll
+                    for (int dd = 0; dd < 2; dd++) {
+                        const int dt = 2 * b + dd;
+                        const uint4 c = vc[dt];
+                        const half8_t vf = ks ? dequant8_signed(c.z, c.w) : dequant8_signed(c.x, c.y);
+                        o[dt] = mfma16x16x32(vf, ph, o[dt]);
+                        o[dt] = mfma16x16x32(vf, pl, o[dt]);
+                    }
+                }
+            }
+            mrow = mnew;
+        }
+        if (p + 1 < p1) {
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                for (int q = 0; q < NG / 2; q++) kc[tt][q] = kn[tt][q];
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) vc[dt] = vn[dt];
+        }
+    }
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    float* dst = part + it.part + (size_t)l16 * (D + 2);
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) dst[2 + dt * 16 + 4 * j4 + r] = o[dt][r];
+    if (j4 == 0) {
+        dst[0] = mrow;
+        dst[1] = lsum;
+    }
+}
+
+void launch_attn2(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
+                  const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
+                  int ppw, float* part) {
+    if (nitems <= 0) return;
+    const int blocks = (nitems + 3) / 4;
+    if (g.ng == 4)
+        hipLaunchKernelGGL((k_attn2<4>), dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool,
+                           page_table, g, group, ppw, part);
+    else
+        hipLaunchKernelGGL((k_attn2<2>), dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool,
+                           page_table, g, group, ppw, part);
+    CHECK_LAUNCH();
+}
+
+// Merge the chunk partials of one (job, kv head, m-tile): log-sum-exp over
+// chunks in order, normalise, and write the merged-heads rows as the o_proj
+// operand (merge_heads, web/model/kernels.js:1315-1329, is this indexing).
+// The chunks' weights exp(m_c - M) sit in LDS.
+constexpr int COMBINE_CMAX = 512;
+__global__ __launch_bounds__(256) void k_attn_combine2(const JobDev* __restrict__ jobs, int njobs,
+                                                       const AttnItem* __restrict__ items,
+                                                       const float* __restrict__ part, KVGeom g, int nH, int group,
+                                                       int KU, uint4* __restrict__ Xp, float* __restrict__ ctx_out,
+                                                       const int32_t* __restrict__ wg_job) {
+    __shared__ float wgt[16][COMBINE_CMAX + 1];
+    __shared__ float Ms[16], Ls[16];
+    const int job = wg_job[3 * blockIdx.x], kvh = wg_job[3 * blockIdx.x + 1], mt = wg_job[3 * blockIdx.x + 2];
+    const JobDev jb = jobs[job];
+    const int D = g.D;
+    const int R = jb.n * group;
+    const int nc = jb.nchunk;
+    const int ibase = jb.item0 + (kvh * jb.mtq + mt) * nc;
+    for (int idx = threadIdx.x; idx < 16 * nc; idx += 256) {
+        const int rl = idx / nc, c = idx % nc;
+        wgt[rl][c] = part[items[ibase + c].part + (size_t)rl * (D + 2)];
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        float M = -INFINITY;
+        for (int c = 0; c < nc; c++) M = fmaxf(M, wgt[threadIdx.x][c]);
+        Ms[threadIdx.x] = M;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 16 * nc; idx += 256) {
+        const int rl = idx / nc, c = idx % nc;
+        const float mc = wgt[rl][c];
+        wgt[rl][c] = (mc == -INFINITY) ? 0.0f : expf(mc - Ms[rl]);
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        float L = 0.0f;
+        for (int c = 0; c < nc; c++) L += part[items[ibase + c].part + (size_t)threadIdx.x * (D + 2) + 1] * wgt[threadIdx.x][c];
+        Ls[threadIdx.x] = L;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 16 * (D / 8); idx += 256) {
+        const int rl = idx / (D / 8), d0 = (idx % (D / 8)) * 8;
+        const int rho = mt * 16 + rl;
+        if (rho >= R) continue;
+        float O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int c = 0; c < nc; c++) {
+            const float w = wgt[rl][c];
+            if (w == 0.0f) continue;
+            const float4* src = (const float4*)(part + items[ibase + c].part + (size_t)rl * (D + 2) + 2 + d0);
+            const float4 a = src[0], b = src[1];
+            O[0] += a.x * w; O[1] += a.y * w; O[2] += a.z * w; O[3] += a.w * w;
+            O[4] += b.x * w; O[5] += b.y * w; O[6] += b.z * w; O[7] += b.w * w;
+        }
+        float v[8];
+        const float L = Ls[rl];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = O[j] / L;
+        const int i = rho / group, gi = rho % group;
+        const int r = jb.row0 + i;
+        const int k = (kvh * group + gi) * D + d0;
+        if (ctx_out) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) ctx_out[(size_t)r * nH * D + k + j] = v[j];
+        }
+        write_hilo(Xp, r, k / 8, KU, v);
+    }
+}
+
+void launch_attn_combine2(hipStream_t st, const JobDev* jobs, int njobs, const AttnItem* items, const float* part,
+                          const KVGeom& g, int nH, int group, int KU, uint4* Xp, float* ctx_out,
+                          const int32_t* wg_job, int nwg) {
+    if (nwg <= 0) return;
+    hipLaunchKernelGGL(k_attn_combine2, dim3(nwg), dim3(256), 0, st, jobs, njobs, items, part, g, nH, group, KU, Xp,
+                       ctx_out, wg_job);
+    CHECK_LAUNCH();
+}
+
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
                  const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g,
                  int group, float* part) {
@@ -800,8 +1241,54 @@ __global__ void k_topk_unpack(const uint64_t* __restrict__ keys, int rows, int M
     ids[i] = 0xffffffffu - (uint32_t)(k & 0xffffffffu);
 }
 
+// M = 1 (greedy, argmax_rows semantics: web/model/kernels.js:1411-1443): the
+// largest key of 4096 entries per workgroup, then of the workgroups' keys.
+__global__ __launch_bounds__(256) void k_argmax_stage(const float* __restrict__ logits,
+                                                      const uint64_t* __restrict__ keys_in, int n,
+                                                      uint64_t* __restrict__ out) {
+    __shared__ uint64_t red[256];
+    const int row = blockIdx.y;
+    const int base = blockIdx.x * TOPK_CH;
+    uint64_t best = 0;
+    for (int k = threadIdx.x; k < TOPK_CH; k += 256) {
+        const int i = base + k;
+        if (i >= n) break;
+        const uint64_t key = logits ? topk_key(logits[(size_t)row * n + i], (uint32_t)i) : keys_in[(size_t)row * n + i];
+        best = key > best ? key : best;
+    }
+    red[threadIdx.x] = best;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x + s] > red[threadIdx.x] ? red[threadIdx.x + s] : red[threadIdx.x];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[(size_t)row * gridDim.x + blockIdx.x] = red[0];
+}
+
 void launch_topk(hipStream_t st, const float* logits, int rows, int V, int M, uint64_t* a, uint64_t* b,
                  float* vals, uint32_t* ids) {
+    if (M == 1) {
+        int n = V;
+        const float* lg = logits;
+        const uint64_t* in = nullptr;
+        uint64_t* out = a;
+        uint64_t* other = b;
+        for (;;) {
+            const int groups = (n + TOPK_CH - 1) / TOPK_CH;
+            hipLaunchKernelGGL(k_argmax_stage, dim3(groups, rows), dim3(256), 0, st, lg, in, n, out);
+            CHECK_LAUNCH();
+            if (groups == 1) break;
+            lg = nullptr;
+            in = out;
+            n = groups;
+            uint64_t* t = out;
+            out = other;
+            other = t;
+        }
+        hipLaunchKernelGGL(k_topk_unpack, dim3((rows + 255) / 256), dim3(256), 0, st, out, rows, 1, vals, ids);
+        CHECK_LAUNCH();
+        return;
+    }
     int n = V;
     const float* lg = logits;
     const uint64_t* in = nullptr;

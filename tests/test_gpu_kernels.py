@@ -97,8 +97,9 @@ def test_topk_exact(ctx, V, M):
 
 
 def test_rmsnorm_vs_oracle(ctx):
-    """rmsnorm (web/model/kernels.js:930-976): the kernel keeps the reference's
-    256-lane strided sum and tree, so it matches the oracle to 1 ulp."""
+    """rmsnorm (web/model/kernels.js:930-976). The GPU sums squares in blocks
+    of 256 columns (then the blocks in order) instead of 256 strided lanes, so
+    the scale differs by a few f32 ulp: within 1e-6 relative."""
     from oracle import lib as L
     rng = np.random.default_rng(4)
     for T, H in [(3, 576), (5, 5120), (2, 70 * 4)]:
@@ -106,7 +107,7 @@ def test_rmsnorm_vs_oracle(ctx):
         w = (rng.random(H) + 0.5).astype(np.float32)
         got = ctx.op_rmsnorm(x, w)
         want = L.rmsnorm(x, w, ctx.d["rms_eps"])
-        assert np.allclose(got, want, rtol=2.0 ** -22, atol=0)
+        assert np.allclose(got, want, rtol=1e-6, atol=0)
 
 
 def _oracle_cache(d, n_pages, page=64):
