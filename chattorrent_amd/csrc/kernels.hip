@@ -58,57 +58,95 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint4* __restrict__ Wc,
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) acc[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    const uint4* wbase = Wc + (size_t)nt0 * KU * 64 + lane;
+    // Per lane: W fragments of unit u for each n-tile at wbase + (nt*KU + u)*64,
+    // its scales at sbase + (nt*KU + u)*16, and the X fragments of m-tile mt,
+    // group g at xbase + ((mt*G2 + g)*2 + hl)*64.
+    const u32x4* wbase = (const u32x4*)Wc + (size_t)nt0 * KU * 64 + lane;
     const uint32_t* sbase = Ws + (size_t)nt0 * KU * 16 + (lane & 15);
+    const uint4* xbase = Xp + (size_t)mt0 * G2 * 128 + lane;
 
-    int u = u0 + wave;
-    uint4 w[NT];
-    uint32_t s[NT];
-    if (u < u1) {
+    // The weights stream from HBM two units ahead of use (their latency is
+    // the long one); the L2-resident activations one unit ahead.
+    u32x4 wa[NT], wb[NT];
+    uint32_t sa[NT], sb[NT];
+    uint4 xh[MT][2], xl[MT][2];
+    auto load_w = [&](int uu, u32x4 (&wv)[NT], uint32_t (&sv)[NT]) {
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) {
-            w[nt] = wbase[((size_t)nt * KU + u) * 64];
-            s[nt] = sbase[((size_t)nt * KU + u) * 16];
+            wv[nt] = __builtin_nontemporal_load(wbase + ((size_t)nt * KU + uu) * 64);
+            sv[nt] = sbase[((size_t)nt * KU + uu) * 16];
         }
-    }
-    for (; u < u1; u += 4) {
-        uint4 wc[NT];
-        uint32_t sc[NT];
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) { wc[nt] = w[nt]; sc[nt] = s[nt]; }
-        if (u + 4 < u1) {
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++) {
-                w[nt] = wbase[((size_t)nt * KU + u + 4) * 64];
-                s[nt] = sbase[((size_t)nt * KU + u + 4) * 16];
-            }
-        }
-        uint4 xh[MT][2], xl[MT][2];
+    };
+    auto load_x = [&](int uu, uint4 (&hv)[MT][2], uint4 (&lv)[MT][2]) {
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                const size_t at = (((size_t)(mt0 + mt) * G2 + 2 * u + h) * 2) * 64 + lane;
-                xh[mt][h] = Xp[at];
-                xl[mt][h] = Xp[at + 64];
+                const size_t at = (((size_t)mt * G2 + 2 * uu + h) * 2) * 64;
+                hv[mt][h] = xbase[at];
+                lv[mt][h] = xbase[at + 64];
             }
+    };
+    // One unit's arithmetic on its fragments (no copies between buffers: a
+    // register copy of a pending load would wait for it).
+    auto compute = [&](const u32x4 (&wc)[NT], const uint32_t (&sc)[NT], const uint4 (&ch)[MT][2],
+                       const uint4 (&cl)[MT][2]) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
+            half8_t b[NT];
+            float scale[NT];
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
-                const half8_t b = h ? dequant8_biased(wc[nt].z, wc[nt].w)
-                                    : dequant8_biased(wc[nt].x, wc[nt].y);
+                b[nt] = h ? dequant8_biased(wc[nt][2], wc[nt][3]) : dequant8_biased(wc[nt][0], wc[nt][1]);
                 const uint16_t sb = h ? (uint16_t)(sc[nt] >> 16) : (uint16_t)(sc[nt] & 0xffffu);
-                const float scale = (float)__builtin_bit_cast(_Float16, sb);
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++) {
-                    float4_t p = {0.f, 0.f, 0.f, 0.f};
-                    p = mfma16x16x32(__builtin_bit_cast(half8_t, xh[mt][h]), b, p);
-                    p = mfma16x16x32(__builtin_bit_cast(half8_t, xl[mt][h]), b, p);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) acc[mt][nt][r] = __builtin_fmaf(scale, p[r], acc[mt][nt][r]);
-                }
+                scale[nt] = (float)__builtin_bit_cast(_Float16, sb);
             }
+            // Independent MFMA chains (hi, then lo into the same partial) so
+            // the matrix core pipelines them; then one scale FMA per output.
+            float4_t p[MT][NT];
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    p[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, ch[mt][h]), b[nt],
+                                             float4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    p[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, cl[mt][h]), b[nt], p[mt][nt]);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        acc[mt][nt][r] = __builtin_fmaf(scale[nt], p[mt][nt][r], acc[mt][nt][r]);
+        }
+    };
+    // Units u, u+4, ... of this wave, two per trip with alternating buffers:
+    // A holds even steps, B odd; X alternates between (xh, xl) and (yh, yl).
+    // The wave index is made scalar so every branch here is uniform, and the
+    // prefetches are unconditional (past the end they re-read the last unit),
+    // so the compiler can wait for exactly the loads each step needs.
+    uint4 yh[MT][2], yl[MT][2];
+    const int uw = u0 + __builtin_amdgcn_readfirstlane(wave);
+    if (uw < u1) {
+        const int last = u1 - 1;
+        int u = uw;
+        load_w(u, wa, sa);
+        load_x(u, xh, xl);
+        load_w(min(u + 4, last), wb, sb);
+        for (;;) {
+            load_x(min(u + 4, last), yh, yl);
+            compute(wa, sa, xh, xl);
+            load_w(min(u + 8, last), wa, sa);
+            if (u + 4 >= u1) break;
+            load_x(min(u + 8, last), xh, xl);
+            compute(wb, sb, yh, yl);
+            load_w(min(u + 12, last), wb, sb);
+            u += 8;
+            if (u >= u1) break;
         }
     }
 
