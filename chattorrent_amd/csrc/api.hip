@@ -60,6 +60,8 @@ struct cc_ctx {
     uint4* xp_f = nullptr;         // operand for K = ffn
     float* part = nullptr;
     size_t part_floats = 0;
+    int ncu = 0;                   // compute units: the matmul's workgroup count
+    float* cut = nullptr;          // matmul pairs cut between waves
     uint4* qp = nullptr;
     size_t qp_units = 0;
     float* apart = nullptr;
@@ -68,7 +70,8 @@ struct cc_ctx {
     int ppw = 8;                   // pages per attention work item
     AttnItem* d_items = nullptr;
     size_t items_cap = 0;
-    float* logits = nullptr;
+    float* logits = nullptr;       // LM-head planes [P][rows][vocab]
+    int head_planes = 1, head_rows = 0;
     uint64_t* tk_a = nullptr;
     uint64_t* tk_b = nullptr;
     float* d_vals = nullptr;
@@ -128,23 +131,13 @@ hipError_t dalloc(cc_ctx* ctx, T** p, size_t bytes, uint64_t* acct) {
     return hipSuccess;
 }
 
-// K splits of a projection: from N and K only (never M), so every row gets the
-// same reduction whatever the batch.
-int splits_for(const QTensor& w, int nt) {
-    const int strips = w.Nt / nt;
-    int s = ceil_div(640, std::max(strips, 1));
-    s = std::min(s, std::max(1, w.KU / 16));
-    return std::max(1, s);
-}
-
 hipError_t alloc_q(cc_ctx* ctx, QTensor& q, int N, int K) {
     q.N = N;
     q.K = K;
-    q.Nt = ceil_div(ceil_div(N, 16), 4) * 4;   // strips of 4 n-tiles
+    q.Nt = ceil_div(ceil_div(N, 16), 2) * 2;   // tile pairs
     q.KU = ceil_div(K, 64);
-    hipError_t e = dalloc(ctx, &q.codes, (size_t)q.Nt * q.KU * 1024, &ctx->weight_bytes);
-    if (e != hipSuccess) return e;
-    return dalloc(ctx, &q.scales, (size_t)q.Nt * q.KU * 64, &ctx->weight_bytes);
+    q.P = lx_planes(q.KU);
+    return dalloc(ctx, &q.codes, (size_t)q.Nt * q.KU * (LX_REC / 2), &ctx->weight_bytes);
 }
 
 void build_rope_table(cc_ctx* ctx, std::vector<float>& t) {
@@ -186,9 +179,17 @@ cc_status check_dims(cc_ctx* ctx, const cc_dims& d, const cc_opts& o) {
     if (d.head_dim != 64 && d.head_dim != 128)
         return fail(ctx, CC_EARG, "head_dim must be 64 or 128 (the int8 KV blocks are 32 wide)");
     if (d.q8_group != 32) return fail(ctx, CC_EARG, "q8 weights must use one scale per 32 values");
-    if (d.hidden % 64 || d.ffn % 16) return fail(ctx, CC_EARG, "hidden must be a multiple of 64, ffn of 16");
-    if ((d.n_kv_heads * d.head_dim) % 16) return fail(ctx, CC_EARG, "n_kv_heads*head_dim must be a multiple of 16");
+    // Fused q|k|v and gate|up start each part on a tile pair (32 rows).
+    if (d.hidden % 64 || d.ffn % 32) return fail(ctx, CC_EARG, "hidden must be a multiple of 64, ffn of 32");
+    if ((d.n_kv_heads * d.head_dim) % 32) return fail(ctx, CC_EARG, "n_kv_heads*head_dim must be a multiple of 32");
     if (d.hidden > 16384) return fail(ctx, CC_EARG, "hidden above 16384 is not supported");
+    // The matmul addresses a weight with 32-bit byte offsets.
+    const double H = d.hidden, F = d.ffn;
+    const double big = std::max({(double)d.vocab * H, 2.0 * F * H, F * H,
+                                 (H + 2.0 * d.n_kv_heads * d.head_dim) * H}) * 1.0625;
+    if (big > 2.0e9) return fail(ctx, CC_EARG, "a weight above 2 GB is not supported");
+    if ((double)o.t_max * std::max(d.vocab, 2 * d.ffn) * 4.0 > 2.0e9)
+        return fail(ctx, CC_EARG, "t_max rows of logits must stay under 2 GB");
     const int positions = d.n_layer + 2;
     if (o.lo < 0 || o.hi > positions || o.lo >= o.hi) return fail(ctx, CC_EARG, "bad position range");
     if (o.n_max <= 0 || o.t_max <= 0 || o.slots <= 0 || o.sessions <= 0 || o.max_jobs <= 0)
@@ -316,6 +317,11 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
     }
     auto body = [&]() -> cc_status {
         HIPCHK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+        {
+            hipDeviceProp_t prop;
+            HIPCHK(hipGetDeviceProperties(&prop, o.device));
+            ctx->ncu = std::max(1, prop.multiProcessorCount);
+        }
         HIPCHK(hipEventCreate(&ctx->ev0));
         HIPCHK(hipEventCreate(&ctx->ev1));
         ctx->group = d.n_heads / d.n_kv_heads;
@@ -388,11 +394,11 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         size_t pf = 16;
         if (!ctx->layers.empty()) {
             const Layer& L = ctx->layers[0];
-            for (const QTensor* q : {&L.qkv, &L.o, &L.gu, &L.down})
-                pf = std::max(pf, (size_t)splits_for(*q, 4) * T * q->N);
+            for (const QTensor* q : {&L.qkv, &L.o, &L.gu, &L.down}) pf = std::max(pf, (size_t)q->P * T * q->N);
         }
         ctx->part_floats = pf;
         HIPCHK(dalloc(ctx, &ctx->part, pf * 4, &ctx->scratch_bytes));
+        HIPCHK(dalloc(ctx, &ctx->cut, lx_cut_floats(T, ctx->ncu) * 4, &ctx->scratch_bytes));
         // Q operands: sum over jobs of nKV * ceil(n*group/16) * ng * 2 * 64 uint4.
         ctx->qp_units = (size_t)(ceil_div(T * ctx->group, 16) + o.max_jobs) * nKV * (D / 32) * 128;
         HIPCHK(dalloc(ctx, &ctx->qp, ctx->qp_units * 16, &ctx->scratch_bytes));
@@ -405,7 +411,8 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         HIPCHK(dalloc(ctx, &ctx->apart, ctx->apart_floats * 4, &ctx->scratch_bytes));
         HIPCHK(dalloc(ctx, &ctx->ssq, (size_t)T * ceil_div(H, 256) * 4, &ctx->scratch_bytes));
         if (ctx->head) {
-            HIPCHK(dalloc(ctx, &ctx->logits, (size_t)T * d.vocab * 4, &ctx->scratch_bytes));
+            ctx->head_planes = lx_planes(ceil_div(H, 64));
+            HIPCHK(dalloc(ctx, &ctx->logits, (size_t)ctx->head_planes * T * d.vocab * 4, &ctx->scratch_bytes));
             const size_t keys = (size_t)T * ceil_div(d.vocab, 4096) * TOPK_MAX;
             HIPCHK(dalloc(ctx, &ctx->tk_a, keys * 8, &ctx->scratch_bytes));
             HIPCHK(dalloc(ctx, &ctx->tk_b, keys * 8, &ctx->scratch_bytes));
@@ -625,31 +632,18 @@ cc_status cc_read_pages(cc_ctx* ctx, int32_t slot, uint32_t* out, int32_t n) {
     return CC_OK;
 }
 
-cc_status cc_debug_read(cc_ctx* ctx, int32_t which, size_t offset, size_t bytes, void* out) {
-    if (!ctx || !out) return CC_EARG;
-    const void* src = nullptr;
-    switch (which) {
-        case 0: src = ctx->x; break;
-        case 1: src = ctx->xp_h; break;
-        case 2: src = ctx->logits; break;
-        case 3: src = ctx->wte.codes; break;
-        case 4: src = ctx->wte.scales; break;
-        case 5: src = ctx->norm; break;
-        case 6: src = ctx->d_meta; break;
-        case 7: src = ctx->apart; break;
-        case 8: src = ctx->qp; break;
-        default: return fail(ctx, CC_EARG, "unknown buffer");
-    }
-    if (!src) return fail(ctx, CC_EARG, "buffer not allocated");
-    HIPCHK(hipStreamSynchronize(ctx->stream));
-    HIPCHK(hipMemcpy(out, (const uint8_t*)src + offset, bytes, hipMemcpyDeviceToHost));
-    return CC_OK;
-}
-
 cc_status cc_read_logits(cc_ctx* ctx, int32_t rows, float* out) {
-    if (!ctx || !out || !ctx->logits || rows < 1 || rows > ctx->o.t_max) return fail(ctx, CC_EARG, "no logits here");
+    if (!ctx || !out || !ctx->logits || rows < 1 || rows != ctx->head_rows)
+        return fail(ctx, CC_EARG, "rows must be the last pass's sampled rows");
     HIPCHK(hipStreamSynchronize(ctx->stream));
-    HIPCHK(hipMemcpy(out, ctx->logits, (size_t)rows * ctx->d.vocab * 4, hipMemcpyDeviceToHost));
+    // The head's planes, added in plane order as the sampling kernels add them.
+    const size_t n = (size_t)rows * ctx->d.vocab;
+    std::vector<float> plane(n);
+    HIPCHK(hipMemcpy(out, ctx->logits, n * 4, hipMemcpyDeviceToHost));
+    for (int q = 1; q < ctx->head_planes; q++) {
+        HIPCHK(hipMemcpy(plane.data(), ctx->logits + q * n, n * 4, hipMemcpyDeviceToHost));
+        for (size_t i = 0; i < n; i++) out[i] = out[i] + plane[i];
+    }
     return CC_OK;
 }
 
@@ -767,9 +761,9 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
         if (b == b0)
             launch_resid_norm(st, ctx->x, nullptr, nullptr, 0, T, Mpad, H, 0, L.ln1, d.rms_eps, L.qkv.KU, ctx->xp_h,
                               nullptr, ctx->ssq);
-        const int sq = splits_for(L.qkv, 4);
+        const int sq = L.qkv.P;
         int e = prof_begin(ctx);
-        launch_gemm(st, L.qkv, ctx->xp_h, ctx->part, T, sq, 4);
+        launch_gemm(st, L.qkv, ctx->xp_h, ctx->part, T, ctx->cut, ctx->ncu);
         prof_end(ctx, e, CC_K_QKV, qbytes(L.qkv));
         launch_fin_qkv(st, ctx->part, sq, T, drow_job, djobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
                        L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 1);
@@ -779,20 +773,20 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
         prof_end(ctx, e, CC_K_ATTN, p.kv_bytes);
         launch_attn_combine2(st, djobs, (int)p.jobs.size(), ditems, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU,
                              ctx->xp_o, nullptr, dcwg, p.ncwg);
-        const int so = splits_for(L.o, 4);
+        const int so = L.o.P;
         e = prof_begin(ctx);
-        launch_gemm(st, L.o, ctx->xp_o, ctx->part, T, so, 4);
+        launch_gemm(st, L.o, ctx->xp_o, ctx->part, T, ctx->cut, ctx->ncu);
         prof_end(ctx, e, CC_K_O, qbytes(L.o));
         launch_resid_norm(st, ctx->x, nullptr, ctx->part, so, T, Mpad, H, 0, L.ln2, d.rms_eps, L.gu.KU, ctx->xp_h,
                           nullptr, ctx->ssq);
-        const int sg = splits_for(L.gu, 4);
+        const int sg = L.gu.P;
         e = prof_begin(ctx);
-        launch_gemm(st, L.gu, ctx->xp_h, ctx->part, T, sg, 4);
+        launch_gemm(st, L.gu, ctx->xp_h, ctx->part, T, ctx->cut, ctx->ncu);
         prof_end(ctx, e, CC_K_GU, qbytes(L.gu));
         launch_fin_swiglu(st, ctx->part, sg, T, Mpad, d.ffn, L.down.KU, ctx->xp_f);
-        const int sd = splits_for(L.down, 4);
+        const int sd = L.down.P;
         e = prof_begin(ctx);
-        launch_gemm(st, L.down, ctx->xp_f, ctx->part, T, sd, 4);
+        launch_gemm(st, L.down, ctx->xp_f, ctx->part, T, ctx->cut, ctx->ncu);
         prof_end(ctx, e, CC_K_DOWN, qbytes(L.down));
         const bool next = b + 1 < b1;
         launch_resid_norm(st, ctx->x, nullptr, ctx->part, sd, T, Mpad, H, 1,
@@ -917,9 +911,10 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         launch_resid_norm(st, ctx->x, (const int32_t*)(ctx->d_meta + ml.head_rows), nullptr, 0, S, Mpad, d.hidden, 0,
                           ctx->norm, d.rms_eps, hw.KU, ctx->xp_h, nullptr, ctx->ssq);
         const int e = prof_begin(ctx);
-        launch_gemm(st, hw, ctx->xp_h, ctx->logits, S, 1, 4);
+        launch_gemm(st, hw, ctx->xp_h, ctx->logits, S, ctx->cut, ctx->ncu);
         prof_end(ctx, e, CC_K_HEAD, qbytes(hw));
-        launch_topk(st, ctx->logits, S, d.vocab, topk, ctx->tk_a, ctx->tk_b, ctx->d_vals, ctx->d_ids);
+        ctx->head_rows = S;
+        launch_topk(st, ctx->logits, hw.P, S, d.vocab, topk, ctx->tk_a, ctx->tk_b, ctx->d_vals, ctx->d_ids);
         HIPCHK(hipMemcpyAsync(hout, ctx->d_vals, (size_t)S * topk * 4, hipMemcpyDeviceToHost, st));
         HIPCHK(hipMemcpyAsync((uint8_t*)hout + (size_t)S * topk * 4, ctx->d_ids, (size_t)S * topk * 4,
                               hipMemcpyDeviceToHost, st));
@@ -952,16 +947,18 @@ cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K, con
     QTensor q{};
     q.N = N;
     q.K = K;
-    q.Nt = ceil_div(ceil_div(N, 16), 4) * 4;
+    q.Nt = ceil_div(ceil_div(N, 16), 2) * 2;
     q.KU = ceil_div(K, 64);
+    q.P = lx_planes(q.KU);
     const int ng = ceil_div(K, 32);
     const int Mt = 2 * ceil_div(M, 32);
-    const int sp = splits_for(q, 4);
+    const int sp = q.P;
     int8_t* dW = nullptr; uint16_t* dS = nullptr; float* dX = nullptr; float* dP = nullptr; float* dY = nullptr;
     uint4* dXp = nullptr;
-    HIPCHK(hipMalloc(&q.codes, (size_t)q.Nt * q.KU * 1024));
-    HIPCHK(hipMalloc(&q.scales, (size_t)q.Nt * q.KU * 64));
-    HIPCHK(hipMemsetAsync(q.scales, 0, (size_t)q.Nt * q.KU * 64, ctx->stream));
+    float* dC = nullptr;
+    HIPCHK(hipMalloc(&q.codes, (size_t)q.Nt * q.KU * (LX_REC / 2)));
+    HIPCHK(hipMemsetAsync(q.codes, 0, (size_t)q.Nt * q.KU * (LX_REC / 2), ctx->stream));
+    HIPCHK(hipMalloc(&dC, lx_cut_floats(M, ctx->ncu) * 4));
     HIPCHK(hipMalloc(&dW, (size_t)N * K));
     HIPCHK(hipMalloc(&dS, (size_t)N * ng * 2));
     HIPCHK(hipMalloc(&dX, (size_t)M * K * 4));
@@ -974,11 +971,12 @@ cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K, con
     hipStream_t st = ctx->stream;
     launch_tile_q8(st, dW, dS, N, K, 32, q, 0);
     launch_prep_rows(st, dX, K, M, Mt * 16, K, q.KU, dXp);
-    launch_gemm(st, q, dXp, dP, M, sp, 4);
+    launch_gemm(st, q, dXp, dP, M, dC, ctx->ncu);
     launch_sum_splits(st, dP, sp, M, N, dY);
     HIPCHK(hipStreamSynchronize(st));
+    HIPCHK(take_launch_error());
     HIPCHK(hipMemcpy(Y, dY, (size_t)M * N * 4, hipMemcpyDeviceToHost));
-    for (void* v : {(void*)q.codes, (void*)q.scales, (void*)dW, (void*)dS, (void*)dX, (void*)dXp, (void*)dP, (void*)dY})
+    for (void* v : {(void*)q.codes, (void*)dC, (void*)dW, (void*)dS, (void*)dX, (void*)dXp, (void*)dP, (void*)dY})
         hipFree(v);
     return CC_OK;
 }
@@ -1006,7 +1004,7 @@ cc_status cc_op_topk(cc_ctx* ctx, const float* logits, int32_t rows, int32_t V, 
     HIPCHK(hipMalloc(&dv, (size_t)rows * M * 4));
     HIPCHK(hipMalloc(&di, (size_t)rows * M * 4));
     HIPCHK(hipMemcpy(dL, logits, (size_t)rows * V * 4, hipMemcpyHostToDevice));
-    launch_topk(ctx->stream, dL, rows, V, M, a, b, dv, di);
+    launch_topk(ctx->stream, dL, 1, rows, V, M, a, b, dv, di);
     HIPCHK(hipStreamSynchronize(ctx->stream));
     HIPCHK(hipMemcpy(vals, dv, (size_t)rows * M * 4, hipMemcpyDeviceToHost));
     HIPCHK(hipMemcpy(ids, di, (size_t)rows * M * 4, hipMemcpyDeviceToHost));

@@ -4,15 +4,33 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-// Tiled q8 weight (one 16-row x 64-column unit = 1 KiB of codes + 64 B of
-// scales): codes [Nt][KU][64 lanes][16 B], byte b of lane l holds
-// W[16t + l%16][64u + 32(b/8) + 8(l/16) + b%8] stored as q ^ 0x80; scales
-// [Nt][KU][16][2] f16 for groups 2u, 2u+1 of row 16t + i.
+// q8 weight in matmul stream order. A tile is 16 rows x 64 columns of K (a
+// "unit"); tiles pair up (t, t^1). K units split into P planes, plane r
+// covering units [r*KU/P, (r+1)*KU/P) (at most LX_UNITS each). For each
+// plane, then each tile pair, then each unit of the plane, one record of
+// LX_REC bytes:
+//   [nt*1024 + lane*16 + b]  code of W[16t + lane%16][64u + 32(b/8) + 8(lane/16) + b%8]
+//                            stored as q ^ 0x80 (t = 2*pair + nt)
+//   [2048 + c*8 + nt*4 + h*2] f16 scale of row 16t + c, group 2u + h
+// so the matmul reads each workgroup's weights as one forward stream.
+constexpr int LX_UNITS = 20;     // K units whose activations one workgroup keeps in LDS
+constexpr int LX_REC = 2176;     // bytes per (tile pair, unit) record
+
 struct QTensor {
-    uint8_t* codes = nullptr;
-    uint16_t* scales = nullptr;
-    int N = 0, K = 0, Nt = 0, KU = 0;
+    uint8_t* codes = nullptr;    // records, Nt*KU*1088 bytes
+    int N = 0, K = 0, Nt = 0, KU = 0, P = 1;
 };
+
+__host__ __device__ inline int lx_plane_start(int r, int KU, int P) { return (r * KU) / P; }
+__host__ __device__ inline int lx_planes(int KU) { return (KU + LX_UNITS - 1) / LX_UNITS; }
+// Byte offset of the record holding tile t, unit u.
+__host__ __device__ inline size_t lx_record(int t, int u, int KU, int P, int Nt) {
+    int r = (u * P) / KU;
+    while (r + 1 < P && lx_plane_start(r + 1, KU, P) <= u) r++;
+    while (r > 0 && lx_plane_start(r, KU, P) > u) r--;
+    const int ua = lx_plane_start(r, KU, P), len = lx_plane_start(r + 1, KU, P) - ua;
+    return ((size_t)ua * (Nt / 2) + (size_t)(t >> 1) * len + (size_t)(u - ua)) * LX_REC;
+}
 
 // One pass's per-job table on the device (built on the host each step).
 struct JobDev {
@@ -32,8 +50,10 @@ struct KVGeom {
     int max_pages;
 };
 
-void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M,
-                 int splits, int nt);
+// Y planes: out[(r*M + m)*N + n], r < w.P; `cut` holds lx_cut_floats(..) floats.
+void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, float* cut, int ncu);
+size_t lx_cut_floats(int M, int ncu);
+int lx_groups(const QTensor& w, int ncu);
 void launch_prep_rows(hipStream_t st, const float* x, int ldx, int M, int Mpad, int K, int KU,
                       uint4* Xp);
 void launch_rmsnorm_prep(hipStream_t st, const float* x, const int32_t* rows, int M, int Mpad,
@@ -54,7 +74,7 @@ void launch_attn_combine(hipStream_t st, const JobDev* jobs, int njobs, const At
                          int KU, uint4* Xp, float* ctx_out);
 void launch_embed(hipStream_t st, const int32_t* ids, const uint16_t* hidden, int T, const QTensor& wte,
                   float* x);
-void launch_topk(hipStream_t st, const float* logits, int rows, int V, int M, uint64_t* a,
+void launch_topk(hipStream_t st, const float* logits, int planes, int rows, int V, int M, uint64_t* a,
                  uint64_t* b, float* vals, uint32_t* ids);
 void launch_round_f16(hipStream_t st, float* a, int64_t n);
 void launch_alloc_pages(hipStream_t st, const int32_t* plan, int njobs, const uint32_t* free_stack,

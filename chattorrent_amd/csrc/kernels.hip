@@ -10,6 +10,7 @@
 // reduction ("finish") kernels that feed the next projection its operand.
 #include "common.h"
 #include "kernels.h"
+#include <algorithm>
 
 // The first launch error since the last take_launch_error(); cc_step and the
 // other entry points report it as CC_EDEVICE after their synchronisation.
@@ -26,71 +27,96 @@ hipError_t take_launch_error() {
     } while (0)
 
 // ===================================================================== GEMM ===
-// Y[M, N] = X[M, K] . W[N, K]^T for a tiled q8 W (kernels.h QTensor) and an
+// Y[M, N] = X[M, K] . W[N, K]^T for a q8 W in record order (kernels.h) and an
 // activation operand Xp prepared by the prep/finish kernels:
 //   Xp[((mt*G2 + g)*2 + hl)*64 + lane] = 8 f16 of X[16mt + lane%16][32g + 8(lane/16) ..]
 // (hl = 0: hi part, 1: lo part; G2 = 2*KU groups, zero beyond K).
-// Grid: x = strips of NT n-tiles (16 columns each), y = K splits of `ups`
-// units (64 columns of K), z = blocks of MT m-tiles. Four waves share a strip
-// and split its units round-robin; their partial sums are added in LDS in a
-// fixed order, so a result never depends on timing, on M, or on the other
-// rows (each row's MFMA output depends only on that row's operand).
-// Output: out[(split*M + m)*N + n]; the finish kernels add the splits in order.
-// Reference: matmul_gemv_q8 / matmul_gemv_rows_q8 / matmul_rows_q8
-// (web/model/kernels.js:449-751): per group, acc += scale * dot(x, q).
-template <int MT, int NT>
-__global__ __launch_bounds__(256) void k_gemm_q8(const uint4* __restrict__ Wc,
-                                                 const uint32_t* __restrict__ Ws,
-                                                 const uint4* __restrict__ Xp,
-                                                 float* __restrict__ out,
-                                                 int KU, int M, int N, int ups) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nt0 = blockIdx.x * NT;
-    const int split = blockIdx.y;
-    const int mt0 = blockIdx.z * MT;
-    const int G2 = 2 * KU;
-    const int u0 = split * ups;
-    const int u1 = min(KU, u0 + ups);
+// Reference: matmul_gemv_q8 / matmul_gemv_rows_q8 / matmul_rows_q8 /
+// matmul_tiled_q8 (web/model/kernels.js:449-804): per group, acc += scale * dot(x, q).
+//
+// Workgroup g (8 waves) serves plane r = g % P and a contiguous block of tile
+// pairs; it first copies the plane's activations (MT m-tiles x <= LX_UNITS
+// units, <= 160 KiB) into LDS, so the waves' only global loads are the weight
+// records, which stream LX_R - 1 steps ahead. A "step" is one (pair, unit)
+// record; the workgroup's steps are split evenly over its waves in record
+// order, so each wave reads one forward run of memory. A pair cut between
+// waves is finished by the wave holding its first units, adding the others'
+// parts in unit order. Every split point depends on N, K and the CU count,
+// never on M, so a row's result is the same in any batch.
+// Output: plane r to out[(r*M + m)*N + n]; consumers add planes 0..P-1 in order.
+constexpr int LX_WAVES = 8;
+constexpr int LX_R = 4;
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int MT>
+__global__ __launch_bounds__(64 * LX_WAVES) void k_gemm_lx(const uint8_t* __restrict__ Wr,
+                                                           const uint4* __restrict__ Xp, float* __restrict__ out,
+                                                           float* __restrict__ cut, int KU, int M, int N, int Nt,
+                                                           int P, int Gm) {
+    constexpr int NT = 2, R = LX_R, PW = R - 1, WAVES = LX_WAVES;
+    extern __shared__ __attribute__((aligned(1024))) u32x4 xs[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = blockIdx.x % P, j = blockIdx.x / P;
+    const int ua = lx_plane_start(r, KU, P), len = lx_plane_start(r + 1, KU, P) - ua;
+    const int npairs = Nt / NT;
+    const int p0 = (j * npairs) / Gm, p1 = ((j + 1) * npairs) / Gm;
+    const int steps = (p1 - p0) * len;
+    const int sw0 = (wave * steps) / WAVES, sw1 = ((wave + 1) * steps) / WAVES;
+    const int nst = sw1 - sw0;
+    const int mt0 = blockIdx.y * MT;
+    const int G2 = 2 * KU;
+    const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)Wr, 0, 0x7fffffff, 0x00020000);
+    const auto rx = __builtin_amdgcn_make_buffer_rsrc((void*)Xp, 0, 0x7fffffff, 0x00020000);
+    // Plane r's rows only: stores of rows >= M fall outside and are dropped.
+    const auto ro = __builtin_amdgcn_make_buffer_rsrc((void*)(out + (size_t)r * M * N), 0, M * N * 4, 0x00020000);
+    const auto rc = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(cut + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * WAVES * MT * NT * 256), 0,
+        WAVES * MT * NT * 1024, 0x00020000);
+    const int vw = lane * 16, vs = NT * 1024 + (lane & 15) * NT * 4;
+    const int vo = (4 * (lane >> 4) * N + (lane & 15)) * 4;
+    const int rec0 = ua * npairs + p0 * len;
+
+    u32x4 w[R][NT];
+    uint32_t s[R][NT];
+    int sl = sw0;   // next step to load; stays on the last one past the end
+    auto load_w = [&](u32x4 (&wv)[NT], uint32_t (&sv)[NT]) {
+        const int off = (rec0 + sl) * LX_REC;
+        wv[0] = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, off, 2);
+        wv[1] = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, off + 1024, 2);
+        const auto sc = __builtin_amdgcn_raw_buffer_load_b64(rw, vs, off, 0);
+        sv[0] = sc[0];
+        sv[1] = sc[1];
+        if (sl + 1 < sw1) sl++;
+    };
+    if (nst > 0) {
+#pragma unroll
+        for (int i = 0; i < PW; i++) load_w(w[i], s[i]);
+    }
+    // Activations of this plane into LDS: block (u, mt, q) of 1 KiB, q = 2h + hl.
+    {
+        const int nblk = len * MT * 4;
+        for (int b = wave; b < nblk; b += WAVES) {
+            const int u = b / (MT * 4), mt = (b / 4) % MT, q = b % 4;
+            const int src = ((mt0 + mt) * G2 + 2 * (ua + u) + (q >> 1)) * 2 + (q & 1);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(xs + b * 64), 16, vw, src * 1024, 0, 0);
+        }
+    }
     float4_t acc[MT][NT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++) acc[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
 
-    // Per lane: W fragments of unit u for each n-tile at wbase + (nt*KU + u)*64,
-    // its scales at sbase + (nt*KU + u)*16, and the X fragments of m-tile mt,
-    // group g at xbase + ((mt*G2 + g)*2 + hl)*64.
-    const u32x4* wbase = (const u32x4*)Wc + (size_t)nt0 * KU * 64 + lane;
-    const uint32_t* sbase = Ws + (size_t)nt0 * KU * 16 + (lane & 15);
-    const uint4* xbase = Xp + (size_t)mt0 * G2 * 128 + lane;
-
-    // The weights stream from HBM two units ahead of use (their latency is
-    // the long one); the L2-resident activations one unit ahead.
-    u32x4 wa[NT], wb[NT];
-    uint32_t sa[NT], sb[NT];
-    uint4 xh[MT][2], xl[MT][2];
-    auto load_w = [&](int uu, u32x4 (&wv)[NT], uint32_t (&sv)[NT]) {
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            wv[nt] = __builtin_nontemporal_load(wbase + ((size_t)nt * KU + uu) * 64);
-            sv[nt] = sbase[((size_t)nt * KU + uu) * 16];
-        }
-    };
-    auto load_x = [&](int uu, uint4 (&hv)[MT][2], uint4 (&lv)[MT][2]) {
+    auto compute = [&](const u32x4 (&wc)[NT], const uint32_t (&sc)[NT], int u) {
+        u32x4 xv[MT][4];
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const size_t at = (((size_t)mt * G2 + 2 * uu + h) * 2) * 64;
-                hv[mt][h] = xbase[at];
-                lv[mt][h] = xbase[at + 64];
-            }
-    };
-    // One unit's arithmetic on its fragments (no copies between buffers: a
-    // register copy of a pending load would wait for it).
-    auto compute = [&](const u32x4 (&wc)[NT], const uint32_t (&sc)[NT], const uint4 (&ch)[MT][2],
-                       const uint4 (&cl)[MT][2]) {
+            for (int q = 0; q < 4; q++) xv[mt][q] = xs[((u * MT + mt) * 4 + q) * 64 + lane];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             half8_t b[NT];
@@ -98,100 +124,153 @@ __global__ __launch_bounds__(256) void k_gemm_q8(const uint4* __restrict__ Wc,
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 b[nt] = h ? dequant8_biased(wc[nt][2], wc[nt][3]) : dequant8_biased(wc[nt][0], wc[nt][1]);
-                const uint16_t sb = h ? (uint16_t)(sc[nt] >> 16) : (uint16_t)(sc[nt] & 0xffffu);
-                scale[nt] = (float)__builtin_bit_cast(_Float16, sb);
+                const uint16_t s16 = h ? (uint16_t)(sc[nt] >> 16) : (uint16_t)(sc[nt] & 0xffffu);
+                scale[nt] = (float)__builtin_bit_cast(_Float16, s16);
             }
-            // Independent MFMA chains (hi, then lo into the same partial) so
-            // the matrix core pipelines them; then one scale FMA per output.
-            float4_t p[MT][NT];
+            // hi then lo into one partial per output, then one scale FMA
+            float4_t pp[MT][NT];
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
-                    p[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, ch[mt][h]), b[nt],
-                                             float4_t{0.f, 0.f, 0.f, 0.f});
+                    pp[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[mt][2 * h]), b[nt],
+                                              float4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
-                    p[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, cl[mt][h]), b[nt], p[mt][nt]);
+                    pp[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[mt][2 * h + 1]), b[nt], pp[mt][nt]);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        acc[mt][nt][r] = __builtin_fmaf(scale[nt], p[mt][nt][r], acc[mt][nt][r]);
+                    for (int e = 0; e < 4; e++)
+                        acc[mt][nt][e] = __builtin_fmaf(scale[nt], pp[mt][nt][e], acc[mt][nt][e]);
         }
     };
-    // Units u, u+4, ... of this wave, two per trip with alternating buffers:
-    // A holds even steps, B odd; X alternates between (xh, xl) and (yh, yl).
-    // The wave index is made scalar so every branch here is uniform, and the
-    // prefetches are unconditional (past the end they re-read the last unit),
-    // so the compiler can wait for exactly the loads each step needs.
-    uint4 yh[MT][2], yl[MT][2];
-    const int uw = u0 + __builtin_amdgcn_readfirstlane(wave);
-    if (uw < u1) {
-        const int last = u1 - 1;
-        int u = uw;
-        load_w(u, wa, sa);
-        load_x(u, xh, xl);
-        load_w(min(u + 4, last), wb, sb);
-        for (;;) {
-            load_x(min(u + 4, last), yh, yl);
-            compute(wa, sa, xh, xl);
-            load_w(min(u + 8, last), wa, sa);
-            if (u + 4 >= u1) break;
-            load_x(min(u + 8, last), xh, xl);
-            compute(wb, sb, yh, yl);
-            load_w(min(u + 12, last), wb, sb);
-            u += 8;
-            if (u >= u1) break;
+    auto store_plane = [&](int pair) {
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            const int tile = (p0 + pair) * NT + nt;
+            if (tile * 16 >= N) continue;
+            // columns past N of a partial tile would land in the next row
+            if (tile * 16 + 16 > N && tile * 16 + (lane & 15) >= N) continue;
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float v = acc[mt][nt][e];
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ro,
+                                                          vo + (((mt0 + mt) * 16 + e) * N + tile * 16) * 4, 0, 0);
+                }
+        }
+    };
+    int pc = 0, uc = 0;   // (pair, unit) of the step being computed
+    if (nst > 0) {
+        pc = sw0 / len;
+        uc = sw0 - pc * len;
+    }
+    bool head_open = false;
+    // After a pair's last unit (or this wave's last step) its partial goes to
+    // `out` (whole pair), to this wave's cut slot (pair began in an earlier
+    // wave), or stays in acc (pair goes on in later waves).
+    auto finish_step = [&](int st) {
+        if (uc == len - 1 || st == sw1 - 1) {
+            if (pc * len < sw0) {
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++)
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mt][nt]), rc, vw,
+                                                               ((wave * MT + mt) * NT + nt) * 1024, 0);
+            } else if ((pc + 1) * len <= sw1) {
+                store_plane(pc);
+            } else {
+                head_open = true;
+            }
+            if (!head_open) {
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                    for (int nt = 0; nt < NT; nt++) acc[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        if (++uc == len) {
+            uc = 0;
+            pc++;
+        }
+    };
+    if (nst > 0) {
+        int k = 0;
+        for (; k + R <= nst; k += R) {
+#pragma unroll
+            for (int I = 0; I < R; I++) {
+                load_w(w[(I + PW) % R], s[(I + PW) % R]);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(w[I], s[I], uc);
+                __builtin_amdgcn_sched_barrier(0);
+                finish_step(sw0 + k + I);
+            }
+        }
+        // At most PW steps remain, already in ring slots 0 .. PW-1.
+#pragma unroll
+        for (int I = 0; I < PW; I++) {
+            if (k + I < nst) {
+                compute(w[I], s[I], uc);
+                finish_step(sw0 + k + I);
+            }
         }
     }
-
-    __shared__ float4_t red[4 * MT * NT * 64];
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) red[(wave * MT * NT + mt * NT + nt) * 64 + lane] = acc[mt][nt];
     __syncthreads();
-    for (int e = threadIdx.x; e < MT * NT * 64; e += 256) {
-        float4_t v = red[e];
+    if (head_open) {
+        const int pair = (sw1 - 1) / len, pe = (pair + 1) * len;
+        for (int w2 = wave + 1; w2 < WAVES; w2++) {
+            const int a2 = (w2 * steps) / WAVES, b2 = ((w2 + 1) * steps) / WAVES;
+            if (a2 >= pe) break;
+            if (b2 <= a2) continue;
 #pragma unroll
-        for (int wv = 1; wv < 4; wv++) {
-            const float4_t o = red[wv * MT * NT * 64 + e];
+            for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) v[r] = v[r] + o[r];
+                for (int nt = 0; nt < NT; nt++) {
+                    const float4_t o = __builtin_bit_cast(
+                        float4_t, __builtin_amdgcn_raw_buffer_load_b128(rc, vw, ((w2 * MT + mt) * NT + nt) * 1024, 1));
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[mt][nt][e] = acc[mt][nt][e] + o[e];
+                }
         }
-        const int l = e & 63, tile = e >> 6, mt = tile / NT, nt = tile % NT;
-        const int n = (nt0 + nt) * 16 + (l & 15);
-        if (n >= N) continue;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = (mt0 + mt) * 16 + 4 * (l >> 4) + r;
-            if (m < M) out[((size_t)split * M + m) * N + n] = v[r];
-        }
+        store_plane(pair);
     }
 }
 
-void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, int splits,
-                 int nt) {
-    const int ups = (w.KU + splits - 1) / splits;
-    const int mblocks16 = (M + 15) / 16;
-    if (mblocks16 <= 1) {
-        dim3 grid(w.Nt / nt, splits, 1);
-        if (nt == 4) hipLaunchKernelGGL((k_gemm_q8<1, 4>), grid, dim3(256), 0, st, (const uint4*)w.codes,
-                                        (const uint32_t*)w.scales, Xp, out, w.KU, M, w.N, ups);
-        else hipLaunchKernelGGL((k_gemm_q8<1, 2>), grid, dim3(256), 0, st, (const uint4*)w.codes,
-                                (const uint32_t*)w.scales, Xp, out, w.KU, M, w.N, ups);
-    } else {
-        dim3 grid(w.Nt / nt, splits, (mblocks16 + 1) / 2);
-        if (nt == 4) hipLaunchKernelGGL((k_gemm_q8<2, 4>), grid, dim3(256), 0, st, (const uint4*)w.codes,
-                                        (const uint32_t*)w.scales, Xp, out, w.KU, M, w.N, ups);
-        else hipLaunchKernelGGL((k_gemm_q8<2, 2>), grid, dim3(256), 0, st, (const uint4*)w.codes,
-                                (const uint32_t*)w.scales, Xp, out, w.KU, M, w.N, ups);
+int lx_groups(const QTensor& w, int ncu) {
+    const int per = std::max(1, std::min(ncu / w.P, w.Nt / 2));
+    return w.P * per;
+}
+
+size_t lx_cut_floats(int M, int ncu) {
+    // grid.x <= ncu, grid.y m-blocks of 32 rows; one slot per wave of MT=2 x NT=2 tiles
+    return (size_t)ncu * ((M + 31) / 32) * LX_WAVES * 2 * 2 * 256;
+}
+
+template <int MT>
+static void launch_lx(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, float* cut, int ncu) {
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute((const void*)k_gemm_lx<MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  LX_UNITS * MT * 4096);
     }
+    const int G = lx_groups(w, ncu), Gm = G / w.P;
+    const int lenmax = (w.KU + w.P - 1) / w.P;
+    dim3 grid(G, (M + 16 * MT - 1) / (16 * MT));
+    hipLaunchKernelGGL(k_gemm_lx<MT>, grid, dim3(64 * LX_WAVES), (size_t)lenmax * MT * 4096, st, w.codes, Xp, out, cut,
+                       w.KU, M, w.N, w.Nt, w.P, Gm);
+}
+
+void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, float* cut, int ncu) {
+    if (M <= 16) launch_lx<1>(st, w, Xp, out, M, cut, ncu);
+    else launch_lx<2>(st, w, Xp, out, M, cut, ncu);
     CHECK_LAUNCH();
 }
 
@@ -1194,8 +1273,7 @@ void launch_attn_combine(hipStream_t st, const JobDev* jobs, int njobs, const At
 // embedding rows are rounded like a block's output, stage.js:1365-1370);
 // or, for a pass entering past position 0, the f16 rows handed in.
 __global__ void k_embed(const int32_t* __restrict__ ids, const uint16_t* __restrict__ hidden, int T, int H,
-                        const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales, int KU,
-                        float* __restrict__ x) {
+                        const uint8_t* __restrict__ rec, int Nt, int KU, int P, float* __restrict__ x) {
     const int t = blockIdx.y;
     const int h = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= T || h >= H) return;
@@ -1206,17 +1284,16 @@ __global__ void k_embed(const int32_t* __restrict__ ids, const uint16_t* __restr
     const int v = ids[t];
     const int tile = v >> 4, u = h >> 6, lane = (v & 15) + 16 * ((h & 31) >> 3);
     const int byte = 8 * ((h & 63) >> 5) + (h & 7);
-    const uint8_t b = codes[(((size_t)tile * KU + u) * 64 + lane) * 16 + byte];
-    const int8_t q = (int8_t)(b ^ 0x80);
-    const uint16_t sb = scales[(((size_t)tile * KU + u) * 16 + (v & 15)) * 2 + ((h >> 5) & 1)];
+    const uint8_t* r = rec + lx_record(tile, u, KU, P, Nt);
+    const int8_t q = (int8_t)(r[(tile & 1) * 1024 + lane * 16 + byte] ^ 0x80);
+    const uint16_t sb = *(const uint16_t*)(r + 2048 + (v & 15) * 8 + (tile & 1) * 4 + ((h >> 5) & 1) * 2);
     x[(size_t)t * H + h] = round_f16_value((float)q * half_value(sb));
 }
 
 void launch_embed(hipStream_t st, const int32_t* ids, const uint16_t* hidden, int T, const QTensor& wte,
                   float* x) {
     dim3 grid((wte.K + 255) / 256, T);
-    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, st, ids, hidden, T, wte.K, wte.codes, wte.scales, wte.KU,
-                       x);
+    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, st, ids, hidden, T, wte.K, wte.codes, wte.Nt, wte.KU, wte.P, x);
     CHECK_LAUNCH();
 }
 
@@ -1235,16 +1312,26 @@ __device__ static inline uint64_t topk_key(float v, uint32_t i) {
 
 constexpr int TOPK_CH = 4096;
 
-__global__ __launch_bounds__(256) void k_topk_stage(const float* __restrict__ logits,
+// A head logit: the LM-head matmul's planes added in order.
+__device__ static inline float plane_sum(const float* __restrict__ p, int planes, size_t stride, size_t i) {
+    float v = p[i];
+    for (int q = 1; q < planes; q++) v = v + p[q * stride + i];
+    return v;
+}
+
+__global__ __launch_bounds__(256) void k_topk_stage(const float* __restrict__ logits, int planes,
                                                     const uint64_t* __restrict__ keys_in, int n, int M,
                                                     uint64_t* __restrict__ out) {
+    const size_t stride = (size_t)gridDim.y * n;
     __shared__ uint64_t s[TOPK_CH];
     const int row = blockIdx.y;
     const int base = blockIdx.x * TOPK_CH;
     for (int k = threadIdx.x; k < TOPK_CH; k += 256) {
         const int i = base + k;
         uint64_t key = 0;
-        if (i < n) key = logits ? topk_key(logits[(size_t)row * n + i], (uint32_t)i) : keys_in[(size_t)row * n + i];
+        if (i < n)
+            key = logits ? topk_key(plane_sum(logits, planes, stride, (size_t)row * n + i), (uint32_t)i)
+                         : keys_in[(size_t)row * n + i];
         s[k] = key;
     }
     __syncthreads();
@@ -1281,9 +1368,10 @@ __global__ void k_topk_unpack(const uint64_t* __restrict__ keys, int rows, int M
 
 // M = 1 (greedy, argmax_rows semantics: web/model/kernels.js:1411-1443): the
 // largest key of 4096 entries per workgroup, then of the workgroups' keys.
-__global__ __launch_bounds__(256) void k_argmax_stage(const float* __restrict__ logits,
+__global__ __launch_bounds__(256) void k_argmax_stage(const float* __restrict__ logits, int planes,
                                                       const uint64_t* __restrict__ keys_in, int n,
                                                       uint64_t* __restrict__ out) {
+    const size_t stride = (size_t)gridDim.y * n;
     __shared__ uint64_t red[256];
     const int row = blockIdx.y;
     const int base = blockIdx.x * TOPK_CH;
@@ -1291,7 +1379,8 @@ __global__ __launch_bounds__(256) void k_argmax_stage(const float* __restrict__ 
     for (int k = threadIdx.x; k < TOPK_CH; k += 256) {
         const int i = base + k;
         if (i >= n) break;
-        const uint64_t key = logits ? topk_key(logits[(size_t)row * n + i], (uint32_t)i) : keys_in[(size_t)row * n + i];
+        const uint64_t key = logits ? topk_key(plane_sum(logits, planes, stride, (size_t)row * n + i), (uint32_t)i)
+                                    : keys_in[(size_t)row * n + i];
         best = key > best ? key : best;
     }
     red[threadIdx.x] = best;
@@ -1303,8 +1392,8 @@ __global__ __launch_bounds__(256) void k_argmax_stage(const float* __restrict__ 
     if (threadIdx.x == 0) out[(size_t)row * gridDim.x + blockIdx.x] = red[0];
 }
 
-void launch_topk(hipStream_t st, const float* logits, int rows, int V, int M, uint64_t* a, uint64_t* b,
-                 float* vals, uint32_t* ids) {
+void launch_topk(hipStream_t st, const float* logits, int planes, int rows, int V, int M, uint64_t* a,
+                 uint64_t* b, float* vals, uint32_t* ids) {
     if (M == 1) {
         int n = V;
         const float* lg = logits;
@@ -1313,7 +1402,7 @@ void launch_topk(hipStream_t st, const float* logits, int rows, int V, int M, ui
         uint64_t* other = b;
         for (;;) {
             const int groups = (n + TOPK_CH - 1) / TOPK_CH;
-            hipLaunchKernelGGL(k_argmax_stage, dim3(groups, rows), dim3(256), 0, st, lg, in, n, out);
+            hipLaunchKernelGGL(k_argmax_stage, dim3(groups, rows), dim3(256), 0, st, lg, planes, in, n, out);
             CHECK_LAUNCH();
             if (groups == 1) break;
             lg = nullptr;
@@ -1334,7 +1423,7 @@ void launch_topk(hipStream_t st, const float* logits, int rows, int V, int M, ui
     uint64_t* other = b;
     for (;;) {
         const int groups = (n + TOPK_CH - 1) / TOPK_CH;
-        hipLaunchKernelGGL(k_topk_stage, dim3(groups, rows), dim3(256), 0, st, lg, in, n, M, out);
+        hipLaunchKernelGGL(k_topk_stage, dim3(groups, rows), dim3(256), 0, st, lg, planes, in, n, M, out);
         CHECK_LAUNCH();
         if (groups == 1) break;
         lg = nullptr;
@@ -1418,8 +1507,8 @@ void launch_release_pages(hipStream_t st, int slot, int owned, uint32_t* free_st
 // `row_tile0` of w (fused tensors stack their row tiles). Codes
 // clamp(round(N(0,40)), ±127) from the Irwin-Hall generator at index n*K + k;
 // f16 scales ~U(1e-4, 4e-4) at index n*ng + g in stream ^ 0x5ca1e.
-__global__ void k_gen_q8(uint8_t* __restrict__ codes, uint16_t* __restrict__ scales, int KU, int row_tile0,
-                         int N, int K, uint64_t seed, uint64_t stream) {
+__global__ void k_gen_q8(uint8_t* __restrict__ rec, int Nt, int KU, int P, int row_tile0, int N, int K,
+                         uint64_t seed, uint64_t stream) {
     const int tiles = (N + 15) / 16;
     const int64_t total = (int64_t)tiles * KU * 64;
     const int ng = (K + 31) / 32;
@@ -1429,6 +1518,8 @@ __global__ void k_gen_q8(uint8_t* __restrict__ codes, uint16_t* __restrict__ sca
         const int64_t tu = i >> 6;
         const int u = (int)(tu % KU), t = (int)(tu / KU);
         const int n = 16 * t + (lane & 15);
+        const int tg = row_tile0 + t;
+        uint8_t* r = rec + lx_record(tg, u, KU, P, Nt);
         uint8_t b[16];
 #pragma unroll
         for (int j = 0; j < 16; j++) {
@@ -1437,7 +1528,7 @@ __global__ void k_gen_q8(uint8_t* __restrict__ codes, uint16_t* __restrict__ sca
             if (n < N && k < K) q = gen_code(cc_rng(seed, stream, (uint64_t)n * K + k));
             b[j] = (uint8_t)((q & 0xff) ^ 0x80);
         }
-        uint8_t* dst = codes + ((((size_t)(row_tile0 + t)) * KU + u) * 64 + lane) * 16;
+        uint8_t* dst = r + (tg & 1) * 1024 + lane * 16;
 #pragma unroll
         for (int j = 0; j < 16; j++) dst[j] = b[j];
         if (lane < 16) {
@@ -1445,7 +1536,7 @@ __global__ void k_gen_q8(uint8_t* __restrict__ codes, uint16_t* __restrict__ sca
                 const int gg = 2 * u + h;
                 uint16_t sbits = 0;
                 if (n < N && gg < ng) sbits = gen_scale_f16(seed, stream ^ 0x5ca1eull, (uint64_t)n * ng + gg, 1e-4, 4e-4);
-                scales[(((size_t)(row_tile0 + t)) * KU + u) * 32 + lane * 2 + h] = sbits;
+                *(uint16_t*)(r + 2048 + lane * 8 + (tg & 1) * 4 + h * 2) = sbits;
             }
         }
     }
@@ -1456,14 +1547,14 @@ void launch_gen_q8(hipStream_t st, const QTensor& w, int row_tile0, int N, int K
     const int64_t total = (int64_t)((N + 15) / 16) * w.KU * 64;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(k_gen_q8, dim3((unsigned)blocks), dim3(256), 0, st, w.codes, w.scales, w.KU, row_tile0,
+    hipLaunchKernelGGL(k_gen_q8, dim3((unsigned)blocks), dim3(256), 0, st, w.codes, w.Nt, w.KU, w.P, row_tile0,
                        N, K, seed, stream);
     CHECK_LAUNCH();
 }
 
-// Host int8 [N, K] codes + f16 scales [N, ceil(K/group)] (group 32) -> tiled.
+// Host int8 [N, K] codes + f16 scales [N, ceil(K/group)] (group 32) -> records.
 __global__ void k_tile_q8(const int8_t* __restrict__ src, const uint16_t* __restrict__ sc, int N, int K,
-                          uint8_t* __restrict__ codes, uint16_t* __restrict__ scales, int KU, int row_tile0) {
+                          uint8_t* __restrict__ rec, int Nt, int KU, int P, int row_tile0) {
     const int tiles = (N + 15) / 16;
     const int64_t total = (int64_t)tiles * KU * 64;
     const int ng = (K + 31) / 32;
@@ -1473,7 +1564,9 @@ __global__ void k_tile_q8(const int8_t* __restrict__ src, const uint16_t* __rest
         const int64_t tu = i >> 6;
         const int u = (int)(tu % KU), t = (int)(tu / KU);
         const int n = 16 * t + (lane & 15);
-        uint8_t* dst = codes + ((((size_t)(row_tile0 + t)) * KU + u) * 64 + lane) * 16;
+        const int tg = row_tile0 + t;
+        uint8_t* r = rec + lx_record(tg, u, KU, P, Nt);
+        uint8_t* dst = r + (tg & 1) * 1024 + lane * 16;
         for (int j = 0; j < 16; j++) {
             const int k = 64 * u + 32 * (j >> 3) + 8 * (lane >> 4) + (j & 7);
             const int q = (n < N && k < K) ? src[(size_t)n * K + k] : 0;
@@ -1482,7 +1575,7 @@ __global__ void k_tile_q8(const int8_t* __restrict__ src, const uint16_t* __rest
         if (lane < 16)
             for (int h = 0; h < 2; h++) {
                 const int gg = 2 * u + h;
-                scales[(((size_t)(row_tile0 + t)) * KU + u) * 32 + lane * 2 + h] =
+                *(uint16_t*)(r + 2048 + lane * 8 + (tg & 1) * 4 + h * 2) =
                     (n < N && gg < ng) ? sc[(size_t)n * ng + gg] : (uint16_t)0;
             }
     }
@@ -1494,8 +1587,8 @@ void launch_tile_q8(hipStream_t st, const int8_t* codes, const uint16_t* scales,
     const int64_t total = (int64_t)((N + 15) / 16) * w.KU * 64;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(k_tile_q8, dim3((unsigned)blocks), dim3(256), 0, st, codes, scales, N, K, w.codes,
-                       w.scales, w.KU, row_tile0);
+    hipLaunchKernelGGL(k_tile_q8, dim3((unsigned)blocks), dim3(256), 0, st, codes, scales, N, K, w.codes, w.Nt,
+                       w.KU, w.P, row_tile0);
     CHECK_LAUNCH();
 }
 
