@@ -811,10 +811,16 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
     if (at < ctx->o.lo || at >= ctx->o.hi || to <= at || to > ctx->o.hi)
         return bad(-1, "positions " + std::to_string(at) + ".." + std::to_string(to) + " are not held here");
     const bool gather = at == 0;
-    const bool head = to == positions;
+    // A pass to the end of the line samples its jobs' `sampled` rows; with
+    // none (a prefill chunk's fill or a replay, web/model/stage.js:1219-1222)
+    // it only writes the caches and runs no LM head.
+    const bool at_end = to == positions;
+    int S_all = 0;
+    for (int j = 0; j < njobs && jobs; j++) S_all += at_end ? std::max(0, jobs[j].sampled) : 0;
+    const bool head = at_end && S_all > 0;
     if (head && (topk < 1 || topk > TOPK_MAX)) return bad(-1, "topk must be 1..256");
     if (head && (!top_vals || !top_ids)) return bad(-1, "a pass to the head needs top_vals and top_ids");
-    if (!head && !hidden_out) return bad(-1, "a pass that stops before the head needs hidden_out");
+    if (!at_end && !hidden_out) return bad(-1, "a pass that stops before the head needs hidden_out");
     int T = 0;
     std::vector<char> seen(ctx->owned.size(), 0);
     // #prepare's checks (web/model/stage.js:1225-1259).
@@ -835,7 +841,8 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         } else if (!jb.hidden) {
             return bad(j, "a job past position 0 needs its hidden rows");
         }
-        if (head && !(jb.sampled == 1 || jb.sampled == jb.n)) return bad(j, "sampled must be 1 or n at the head");
+        if (at_end && !(jb.sampled == 0 || jb.sampled == 1 || jb.sampled == jb.n))
+            return bad(j, "sampled must be 0, 1 or n at the head");
         T += jb.n;
     }
     if (T > ctx->o.t_max) return bad(-1, "the pass has " + std::to_string(T) + " rows, above t_max");
@@ -918,7 +925,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         HIPCHK(hipMemcpyAsync(hout, ctx->d_vals, (size_t)S * topk * 4, hipMemcpyDeviceToHost, st));
         HIPCHK(hipMemcpyAsync((uint8_t*)hout + (size_t)S * topk * 4, ctx->d_ids, (size_t)S * topk * 4,
                               hipMemcpyDeviceToHost, st));
-    } else {
+    } else if (!at_end) {
         launch_to_half_bits(st, ctx->x, (int64_t)T * d.hidden, ctx->d_hbits);
         HIPCHK(hipMemcpyAsync(hout, ctx->d_hbits, (size_t)T * d.hidden * 2, hipMemcpyDeviceToHost, st));
     }
@@ -934,7 +941,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
     if (head) {
         std::memcpy(top_vals, hout, (size_t)p.S * topk * 4);
         std::memcpy(top_ids, (uint8_t*)hout + (size_t)p.S * topk * 4, (size_t)p.S * topk * 4);
-    } else {
+    } else if (!at_end) {
         std::memcpy(hidden_out, hout, (size_t)T * d.hidden * 2);
     }
     return CC_OK;

@@ -1,0 +1,275 @@
+'use strict';
+// The JS Runner's host policy against the reference's expectations
+// (tools/stage.test.mjs, web/dev/batch.test.js), on the CPU stub backend.
+// Run: node tests/node/runner.test.js (exit status 0 when every case passes).
+
+const assert = require('assert');
+const { Runner, MAX_QUEUE, MAX_SESSION_QUEUE } = require('../../chattorrent_amd/node/runner');
+const { StubBackend } = require('./stub_backend');
+const { toF16, fromF16 } = require('../../chattorrent_amd/node/f16');
+const S = require('../../chattorrent_amd/node/sampling');
+
+const D = { hidden: 8, n_layer: 2, n_heads: 2, n_kv_heads: 1, head_dim: 64, ffn: 32, vocab: 101 };
+const END = D.n_layer + 2;
+
+function make(o) {
+    const opts = Object.assign({ lo: 0, hi: END, nMax: 512, tMax: 16, slots: 2, sessions: 2, idleMs: 50,
+                                 waitMs: 200, batchRows: 16 }, o || {});
+    const be = new StubBackend(D, { nMax: opts.nMax, slots: opts.slots, frames: opts.sessions + 1, tMax: opts.tMax,
+                                    delayMs: opts.delayMs });
+    return { r: new Runner(be, D, opts), be };
+}
+const job = (s, extra) => Object.assign({ k: 'job', s, pos: 0, past: 0, n: 1, ids: [5], opts: { temp: 0 } }, extra);
+const sleep = (ms) => new Promise((res) => setTimeout(res, ms));
+const rejects = async (p, re) => {
+    try { await p; } catch (e) {
+        if (re && !re.test(e.message)) throw new Error(`wrong error: ${e.message}`);
+        return e;
+    }
+    throw new Error('expected a rejection');
+};
+
+const cases = [];
+const test = (name, fn) => cases.push({ name, fn });
+
+test('greedy decode at the head returns the stub model argmax', async () => {
+    const { r, be } = make();
+    const out = await r.run(job('a', { ids: [3] }));
+    assert.strictEqual(out.at, END);
+    const want = (0 + END) * 7 + 3;
+    assert.strictEqual(out.token, want % D.vocab);
+    assert.strictEqual(be.calls.length, 1);
+    assert.deepStrictEqual(be.calls[0].jobs[0], { slot: be.calls[0].jobs[0].slot, past: 0, n: 1, sampled: 1 });
+});
+
+test('queued jobs with the same cursor share one pass, in order, one per session', async () => {
+    const { r, be } = make({ sessions: 4, slots: 4, delayMs: 20 });
+    const first = r.run(job('a'));
+    await sleep(1);   // a's pass is running: the next jobs queue behind it
+    const ps = [r.run(job('b')), r.run(job('c')), r.run(job('b', { past: 1, ids: [6] })), r.run(job('d'))];
+    await Promise.all([first].concat(ps));
+    assert.strictEqual(be.calls.length, 3);
+    assert.strictEqual(be.calls[1].jobs.length, 3);   // b, c, d; b's second job waits
+    assert.strictEqual(be.calls[2].jobs.length, 1);
+    assert.strictEqual(r.counts.batched, 1);
+    assert.strictEqual(r.counts.batchedJobs, 3);
+});
+
+test('prefill chunks, replays and other cursors do not join a batch', async () => {
+    const { r, be } = make({ sessions: 4, slots: 4, delayMs: 20 });
+    const first = r.run(job('a'));
+    await sleep(1);
+    const ps = [r.run(job('b')), r.run(job('c', { fill: true, n: 2, ids: [1, 2] })),
+                r.run(job('d', { pos: 1, ids: undefined }), new Uint16Array(D.hidden))];
+    await Promise.all([first].concat(ps));
+    assert.deepStrictEqual(be.calls.map((c) => c.jobs.length), [1, 1, 1, 1]);
+});
+
+test('batchRows caps the rows of a pass', async () => {
+    const { r, be } = make({ sessions: 4, slots: 4, delayMs: 20, batchRows: 3 });
+    const first = r.run(job('a'));
+    await sleep(1);
+    const ps = [r.run(job('b', { n: 2, ids: [1, 2] })), r.run(job('c', { n: 2, ids: [1, 2] })), r.run(job('d'))];
+    await Promise.all([first].concat(ps));
+    assert.deepStrictEqual(be.calls.map((c) => c.jobs.map((j) => j.n)), [[1], [2, 1], [2]]);
+});
+
+test('busy at MAX_SESSION_QUEUE jobs of one session and MAX_QUEUE sessions', async () => {
+    const { r } = make({ delayMs: 5, sessions: 2, slots: 2 });
+    const ps = [];
+    for (let i = 0; i < MAX_SESSION_QUEUE; i++) ps.push(r.run(job('a', { past: i })).catch(() => null));
+    const e = await rejects(r.run(job('a', { past: 9 })), /no queue slot free/);
+    assert.strictEqual(e.busy, true);
+    for (let i = 1; i < MAX_QUEUE; i++) ps.push(r.run(job('s' + i)).catch(() => null));
+    const e2 = await rejects(r.run(job('late')), /queue slot/);
+    assert.strictEqual(e2.busy, true);
+    await Promise.all(ps);
+});
+
+test('a job past 0 for a session without a frame is cold; after a refusal it is busy', async () => {
+    const { r } = make();
+    const e = await rejects(r.run(job('x', { past: 3 })), /session x is no longer cached here/);
+    assert.ok(!e.busy);
+    r.refused.set('y', Number(process.hrtime.bigint()) / 1e6);
+    const e2 = await rejects(r.run(job('y', { past: 3 })), /refused here for capacity/);
+    assert.strictEqual(e2.busy, true);
+});
+
+test('a rewind is allowed, a skip ahead is cold, and a closed-loop duplicate is stale', async () => {
+    const { r } = make();
+    await r.run(job('a', { n: 3, ids: [1, 2, 3] }));
+    await r.run(job('a', { past: 1, n: 2, ids: [4, 5] }));        // rewind to 1
+    await rejects(r.run(job('a', { past: 7 })), /block 0 holds 3 rows, the job continues from 7/);
+    const e = await rejects(r.run(job('a', { past: 2, auto: true })), /a duplicate of session a's job at 2/);
+    assert.strictEqual(e.stale, true);
+});
+
+test('an idle session is evicted for a new one; with none idle and no wait the job is busy', async () => {
+    const { r } = make({ sessions: 1, slots: 1, idleMs: 30, waitMs: 0 });
+    await r.run(job('a'));
+    const e = await rejects(r.run(job('b')), /no session free/);
+    assert.strictEqual(e.busy, true);
+    await sleep(40);
+    await r.run(job('b'));
+    assert.strictEqual(r.counts.evicted, 1);
+    await rejects(r.run(job('a', { past: 1 })), /session a is no longer cached here/);
+});
+
+test('a waiting session is admitted when a frame is released, in arrival order', async () => {
+    const { r } = make({ sessions: 1, slots: 1, idleMs: 10000, waitMs: 1000 });
+    await r.run(job('a'));
+    const pb = r.run(job('b'));
+    const pc = r.run(job('c'));
+    await sleep(20);
+    assert.strictEqual(r.waiting.length, 2);
+    await r.release('a');
+    const b = await pb;
+    assert.strictEqual(b.at, END);
+    await r.release('b');
+    await pc;
+    assert.strictEqual(r.counts.waited, 2);
+});
+
+test('waiting past the deadline is a capacity refusal', async () => {
+    const { r } = make({ sessions: 1, slots: 1, idleMs: 10000, waitMs: 30 });
+    await r.run(job('a'));
+    const e = await rejects(r.run(job('b')), /no session free/);
+    assert.strictEqual(e.busy, true);
+});
+
+test('KV pages: a context larger than a frame is a configuration error', async () => {
+    const { r } = make({ nMax: 128, tMax: 16 });
+    await r.run(job('a', { n: 16, ids: new Array(16).fill(1) }));
+    await rejects(r.run(job('a', { past: 120, n: 16, ids: new Array(16).fill(1) })), /context 136 exceeds 128/);
+});
+
+test('KV pages: page pressure evicts an idle session whole', async () => {
+    // two frames, pool of one context (2 pages); b needs a page a holds
+    const { r, be } = make({ nMax: 128, tMax: 16, slots: 1, sessions: 2, idleMs: 20 });
+    for (let past = 0; past < 64; past += 16) await r.run(job('a', { past, n: 16, ids: new Array(16).fill(1) }));
+    await r.run(job('a', { past: 64, n: 1 }));
+    assert.strictEqual(be.freePages(), 0);
+    await sleep(30);
+    await r.run(job('b', { n: 16, ids: new Array(16).fill(2) }));
+    assert.strictEqual(r.counts.evicted, 1);
+    assert.strictEqual(be.slotPages(0) + be.slotPages(1), 1);
+});
+
+test('job checks and their messages (stage.js #prepare)', async () => {
+    const { r } = make();
+    await rejects(r.run(job('a', { n: 0, ids: [] })), /a job of 0 tokens is outside 1–16/);
+    await rejects(r.run(job('a', { n: 17, ids: new Array(17).fill(0) })), /outside 1–16/);
+    await rejects(r.run(job('a', { past: -1 })), /past -1 is not a position/);
+    await rejects(r.run(job('a', { past: 600 })), /context 601 exceeds 512/);
+    await rejects(r.run(job('a', { ids: [1, 2] })), /a job at position 0 needs 1 token ids/);
+    await rejects(r.run(job('a', { pos: 1, ids: undefined }), new Uint16Array(3)), /payload is 3 floats, expected 8/);
+    await rejects(r.run(job('a', { pos: 9 })), /position 9 is not held here/);
+    await rejects(r.run(job('a', { n: 2, ids: [1, 2], drafts: [1, 2] })), /a verify job needs 1–7 draft ids/);
+    await rejects(r.run(job('a', { fill: true, drafts: [1] })), /a prefill chunk cannot carry drafts/);
+});
+
+test('verify: drafts accepted while the sample matches, stop at the first mismatch', async () => {
+    const { r } = make();
+    const V = D.vocab;
+    const best = (pos, x) => (pos * 7 + x) % V;
+    // row i sits at position i, input ids[i]; the stub adds the positions crossed
+    const ids = [3, 0, 0, 0];
+    ids[1] = best(0 + END, ids[0]);
+    ids[2] = best(1 + END, ids[1]);
+    ids[3] = (best(2 + END, ids[2]) + 1) % V;   // this draft is wrong
+    const out = await r.run(job('v', { n: 4, ids, drafts: ids.slice(1) }));
+    assert.deepStrictEqual(out.tokens, [ids[1], ids[2], best(2 + END, ids[2])]);
+    assert.strictEqual(out.token, best(2 + END, ids[2]));
+});
+
+test('a pass that stops before the head hands f16 rows on and keeps the boundary log', async () => {
+    const { r } = make();
+    const out = await r.run(job('h', { n: 2, ids: [4, 9] }), null, 2);
+    assert.strictEqual(out.at, 2);
+    assert.ok(out.hidden instanceof Uint16Array);
+    assert.deepStrictEqual(Array.from(fromF16(out.hidden.subarray(0, 1))), [6]);
+    const log = r.logs.get('h').get(2);
+    assert.strictEqual(log.len, 2);
+    assert.deepStrictEqual(log.rows.subarray(0, 2 * D.hidden), out.hidden);
+});
+
+test('a prefill chunk at the end fills the caches and samples nothing', async () => {
+    const { r, be } = make();
+    const out = await r.run(job('f', { fill: true, n: 3, ids: [1, 2, 3] }));
+    assert.strictEqual(out.filled, true);
+    assert.strictEqual(be.calls[0].jobs[0].sampled, 0);
+});
+
+test('release is idempotent and rejects the session\'s waiting jobs', async () => {
+    const { r } = make({ sessions: 1, slots: 1, idleMs: 10000, waitMs: 1000 });
+    await r.run(job('a'));
+    const pb = r.run(job('b'));
+    await sleep(10);
+    await r.release('b');
+    await rejects(pb, /session b ended while it waited for a frame/);
+    await r.release('zzz');
+    await r.release('a');
+    assert.strictEqual(r.counts.released, 1);
+});
+
+test('temp > 0 without top-k reads whole logits rows', async () => {
+    const { r, be } = make();
+    const out = await r.run(job('t', { opts: { temp: 0.7 } }));
+    assert.strictEqual(be.calls[0].topk, 1);
+    assert.ok(Number.isInteger(out.token));
+});
+
+test('sampler: a row drawn from its GPU candidates equals the whole-row draw', async () => {
+    let seed = 12345;
+    const rnd = () => ((seed = (seed * 1103515245 + 12345) % 2147483648) / 2147483648);
+    const V = 500;
+    for (let t = 0; t < 300; t++) {
+        const row = new Float32Array(V).map(() => (rnd() * 20) - 10);
+        const optsList = [{ temp: 0 }, { temp: 0.8, topK: 40 }, { temp: 1.2, topK: 5, rep: 1.3, pen: [[3, 2], [7, 1]], ban: [11] },
+                          { temp: 0, freq: 0.5, pen: [[row.indexOf(Math.max.apply(null, row)), 3]] }];
+        for (const opts of optsList) {
+            const M = S.candidatesFor(opts, V);
+            assert.ok(M !== null);
+            const order = Array.from(row.keys()).sort((a, b) => row[b] - row[a] || a - b).slice(0, M);
+            const r0 = rnd();
+            const whole = S.sampleFromLogitsRow(row, opts, () => r0);
+            const cand = S.sampleFromCandidates(order, order.map((i) => row[i]), opts, V, () => r0);
+            assert.strictEqual(cand, whole, JSON.stringify(opts));
+        }
+    }
+    assert.strictEqual(S.candidatesFor({ temp: 1 }, V), null);
+    // topK clamps to 200; 200 + 60 banned ids is past TOPK_MAX
+    assert.strictEqual(S.candidatesFor({ temp: 1, topK: 250, ban: new Array(10).fill(0).map((_, i) => i) }, V), 210);
+    assert.strictEqual(S.candidatesFor({ temp: 1, topK: 200, ban: new Array(60).fill(0).map((_, i) => i) }, V), null);
+});
+
+test('f16 hand-off: every half round-trips, ties go to even, ±65504 clamps', async () => {
+    const all = new Uint16Array(65536).map((_, i) => i);
+    const vals = fromF16(all);
+    const back = toF16(vals);
+    for (let h = 0; h < 65536; h++) {
+        const e = (h >>> 10) & 0x1f, m = h & 0x3ff;
+        if (e === 0x1f && m) { assert.strictEqual(back[h] & 0x7e00, 0x7e00); continue; }
+        if (e === 0x1f) { assert.strictEqual(back[h], (h & 0x8000) | 0x7bff); continue; }
+        assert.strictEqual(back[h], h);
+    }
+    assert.strictEqual(toF16([1 + Math.pow(2, -11)])[0], 0x3c00);            // tie to even (down)
+    assert.strictEqual(toF16([1 + 3 * Math.pow(2, -11)])[0], 0x3c02);        // tie to even (up)
+    assert.strictEqual(toF16([1e9])[0], 0x7bff);
+    assert.strictEqual(toF16([-1e9])[0], 0xfbff);
+});
+
+(async () => {
+    let failed = 0;
+    for (const c of cases) {
+        try {
+            await c.fn();
+            console.log(`ok   ${c.name}`);
+        } catch (e) {
+            failed++;
+            console.log(`FAIL ${c.name}\n     ${e && e.stack ? e.stack.split('\n').slice(0, 3).join('\n     ') : e}`);
+        }
+    }
+    console.log(`${cases.length - failed}/${cases.length} passed`);
+    process.exit(failed ? 1 : 0);
+})();

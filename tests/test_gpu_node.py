@@ -1,0 +1,45 @@
+"""The Node host on the GPU: the JS Runner over the N-API addon decodes the
+same greedy tokens as the C ABI driven directly, whole and split across two
+Runners at a block boundary (f16 hand-off)."""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from chattorrent_amd import configs
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+NODE = shutil.which("node")
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+def test_node_runner_matches_c_abi(gpu):
+    from chattorrent_amd.ccdecode import Context
+    d = configs.with_layers(configs.SMOLLM2, 4)
+    rng = np.random.default_rng(7)
+    chats = [rng.integers(0, d["vocab"], n).tolist() for n in (5, 9, 3)]
+    cfg = {"dims": d, "seed": 11, "nMax": 256, "tMax": 32, "chats": chats, "steps": 4, "cut": 3}
+    print("[node] running tests/node/native_pass.js", flush=True)
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "native_pass.js"), json.dumps(cfg)], cwd=ROOT,
+                       stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    # The same decode through the C ABI from Python, every chat in one pass.
+    c = Context(d, n_max=256, t_max=32, slots=3)
+    c.fill_random(11)
+    _, ids = c.step([{"slot": i, "past": 0, "n": len(p), "ids": p, "sampled": 1} for i, p in enumerate(chats)])
+    hist = [[int(ids[i, 0])] for i in range(len(chats))]
+    past = [len(p) for p in chats]
+    for _ in range(cfg["steps"]):
+        _, ids = c.step([{"slot": i, "past": past[i], "n": 1, "ids": [hist[i][-1]], "sampled": 1}
+                         for i in range(len(chats))])
+        for i in range(len(chats)):
+            hist[i].append(int(ids[i, 0]))
+            past[i] += 1
+    assert out["whole"] == hist
+    assert out["split"] == hist
+    assert out["batched"] >= 1
