@@ -89,7 +89,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: every box here has one GPU and this build has no multi-GPU path "
-              "(a data-parallel replica per GPU would need no exchange; see DESIGN.md).", file=sys.stderr)
+              "(the pass would scale as one data-parallel replica per GPU, with no exchange).", file=sys.stderr)
         sys.exit(2)
 
     from chattorrent_amd import configs
@@ -152,7 +152,7 @@ def main():
     achieved = g_b / (g_ms / 1000.0) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_gemm_q8 (all q8 projections + LM head)",
+            "kernel": "k_gemm_lx (all q8 projections + LM head)",
             "avg_launch_us": round(g_ms * 1000.0 / max(g_n, 1), 2),
             "bytes_per_launch": round(g_b / max(g_n, 1)),
             "per_kind": {k: {"ms_per_step": round(v[0] / args.steps, 4), "launches": v[1],
@@ -167,7 +167,7 @@ def main():
         "metric": "aggregate decode tok/s @32 ragged chats, 27B q8; % of HBM roofline",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8 weights x f32 activations (f16 hi/lo MFMA), f32 accumulate",
+        "dtype": "int8xf32",
         "data": "synthetic: random-init q8 weights, random int8 KV, seeded contexts",
         "config": {"workload": "configs[2]: 27B-class q8 (64 layers, d5120, 40/8 heads, ffn 17408, vocab 151936), "
                                "32 chats, contexts log-uniform [128,16384], greedy decode, one packed pass per step",

@@ -26,6 +26,12 @@ const BATCH_ROWS = 32;           // kernels.js GEMV_ROWS_MAX, the reference's de
 const LOG_CHUNK = 256;           // stage.js:34
 const WARMUP = '\0warmup';       // stage.js:31
 
+// cc_upload tensor ids (include/ccdecode.h) by HF tensor name.
+const TENSOR = { q_proj: 0, k_proj: 1, v_proj: 2, o_proj: 3, gate_proj: 4, up_proj: 5, down_proj: 6,
+                 input_layernorm: 7, post_attention_layernorm: 8, wte: 9, norm: 10, lm_head: 11 };
+const BLOCK_TENSORS = ['q_proj', 'k_proj', 'v_proj', 'o_proj', 'gate_proj', 'up_proj', 'down_proj',
+                       'input_layernorm', 'post_attention_layernorm'];
+
 // Thrown by _cacheFor for a job that must wait for a frame; never escapes.
 const WAIT = new Error('waiting for a session frame');
 
@@ -98,6 +104,35 @@ class Runner {
     }
 
     holds(pos) { return pos >= this.lo && pos < this.have; }
+
+    // append(weights) — stage.js:446-468: load position `have`. `weights`
+    // holds host tensors by their HF names: q8 ones as {codes: Int8Array
+    // [N*K], scales: Uint16Array (f16 bits) or Float32Array [N*ceil(K/32)]},
+    // norms as Float32Array. Position 0 needs wte; the last, norm (and
+    // lm_head when untied); a block, its seven projections and two norms.
+    append(weights) {
+        const p = this.have;
+        const w = weights || {};
+        if (p >= this.hi) throw new Error(`nothing left to append: ${this.lo}–${this.hi - 1} is full`);
+        const up = (layer, id, t) => this.backend.upload(layer, id, t.codes || t, t.codes ? t.scales : null);
+        if (p === 0) {
+            if (!w.wte) throw new Error('position 0 is the embedding and needs wte');
+            up(-1, TENSOR.wte, w.wte);
+        } else if (p === positions(this.d.n_layer) - 1) {
+            if (!w.norm) throw new Error('the last position is the head and needs norm');
+            up(-1, TENSOR.norm, w.norm);
+            if (w.lm_head) up(-1, TENSOR.lm_head, w.lm_head);
+            else if (w.wte) up(-1, TENSOR.wte, w.wte);
+        } else {
+            if (!w.q_proj) throw new Error(`position ${p} is a block and needs its tensors`);
+            for (const name of BLOCK_TENSORS) {
+                if (!w[name]) throw new Error(`position ${p} is a block and needs ${name}`);
+                up(p - 1, TENSOR[name], w[name]);
+            }
+        }
+        this.have = p + 1;
+        return this.have;
+    }
 
     get vramBytes() { return this.backend.stats().vramBytes; }
 

@@ -219,6 +219,28 @@ test('temp > 0 without top-k reads whole logits rows', async () => {
     assert.ok(Number.isInteger(out.token));
 });
 
+test('append loads one position at a time and moves `have`', async () => {
+    const { r, be } = make({ have: 0 });
+    assert.strictEqual(r.holds(0), false);
+    assert.throws(() => r.append({}), /position 0 is the embedding and needs wte/);
+    const q8 = (n) => ({ codes: new Int8Array(n), scales: new Uint16Array(n / 32) });
+    r.append({ wte: q8(64) });
+    assert.strictEqual(r.holds(0), true);
+    assert.throws(() => r.append({ wte: q8(64) }), /position 1 is a block and needs its tensors/);
+    const block = { q_proj: q8(64), k_proj: q8(64), v_proj: q8(64), o_proj: q8(64), gate_proj: q8(64),
+                    up_proj: q8(64), down_proj: q8(64), input_layernorm: new Float32Array(8),
+                    post_attention_layernorm: new Float32Array(8) };
+    r.append(block);
+    r.append(block);
+    assert.throws(() => r.append({}), /the last position is the head and needs norm/);
+    assert.strictEqual(r.append({ norm: new Float32Array(8) }), END);
+    assert.throws(() => r.append({}), /nothing left to append: 0–3 is full/);
+    assert.deepStrictEqual(be.uploads.map((u) => [u.layer, u.tensor]),
+        [[-1, 9]].concat([0, 1].flatMap((l) => [0, 1, 2, 3, 4, 5, 6, 7, 8].map((t) => [l, t]))).concat([[-1, 10]]));
+    const out = await r.run(job('a'));
+    assert.strictEqual(out.at, END);
+});
+
 test('sampler: a row drawn from its GPU candidates equals the whole-row draw', async () => {
     let seed = 12345;
     const rnd = () => ((seed = (seed * 1103515245 + 12345) % 2147483648) / 2147483648);

@@ -17,6 +17,7 @@ class StubBackend {
         this.owned = new Array(o.frames).fill(0);
         this.tMax = o.tMax;
         this.calls = [];
+        this.uploads = [];
         this.busy = false;
         this.lastLogits = null;
         this.delayMs = o.delayMs || 0;
@@ -78,6 +79,8 @@ class StubBackend {
         inputs.forEach((r, k) => hidden.fill(r.x + (to - at), k * H, (k + 1) * H));
         return done({ code: 0, status, hidden: toF16(hidden) });
     }
+
+    upload(layer, tensor, data, scales) { this.uploads.push({ layer, tensor, n: data.length, ns: scales ? scales.length : 0 }); }
 
     release(slot) {
         this.freeCount += this.owned[slot];
