@@ -768,10 +768,10 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
         launch_fin_qkv(st, ctx->part, sq, T, drow_job, djobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
                        L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 1);
         e = prof_begin(ctx);
-        launch_attn2(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
+        launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
                      ctx->ppw, ctx->apart);
         prof_end(ctx, e, CC_K_ATTN, p.kv_bytes);
-        launch_attn_combine2(st, djobs, (int)p.jobs.size(), ditems, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU,
+        launch_attn_combine(st, djobs, (int)p.jobs.size(), ditems, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU,
                              ctx->xp_o, nullptr, dcwg, p.ncwg);
         const int so = L.o.P;
         e = prof_begin(ctx);
@@ -1135,9 +1135,9 @@ cc_status cc_op_attend(cc_ctx* ctx, int32_t layer, int32_t slot, const float* q,
     const AttnItem* di = (const AttnItem*)(ctx->d_meta + ml.items);
     launch_fin_qkv(st, dr, 1, n, (const int32_t*)(ctx->d_meta + ml.row_job), dj, d.n_heads, ctx->group, ctx->geom,
                    ctx->tbl, ctx->rot, L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 0);
-    launch_attn2(st, di, p.nitems, dj, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->ppw,
+    launch_attn(st, di, p.nitems, dj, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->ppw,
                  ctx->apart);
-    launch_attn_combine2(st, dj, 1, di, ctx->apart, ctx->geom, d.n_heads, ctx->group, KU, dXp, dctx,
+    launch_attn_combine(st, dj, 1, di, ctx->apart, ctx->geom, d.n_heads, ctx->group, KU, dXp, dctx,
                          (const int32_t*)(ctx->d_meta + ml.cwg), p.ncwg);
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(take_launch_error());

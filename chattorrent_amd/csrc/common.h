@@ -129,7 +129,12 @@ __device__ static inline half8_t dequant8_signed(uint32_t lo, uint32_t hi) {
 
 // x ≈ hi + lo with hi = f16(x) (nearest-even) and lo = f16(x - hi); the
 // difference x - hi is exact in f32, so hi + lo carries ~22 significant bits.
+// x is made opaque first: when x is a product, the compiler may otherwise fold
+// the multiply into the f16 conversion (v_fma_mix, one rounding) for one use
+// of hi and convert the f32 product (two roundings) for another, and the two
+// differ by an f16 ulp about once in 2^13 values — hi + lo is then off by it.
 __device__ static inline void split_hilo(float x, _Float16& hi, _Float16& lo) {
+    asm("" : "+v"(x));
     hi = (_Float16)x;
     lo = (_Float16)(x - (float)hi);
 }

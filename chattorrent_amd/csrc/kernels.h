@@ -56,22 +56,12 @@ size_t lx_cut_floats(int M, int ncu);
 int lx_groups(const QTensor& w, int ncu);
 void launch_prep_rows(hipStream_t st, const float* x, int ldx, int M, int Mpad, int K, int KU,
                       uint4* Xp);
-void launch_rmsnorm_prep(hipStream_t st, const float* x, const int32_t* rows, int M, int Mpad,
-                         int H, int KU, const float* w, float eps, uint4* Xp, float* y);
-void launch_fin_residual(hipStream_t st, float* x, const float* part, int splits, int M, int H,
-                         int round, const float* w, float eps, int KU, uint4* Xp, int Mpad);
 void launch_fin_swiglu(hipStream_t st, const float* part, int splits, int M, int Mpad, int F,
                        int KU, uint4* Xp);
 void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const int32_t* row_job,
                     const JobDev* jobs, int nH, int group, const KVGeom& g, const float* tbl,
                     int rot, uint8_t* kpool, uint8_t* vpool, const uint32_t* page_table,
                     uint4* Qp, float* qkv_out, int do_q, int do_kv);
-void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs,
-                 const uint4* Qp, const uint8_t* kpool, const uint8_t* vpool,
-                 const uint32_t* page_table, const KVGeom& g, int group, float* part);
-void launch_attn_combine(hipStream_t st, const JobDev* jobs, int njobs, const AttnItem* items,
-                         const float* part, const KVGeom& g, int nH, int group, int M, int Mpad,
-                         int KU, uint4* Xp, float* ctx_out);
 void launch_embed(hipStream_t st, const int32_t* ids, const uint16_t* hidden, int T, const QTensor& wte,
                   float* x);
 void launch_topk(hipStream_t st, const float* logits, int planes, int rows, int V, int M, uint64_t* a,
@@ -96,10 +86,10 @@ hipError_t take_launch_error();
 void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const float* part, int splits, int M,
                        int Mpad, int H, int round, const float* w, float eps, int KU, uint4* Xp, float* y,
                        float* ssq);
-void launch_attn2(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
+void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
                   const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
                   int ppw, float* part);
-void launch_attn_combine2(hipStream_t st, const JobDev* jobs, int njobs, const AttnItem* items, const float* part,
+void launch_attn_combine(hipStream_t st, const JobDev* jobs, int njobs, const AttnItem* items, const float* part,
                           const KVGeom& g, int nH, int group, int KU, uint4* Xp, float* ctx_out,
                           const int32_t* wg_job, int nwg);
 void launch_sum_splits(hipStream_t st, const float* part, int splits, int M, int N, float* out);

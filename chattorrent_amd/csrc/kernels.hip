@@ -316,10 +316,8 @@ void launch_prep_rows(hipStream_t st, const float* x, int ldx, int M, int Mpad, 
     CHECK_LAUNCH();
 }
 
-// rmsnorm (web/model/kernels.js:930-976) fused with the operand prep: one
-// workgroup of 256 per row; sum of squares over h = tid, tid+256, ... then a
-// pairwise tree; y = x * (1/sqrt(ss/H + eps)) * w. Rows m >= M write zeros.
-// `rows` (optional) gathers source rows (the head's sampled rows).
+// Sum over a workgroup of 256 as a pairwise tree in LDS (the order the
+// rmsnorm sum of squares, web/model/kernels.js:930-976, is taken in here).
 __device__ static inline float block_sum_256(float v, float* red) {
     red[threadIdx.x] = v;
     __syncthreads();
@@ -332,98 +330,11 @@ __device__ static inline float block_sum_256(float v, float* red) {
     return r;
 }
 
-__global__ __launch_bounds__(256) void k_rmsnorm_prep(const float* __restrict__ x,
-                                                      const int32_t* __restrict__ rows, int M, int H,
-                                                      int KU, const float* __restrict__ w, float eps,
-                                                      uint4* __restrict__ Xp, float* __restrict__ y) {
-    __shared__ float red[256];
-    const int m = blockIdx.x;
-    const int per = 8 * KU;
-    if (m >= M) {
-        const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (Xp) for (int c = threadIdx.x; c < per; c += 256) write_hilo(Xp, m, c, KU, z);
-        return;
-    }
-    const float* xr = x + (size_t)(rows ? rows[m] : m) * H;
-    float ss = 0.0f;
-    for (int h = threadIdx.x; h < H; h += 256) {
-        const float v = xr[h];
-        ss = ss + v * v;
-    }
-    const float tot = block_sum_256(ss, red);
-    const float scale = 1.0f / sqrtf(tot / (float)H + eps);
-    if (y)
-        for (int h = threadIdx.x; h < H; h += 256) y[(size_t)m * H + h] = xr[h] * scale * w[h];
-    if (!Xp) return;
-    for (int c = threadIdx.x; c < per; c += 256) {
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int k = 8 * c + j;
-            v[j] = k < H ? xr[k] * scale * w[k] : 0.0f;
-        }
-        write_hilo(Xp, m, c, KU, v);
-    }
-}
-
-void launch_rmsnorm_prep(hipStream_t st, const float* x, const int32_t* rows, int M, int Mpad, int H,
-                         int KU, const float* w, float eps, uint4* Xp, float* y) {
-    hipLaunchKernelGGL(k_rmsnorm_prep, dim3(Xp ? Mpad : M), dim3(256), 0, st, x, rows, M, H, KU, w, eps,
-                       Xp, y);
-    CHECK_LAUNCH();
-}
-
 // ========================================================= finish kernels ===
-// Residual add (web/model/kernels.js:1334-1346 add_inplace) of the projection
-// (the K splits summed in order), optionally round_f16 (:1356-1383, the
-// per-block residual round, model.js:619-624), then optionally the next
-// rmsnorm (:930-976) and its operand prep. One workgroup per row; the row is
-// kept in LDS between the steps.
-__global__ __launch_bounds__(256) void k_fin_residual(float* __restrict__ x, const float* __restrict__ part,
-                                                      int splits, int M, int H, int round,
-                                                      const float* __restrict__ w, float eps, int KU,
-                                                      uint4* __restrict__ Xp) {
-    extern __shared__ float rowbuf[];
-    __shared__ float red[256];
-    const int m = blockIdx.x;
-    const int per = 8 * KU;
-    if (m >= M) {
-        const float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (Xp) for (int c = threadIdx.x; c < per; c += 256) write_hilo(Xp, m, c, KU, z);
-        return;
-    }
-    float ss = 0.0f;
-    for (int h = threadIdx.x; h < H; h += 256) {
-        float p = part[(size_t)m * H + h];
-        for (int s = 1; s < splits; s++) p = p + part[((size_t)s * M + m) * H + h];
-        float v = x[(size_t)m * H + h] + p;
-        if (round) v = round_f16_value(v);
-        x[(size_t)m * H + h] = v;
-        rowbuf[h] = v;
-        ss = ss + v * v;
-    }
-    if (!Xp) return;
-    const float tot = block_sum_256(ss, red);   // includes the barrier that publishes rowbuf
-    const float scale = 1.0f / sqrtf(tot / (float)H + eps);
-    for (int c = threadIdx.x; c < per; c += 256) {
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int k = 8 * c + j;
-            v[j] = k < H ? rowbuf[k] * scale * w[k] : 0.0f;
-        }
-        write_hilo(Xp, m, c, KU, v);
-    }
-}
-
-void launch_fin_residual(hipStream_t st, float* x, const float* part, int splits, int M, int H, int round,
-                         const float* w, float eps, int KU, uint4* Xp, int Mpad) {
-    hipLaunchKernelGGL(k_fin_residual, dim3(Xp ? Mpad : M), dim3(256), H * sizeof(float), st, x, part,
-                       splits, M, H, round, w, eps, KU, Xp);
-    CHECK_LAUNCH();
-}
-
-// The same residual step spread over the whole chip: grid (column blocks of
+// Residual add (web/model/kernels.js:1334-1346 add_inplace) of a projection,
+// the per-block round_f16 (:1356-1383, model.js:619-624) and the next rmsnorm
+// (:930-976) with its operand prep.
+// Spread over the whole chip: grid (column blocks of
 // 256, rows). Each block adds the projection's K splits in order to its 256
 // residual values (add_inplace), optionally rounds them (round_f16), writes
 // them back and stores its partial sum of squares; k_norm_prep then finishes
@@ -547,7 +458,7 @@ __host__ __device__ static inline int vpos(int s) { return 16 * ((s & 15) >> 2) 
 
 // store_kv (web/model/kernels.js:1024-1073) for a row's K and V, plus RoPE on
 // its Q (kernels.js:1093-1129) into the attention operand, after the q|k|v
-// splits are summed. One workgroup per row; the row sits in LDS.
+// splits are summed.
 // Bit-exact with the reference given the same q|k|v row: RoPE a*cs - o*sn
 // (no fused multiply-add: the build passes -ffp-contract=off), amax,
 // scale = amax/127, inv = scale > 0 ? 1/scale : 0, rint, clamp ±127.
@@ -565,89 +476,12 @@ __device__ static inline float rope_at(const float* src, int c, int rot, const f
     return o * cs + a * sn;
 }
 
-__global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part, int splits, int M,
-                                                 const int32_t* __restrict__ row_job,
-                                                 const JobDev* __restrict__ jobs, int nH, int group,
-                                                 KVGeom g, const float* __restrict__ tbl, int rot,
-                                                 uint8_t* __restrict__ kpool, uint8_t* __restrict__ vpool,
-                                                 const uint32_t* __restrict__ page_table,
-                                                 uint4* __restrict__ Qp, float* __restrict__ qkv_out,
-                                                 int do_q, int do_kv) {
-    extern __shared__ float row[];
-    const int m = blockIdx.x;
-    const int D = g.D, nKV = g.nKV;
-    const int N = (nH + 2 * nKV) * D;
-    for (int e = threadIdx.x; e < N; e += 256) {
-        float p = part[(size_t)m * N + e];
-        for (int s = 1; s < splits; s++) p = p + part[((size_t)s * M + m) * N + e];
-        row[e] = p;
-        if (qkv_out) qkv_out[(size_t)m * N + e] = p;
-    }
-    __syncthreads();
-    const JobDev jb = jobs[row_job[m]];
-    const int i = m - jb.row0;
-    const int pos = jb.past + i;
-
-    // Q: RoPE, then hi/lo fragments [kvh][mtq][g][hl][64] of rows rho = i*group + gi.
-    const int chunks = do_q ? nH * D / 8 : 0;
-    for (int c = threadIdx.x; c < chunks; c += 256) {
-        const int hq = (8 * c) / D, d0 = (8 * c) % D;
-        const float* src = row + hq * D;
-        half8_t hi, lo;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            _Float16 a, b;
-            split_hilo(rope_at(src, d0 + j, rot, tbl, pos), a, b);
-            hi[j] = a;
-            lo[j] = b;
-        }
-        const int kvh = hq / group, gi = hq % group;
-        const int rho = i * group + gi;
-        const int mtq = rho >> 4, lane = (rho & 15) + 16 * ((d0 & 31) >> 3), grp = d0 >> 5;
-        const size_t at = (size_t)jb.qp_off + ((((size_t)kvh * jb.mtq + mtq) * g.ng + grp) * 2) * 64 + lane;
-        Qp[at] = __builtin_bit_cast(uint4, hi);
-        Qp[at + 64] = __builtin_bit_cast(uint4, lo);
-    }
-
-    // K and V: one wave per (head, which); lane l holds d = l + 64q.
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t page = page_table[(size_t)jb.slot * g.max_pages + pos / g.page];
-    const int s = pos % g.page;
-    for (int task = wave; do_kv && task < 2 * nKV; task += 4) {
-        const int n = task >> 1, which = task & 1;
-        const float* src = row + (nH + which * nKV + n) * D;
-        uint8_t* blk = (which ? vpool : kpool) + ((size_t)page * nKV + n) * g.blk;
-        for (int q0 = 0; q0 < D; q0 += 64) {
-            const int d = q0 + lane;
-            const float v = d < D ? (which ? src[d] : rope_at(src, d, rot, tbl, pos)) : 0.0f;
-            float amax = fabsf(v);
-            for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-            const float scale = amax / 127.0f;
-            const float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
-            float q = __builtin_rintf(v * inv);
-            q = fminf(fmaxf(q, -127.0f), 127.0f);
-            if (d < D) {
-                const int8_t code = (int8_t)(int)q;
-                const int b = d >> 5;
-                if (which == 0) {
-                    blk[(size_t)s * D + kpos(d, D)] = (uint8_t)code;
-                    if ((d & 31) == 0) *(float*)(blk + 64 * D + ((size_t)s * g.ng + b) * 4) = scale;
-                } else {
-                    blk[(size_t)d * 64 + vpos(s)] = (uint8_t)code;
-                    if ((d & 31) == 0) *(float*)(blk + 64 * D + ((size_t)b * 64 + vpos(s)) * 4) = scale;
-                }
-            }
-        }
-    }
-}
-
-// The same finish spread over (row, head): one wave per head of a row, four
-// heads per workgroup. The head's D values (K splits summed in order) sit in
-// the wave's LDS slice; Q heads are RoPE'd into the attention operand, K heads
-// RoPE'd and quantised into the pool, V heads quantised — each with exactly
-// the arithmetic above.
+// Spread over (row, head): one wave per head of a row, four heads per
+// workgroup. The head's D values (K splits summed in order) sit in the wave's
+// LDS slice; Q heads are RoPE'd into the attention operand, K heads RoPE'd and
+// quantised into the pool, V heads quantised.
 template <int D>
-__global__ __launch_bounds__(256) void k_fin_qkv2(const float* __restrict__ part, int splits, int M,
+__global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part, int splits, int M,
                                                   const int32_t* __restrict__ row_job,
                                                   const JobDev* __restrict__ jobs, int nH, int group, KVGeom g,
                                                   const float* __restrict__ tbl, int rot, uint8_t* __restrict__ kpool,
@@ -738,10 +572,10 @@ void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const 
     const int nall = nH + 2 * g.nKV;
     dim3 grid((nall + 3) / 4, M);
     if (g.D == 128)
-        hipLaunchKernelGGL(k_fin_qkv2<128>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
+        hipLaunchKernelGGL(k_fin_qkv<128>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
                            rot, kpool, vpool, page_table, Qp, do_q, do_kv);
     else
-        hipLaunchKernelGGL(k_fin_qkv2<64>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
+        hipLaunchKernelGGL(k_fin_qkv<64>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
                            rot, kpool, vpool, page_table, Qp, do_q, do_kv);
     CHECK_LAUNCH();
 }
@@ -749,202 +583,43 @@ void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const 
 // ================================================================ attention ===
 // Ragged GQA attention over each chat's own int8 pages
 // (web/model/kernels.js:1140-1310 qk_scores_gqa, causal_softmax, attn_av_gqa,
-// driven per segment by web/model/model.js:321-351). One work item = (job,
-// kv head, chunk of 4 pages); each wave takes one 64-token page and all the
-// job's query rows rho = i*group + gi of that kv head, so every K/V byte is
-// read once per GQA group:
+// driven per segment by web/model/model.js:321-351). Every K/V byte of a kv
+// head is read once for all the job's query rows rho = i*group + gi of it:
 //   S^T[token][rho] = sum_g sk[token][g] * (K_g . Qhi_g + K_g . Qlo_g) on MFMA,
 //   masked to token < T_act and token <= past + i (causal inside a verify or
 //   prefill run), scaled by 1/sqrt(D);
-//   a page-local softmax (max, exp, sum), then
 //   O^T[d][rho] += V^T[d][token] . (p * sv[token][d/32]) (hi/lo) on MFMA.
-// The four waves' (max, sum, O) merge in LDS; the chunk's partial goes to
-// `part` and k_attn_combine merges chunks (log-sum-exp). The reference's
-// softmax is exact three-pass; this one is online, equal within tolerance.
-template <int NG>
-__global__ __launch_bounds__(256) void k_attn(const AttnItem* __restrict__ items,
-                                              const JobDev* __restrict__ jobs, const uint4* __restrict__ Qp,
-                                              const uint8_t* __restrict__ kpool,
-                                              const uint8_t* __restrict__ vpool,
-                                              const uint32_t* __restrict__ page_table, KVGeom g, int group,
-                                              float* __restrict__ part) {
-    constexpr int D = 32 * NG;
-    constexpr int DT = D / 16;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, j4 = lane >> 4, l16 = lane & 15;
-    const AttnItem it = items[blockIdx.x];
-    const JobDev jb = jobs[it.job];
-    const int T_act = jb.past + jb.n;
-    const int R = jb.n * group;
-    const int pg = it.chunk * 4 + wave;
-    const int npg = (T_act + 63) >> 6;
-    const bool live = pg < npg;
-    const float inv_sqrt_d = 1.0f / sqrtf((float)D);
-
-    __shared__ float sm[4][16], sl[4][16];
-    __shared__ float so[4][16][D + 1];
-
-    const uint8_t* kb = nullptr;
-    const uint8_t* vb = nullptr;
-    if (live) {
-        const uint32_t phys = page_table[(size_t)jb.slot * g.max_pages + pg];
-        kb = kpool + ((size_t)phys * g.nKV + it.kvh) * g.blk;
-        vb = vpool + ((size_t)phys * g.nKV + it.kvh) * g.blk;
-    }
-    // K fragments: token tile tt, lane's 8*NG bytes (NG/2 uint4).
-    uint4 kc[4][NG / 2];
-    uint4 vc[DT];
-    if (live) {
-#pragma unroll
-        for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-            for (int q = 0; q < NG / 2; q++)
-                kc[tt][q] = *(const uint4*)(kb + (size_t)(tt * 16 + l16) * D + (D / 4) * j4 + 16 * q);
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) vc[dt] = *(const uint4*)(vb + (size_t)(dt * 16 + l16) * 64 + 16 * j4);
-    }
-
-    for (int mtq = 0; mtq < jb.mtq; mtq++) {
-        float pr[4][4];
-        float mrow = -INFINITY, lsum = 0.0f;
-        float4_t o[DT];
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
-        if (live) {
-            uint4 qh[NG], ql[NG];
-            const size_t qb = (size_t)jb.qp_off + (((size_t)it.kvh * jb.mtq + mtq) * NG) * 2 * 64 + lane;
-#pragma unroll
-            for (int gg = 0; gg < NG; gg++) {
-                qh[gg] = Qp[qb + (size_t)gg * 128];
-                ql[gg] = Qp[qb + (size_t)gg * 128 + 64];
-            }
-            const int rho = mtq * 16 + l16;
-            const int lim = rho < R ? jb.past + rho / group : -1;   // last visible token
-#pragma unroll
-            for (int tt = 0; tt < 4; tt++) {
-                // K scales of tokens tt*16 + 4*j4 + r, all groups: 4*NG floats.
-                float ks[4 * NG];
-#pragma unroll
-                for (int q = 0; q < NG; q++) {
-                    const float4 f = *(const float4*)(kb + 64 * D + ((size_t)(tt * 16 + 4 * j4) * NG) * 4 + 16 * q);
-                    ks[4 * q] = f.x; ks[4 * q + 1] = f.y; ks[4 * q + 2] = f.z; ks[4 * q + 3] = f.w;
-                }
-                float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int gg = 0; gg < NG; gg++) {
-                    const uint4 c = kc[tt][gg >> 1];
-                    const half8_t kf = (gg & 1) ? dequant8_signed(c.z, c.w) : dequant8_signed(c.x, c.y);
-                    float4_t p = {0.f, 0.f, 0.f, 0.f};
-                    p = mfma16x16x32(kf, __builtin_bit_cast(half8_t, qh[gg]), p);
-                    p = mfma16x16x32(kf, __builtin_bit_cast(half8_t, ql[gg]), p);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(ks[r * NG + gg], p[r], acc[r]);
-                }
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int tok = pg * 64 + tt * 16 + 4 * j4 + r;
-                    const bool ok = tok < T_act && tok <= lim;
-                    pr[tt][r] = ok ? acc[r] * inv_sqrt_d : -INFINITY;
-                    mrow = fmaxf(mrow, pr[tt][r]);
-                }
-            }
-            mrow = fmaxf(mrow, __shfl_xor(mrow, 16));
-            mrow = fmaxf(mrow, __shfl_xor(mrow, 32));
-#pragma unroll
-            for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float e = (mrow == -INFINITY || pr[tt][r] == -INFINITY) ? 0.0f : expf(pr[tt][r] - mrow);
-                    pr[tt][r] = e;
-                    lsum += e;
-                }
-            lsum += __shfl_xor(lsum, 16);
-            lsum += __shfl_xor(lsum, 32);
-            // P . V, one 32-token k-step at a time.
-#pragma unroll
-            for (int b = 0; b < NG; b++) {
-                float sv[16];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const float4 f = *(const float4*)(vb + 64 * D + ((size_t)b * 64 + 16 * j4) * 4 + 16 * q);
-                    sv[4 * q] = f.x; sv[4 * q + 1] = f.y; sv[4 * q + 2] = f.z; sv[4 * q + 3] = f.w;
-                }
-#pragma unroll
-                for (int ks = 0; ks < 2; ks++) {
-                    half8_t ph, pl;
-#pragma unroll
-                    for (int ii = 0; ii < 8; ii++) {
-                        const int tt = 2 * ks + (ii >> 2), r = ii & 3;
-                        const float pv = pr[tt][r] == 0.0f ? 0.0f : pr[tt][r] * sv[4 * tt + r];
-                        _Float16 a, c;
-                        split_hilo(pv, a, c);
-                        ph[ii] = a;
-                        pl[ii] = c;
-                    }
-#pragma unroll
-                    for (int dd = 0; dd < 2; dd++) {
-                        const int dt = 2 * b + dd;
-                        const uint4 c = vc[dt];
-                        const half8_t vf = ks ? dequant8_signed(c.z, c.w) : dequant8_signed(c.x, c.y);
-                        o[dt] = mfma16x16x32(vf, ph, o[dt]);
-                        o[dt] = mfma16x16x32(vf, pl, o[dt]);
-                    }
-                }
-            }
-        }
-        if (j4 == 0) {
-            sm[wave][l16] = mrow;
-            sl[wave][l16] = lsum;
-        }
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) so[wave][l16][dt * 16 + 4 * j4 + r] = o[dt][r];
-        __syncthreads();
-        for (int e = threadIdx.x; e < 16 * D; e += 256) {
-            const int rho = e / D, d = e % D;
-            float M = -INFINITY;
-#pragma unroll
-            for (int wv = 0; wv < 4; wv++) M = fmaxf(M, sm[wv][rho]);
-            float L = 0.0f, O = 0.0f;
-            if (M != -INFINITY) {
-#pragma unroll
-                for (int wv = 0; wv < 4; wv++) {
-                    const float mw = sm[wv][rho];
-                    if (mw == -INFINITY) continue;
-                    const float f = expf(mw - M);
-                    L += sl[wv][rho] * f;
-                    O += so[wv][rho][d] * f;
-                }
-            }
-            float* dst = part + it.part + (size_t)(mtq * 16 + rho) * (D + 2);
-            dst[2 + d] = O;
-            if (d == 0) {
-                dst[0] = M;
-                dst[1] = L;
-            }
-        }
-        __syncthreads();
-    }
-}
-
+// The reference's softmax is exact three-pass; this one is online (per page)
+// with a log-sum-exp merge of the chunks, equal within tolerance.
 // Attention, one wave per work item: (job, kv head, query m-tile, chunk of
-// `ppw` pages). The wave walks its pages in order with the next page's int8
-// K/V fragments already loading while it computes the current one, and keeps
-// an online softmax (running max, sum, rescaled O) across them; its
-// (max, sum, O) partial for the 16 query rows goes to `part` (16 x (D + 2)
-// floats). Per page, the arithmetic is k_attn's: S^T = K . Q^T (hi/lo) scaled
-// per (token, 32-block), masked (token < T_act, token <= past + i) and scaled
-// by 1/sqrt(D); O^T += V^T . (p * sv) (hi/lo).
+// `ppw` pages). The wave walks its pages in order and keeps an online softmax
+// (running max, sum, rescaled O) across them; its (max, sum, O) partial for
+// the 16 query rows goes to `part` (16 x (D + 2) floats, max in natural-log
+// units). Per page: S^T = K . Q^T (hi/lo) scaled per (token, 32-block),
+// masked (token < T_act, token <= past + i) and scaled by 1/sqrt(D);
+// O^T += V^T . (p * sv) (hi/lo).
+//
+// Register budget: two waves per SIMD (<= 256 VGPRs). The K fragments of the
+// next page are loaded into the same registers as soon as S is formed, and
+// the next page's V fragments as soon as the PV products are issued, so one
+// page of K and one of V are ever held. Every page is read through a buffer
+// resource whose base is that page's (page, kv head) block in the pool (64-bit
+// address arithmetic, so pools may exceed 4 GB) and whose size is the block:
+// an offset outside the block reads zero instead of faulting.
+//
+// Every lane builds its fragments and rescales O on every page, with no
+// branch on row state: MFMA reads all lanes' operands whatever the execution
+// mask, and a still fully masked row (max -inf) just takes alpha = 0, p = 0.
 template <int NG>
-__global__ __launch_bounds__(256) void k_attn2(const AttnItem* __restrict__ items, int nitems,
-                                               const JobDev* __restrict__ jobs, const uint4* __restrict__ Qp,
-                                               const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
-                                               const uint32_t* __restrict__ page_table, KVGeom g, int group, int ppw,
-                                               float* __restrict__ part) {
+__global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ items, int nitems,
+                                                 const JobDev* __restrict__ jobs, const uint4* __restrict__ Qp,
+                                                 const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
+                                                 const uint32_t* __restrict__ page_table, KVGeom g, int group, int ppw,
+                                                 float* __restrict__ part) {
     constexpr int D = 32 * NG;
     constexpr int DT = D / 16;
     const int lane = threadIdx.x & 63, j4 = lane >> 4, l16 = lane & 15;
-    const int wid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int wid = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (wid >= nitems) return;   // no barriers below: a finished wave may leave
     const AttnItem it = items[wid];
     const JobDev jb = jobs[it.job];
@@ -970,87 +645,88 @@ __global__ __launch_bounds__(256) void k_attn2(const AttnItem* __restrict__ item
     const uint32_t* pt = page_table + (size_t)jb.slot * g.max_pages;
     const size_t hoff = (size_t)it.kvh * g.blk;
     const size_t pstride = (size_t)g.nKV * g.blk;
+    auto page_rsrc = [&](const uint8_t* pool, int p) {
+        const uint32_t pg = __builtin_amdgcn_readfirstlane(pt[p]);
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(pool + (size_t)pg * pstride + hoff), 0, g.blk, 0x00020000);
+    };
+    // Lane offsets inside a block (layout of k_fin_qkv's writes):
+    const int vk = l16 * D + (D / 4) * j4;       // K codes: token row l16 of a 16-token tile, lane's k-block
+    const int vks = 64 * D + (4 * j4 * NG) * 4;  // K scales of tokens 4*j4.. of a tile
+    const int vv = l16 * 64 + 16 * j4;           // V codes: d row l16 of a d-tile, lane's token block
+    const int vvs = 64 * D + 16 * j4 * 4;        // V scales of the lane's tokens; 32-block b at +256*b
 
     float mrow = -INFINITY, lsum = 0.0f;
     float4_t o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    uint4 kc[4][NG / 2], vc[DT];
-    if (p0 < p1) {
-        const uint8_t* kb = kpool + (size_t)pt[p0] * pstride + hoff;
-        const uint8_t* vb = vpool + (size_t)pt[p0] * pstride + hoff;
+    u32x4 kc[4][NG / 2], vc[DT];
+    auto load_k = [&](__amdgpu_buffer_rsrc_t r) {
 #pragma unroll
         for (int tt = 0; tt < 4; tt++)
 #pragma unroll
             for (int q = 0; q < NG / 2; q++)
-                kc[tt][q] = *(const uint4*)(kb + (size_t)(tt * 16 + l16) * D + (D / 4) * j4 + 16 * q);
+                kc[tt][q] = __builtin_amdgcn_raw_buffer_load_b128(r, vk, tt * 16 * D + 16 * q, 0);
+    };
+    auto load_v = [&](__amdgpu_buffer_rsrc_t r) {
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) vc[dt] = *(const uint4*)(vb + (size_t)(dt * 16 + l16) * 64 + 16 * j4);
-    }
-    for (int p = p0; p < p1; p++) {
-        const uint8_t* kb = kpool + (size_t)pt[p] * pstride + hoff;
-        const uint8_t* vb = vpool + (size_t)pt[p] * pstride + hoff;
-        uint4 kn[4][NG / 2], vn[DT];
-        if (p + 1 < p1) {
-            const uint8_t* kb2 = kpool + (size_t)pt[p + 1] * pstride + hoff;
-            const uint8_t* vb2 = vpool + (size_t)pt[p + 1] * pstride + hoff;
+        for (int dt = 0; dt < DT; dt++) vc[dt] = __builtin_amdgcn_raw_buffer_load_b128(r, vv, dt * 1024, 0);
+    };
+    if (p0 < p1) {
+        auto rk = page_rsrc(kpool, p0);
+        auto rv = page_rsrc(vpool, p0);
+        load_k(rk);
+        load_v(rv);
+        for (int p = p0; p < p1; p++) {
+            // the last page reloads itself instead of branching (an L2 hit)
+            const int pn = p + 1 < p1 ? p + 1 : p;
+            const auto rkn = page_rsrc(kpool, pn);
+            float pr[4][4];
+            float pm = -INFINITY;
 #pragma unroll
-            for (int tt = 0; tt < 4; tt++)
+            for (int tt = 0; tt < 4; tt++) {
+                float ks[4 * NG];
 #pragma unroll
-                for (int q = 0; q < NG / 2; q++)
-                    kn[tt][q] = *(const uint4*)(kb2 + (size_t)(tt * 16 + l16) * D + (D / 4) * j4 + 16 * q);
+                for (int q = 0; q < NG; q++) {
+                    const u32x4 f = __builtin_amdgcn_raw_buffer_load_b128(rk, vks, tt * 16 * NG * 4 + 16 * q, 0);
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) vn[dt] = *(const uint4*)(vb2 + (size_t)(dt * 16 + l16) * 64 + 16 * j4);
-        }
-        float pr[4][4];
-        float pm = -INFINITY;
+                    for (int e = 0; e < 4; e++) ks[4 * q + e] = __uint_as_float(f[e]);
+                }
+                float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++) {
-            float ks[4 * NG];
+                for (int gg = 0; gg < NG; gg++) {
+                    const u32x4 c = kc[tt][gg >> 1];
+                    const half8_t kf = (gg & 1) ? dequant8_signed(c[2], c[3]) : dequant8_signed(c[0], c[1]);
+                    float4_t pp = {0.f, 0.f, 0.f, 0.f};
+                    pp = mfma16x16x32(kf, __builtin_bit_cast(half8_t, qh[gg]), pp);
+                    pp = mfma16x16x32(kf, __builtin_bit_cast(half8_t, ql[gg]), pp);
 #pragma unroll
-            for (int q = 0; q < NG; q++) {
-                const float4 f = *(const float4*)(kb + 64 * D + ((size_t)(tt * 16 + 4 * j4) * NG) * 4 + 16 * q);
-                ks[4 * q] = f.x; ks[4 * q + 1] = f.y; ks[4 * q + 2] = f.z; ks[4 * q + 3] = f.w;
+                    for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(ks[r * NG + gg], pp[r], acc[r]);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int tok = p * 64 + tt * 16 + 4 * j4 + r;
+                    const bool ok = tok < T_act && tok <= lim;
+                    pr[tt][r] = ok ? acc[r] * inv_sqrt_d : -INFINITY;
+                    pm = fmaxf(pm, pr[tt][r]);
+                }
             }
-            float4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int gg = 0; gg < NG; gg++) {
-                const uint4 c = kc[tt][gg >> 1];
-                const half8_t kf = (gg & 1) ? dequant8_signed(c.z, c.w) : dequant8_signed(c.x, c.y);
-                float4_t pp = {0.f, 0.f, 0.f, 0.f};
-                pp = mfma16x16x32(kf, __builtin_bit_cast(half8_t, qh[gg]), pp);
-                pp = mfma16x16x32(kf, __builtin_bit_cast(half8_t, ql[gg]), pp);
-#pragma unroll
-                for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(ks[r * NG + gg], pp[r], acc[r]);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int tok = p * 64 + tt * 16 + 4 * j4 + r;
-                const bool ok = tok < T_act && tok <= lim;
-                pr[tt][r] = ok ? acc[r] * inv_sqrt_d : -INFINITY;
-                pm = fmaxf(pm, pr[tt][r]);
-            }
-        }
-        pm = fmaxf(pm, __shfl_xor(pm, 16));
-        pm = fmaxf(pm, __shfl_xor(pm, 32));
-        const float mnew = fmaxf(mrow, pm);
-        // No branch on the row's state here: a row that is still fully masked
-        // (mnew = -inf) takes alpha = 0 and p = 0 through the same code. MFMA
-        // reads every lane's operands whatever the execution mask, so lanes
-        // must not skip building their fragments.
-        {
+            load_k(rkn);   // the K registers are free: start the next page
+            pm = fmaxf(pm, __shfl_xor(pm, 16));
+            pm = fmaxf(pm, __shfl_xor(pm, 32));
+            const float mnew = fmaxf(mrow, pm);
             const float alpha = mrow == -INFINITY ? 0.0f : expf(mrow - mnew);
             lsum *= alpha;
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) o[dt][r] *= alpha;
+            const float msub = mnew == -INFINITY ? 0.0f : mnew;
 #pragma unroll
             for (int tt = 0; tt < 4; tt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const float e = pr[tt][r] == -INFINITY ? 0.0f : expf(pr[tt][r] - mnew);
+                    const float e = expf(pr[tt][r] - msub);   // masked: exp(-inf) = 0
                     pr[tt][r] = e;
                     lsum += e;
                 }
@@ -1059,8 +735,9 @@ __global__ __launch_bounds__(256) void k_attn2(const AttnItem* __restrict__ item
                 float sv[16];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const float4 f = *(const float4*)(vb + 64 * D + ((size_t)b * 64 + 16 * j4) * 4 + 16 * q);
-                    sv[4 * q] = f.x; sv[4 * q + 1] = f.y; sv[4 * q + 2] = f.z; sv[4 * q + 3] = f.w;
+                    const u32x4 f = __builtin_amdgcn_raw_buffer_load_b128(rv, vvs, b * 256 + 16 * q, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) sv[4 * q + e] = __uint_as_float(f[e]);
                 }
 #pragma unroll
                 for (int ks = 0; ks < 2; ks++) {
@@ -1068,6 +745,7 @@ __global__ __launch_bounds__(256) void k_attn2(const AttnItem* __restrict__ item
 #pragma unroll
                     for (int ii = 0; ii < 8; ii++) {
                         const int tt = 2 * ks + (ii >> 2), r = ii & 3;
+                        // a masked token's scale may be another session's stale value: p = 0 stays 0
                         const float pv = pr[tt][r] == 0.0f ? 0.0f : pr[tt][r] * sv[4 * tt + r];
                         _Float16 a, c;
                         split_hilo(pv, a, c);
@@ -1077,22 +755,17 @@ __global__ __launch_bounds__(256) void k_attn2(const AttnItem* __restrict__ item
 #pragma unroll
                     for (int dd = 0; dd < 2; dd++) {
                         const int dt = 2 * b + dd;
-                        const uint4 c = vc[dt];
-                        const half8_t vf = ks ? dequant8_signed(c.z, c.w) : dequant8_signed(c.x, c.y);
+                        const u32x4 c = vc[dt];
+                        const half8_t vf = ks ? dequant8_signed(c[2], c[3]) : dequant8_signed(c[0], c[1]);
                         o[dt] = mfma16x16x32(vf, ph, o[dt]);
                         o[dt] = mfma16x16x32(vf, pl, o[dt]);
                     }
                 }
             }
             mrow = mnew;
-        }
-        if (p + 1 < p1) {
-#pragma unroll
-            for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-                for (int q = 0; q < NG / 2; q++) kc[tt][q] = kn[tt][q];
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++) vc[dt] = vn[dt];
+            rv = page_rsrc(vpool, pn);
+            load_v(rv);
+            rk = rkn;
         }
     }
     lsum += __shfl_xor(lsum, 16);
@@ -1108,16 +781,16 @@ __global__ __launch_bounds__(256) void k_attn2(const AttnItem* __restrict__ item
     }
 }
 
-void launch_attn2(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
-                  const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
-                  int ppw, float* part) {
+void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
+                 const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
+                 int ppw, float* part) {
     if (nitems <= 0) return;
     const int blocks = (nitems + 3) / 4;
     if (g.ng == 4)
-        hipLaunchKernelGGL((k_attn2<4>), dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool,
+        hipLaunchKernelGGL((k_attn<4>), dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool,
                            page_table, g, group, ppw, part);
     else
-        hipLaunchKernelGGL((k_attn2<2>), dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool,
+        hipLaunchKernelGGL((k_attn<2>), dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool,
                            page_table, g, group, ppw, part);
     CHECK_LAUNCH();
 }
@@ -1127,7 +800,7 @@ void launch_attn2(hipStream_t st, const AttnItem* items, int nitems, const JobDe
 // operand (merge_heads, web/model/kernels.js:1315-1329, is this indexing).
 // The chunks' weights exp(m_c - M) sit in LDS.
 constexpr int COMBINE_CMAX = 512;
-__global__ __launch_bounds__(256) void k_attn_combine2(const JobDev* __restrict__ jobs, int njobs,
+__global__ __launch_bounds__(256) void k_attn_combine(const JobDev* __restrict__ jobs, int njobs,
                                                        const AttnItem* __restrict__ items,
                                                        const float* __restrict__ part, KVGeom g, int nH, int group,
                                                        int KU, uint4* __restrict__ Xp, float* __restrict__ ctx_out,
@@ -1191,80 +864,12 @@ __global__ __launch_bounds__(256) void k_attn_combine2(const JobDev* __restrict_
     }
 }
 
-void launch_attn_combine2(hipStream_t st, const JobDev* jobs, int njobs, const AttnItem* items, const float* part,
+void launch_attn_combine(hipStream_t st, const JobDev* jobs, int njobs, const AttnItem* items, const float* part,
                           const KVGeom& g, int nH, int group, int KU, uint4* Xp, float* ctx_out,
                           const int32_t* wg_job, int nwg) {
     if (nwg <= 0) return;
-    hipLaunchKernelGGL(k_attn_combine2, dim3(nwg), dim3(256), 0, st, jobs, njobs, items, part, g, nH, group, KU, Xp,
+    hipLaunchKernelGGL(k_attn_combine, dim3(nwg), dim3(256), 0, st, jobs, njobs, items, part, g, nH, group, KU, Xp,
                        ctx_out, wg_job);
-    CHECK_LAUNCH();
-}
-
-void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
-                 const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g,
-                 int group, float* part) {
-    if (nitems <= 0) return;
-    if (g.ng == 4)
-        hipLaunchKernelGGL((k_attn<4>), dim3(nitems), dim3(256), 0, st, items, jobs, Qp, kpool, vpool,
-                           page_table, g, group, part);
-    else
-        hipLaunchKernelGGL((k_attn<2>), dim3(nitems), dim3(256), 0, st, items, jobs, Qp, kpool, vpool,
-                           page_table, g, group, part);
-    CHECK_LAUNCH();
-}
-
-// Merge a job's chunk partials (log-sum-exp), normalise, and write the
-// merged-heads row (web/model/kernels.js:1315-1329 merge_heads is this
-// indexing) as the o_proj operand. One workgroup per (job, kv head).
-__global__ __launch_bounds__(256) void k_attn_combine(const JobDev* __restrict__ jobs,
-                                                      const AttnItem* __restrict__ items,
-                                                      const float* __restrict__ part, KVGeom g, int nH,
-                                                      int group, int KU, uint4* __restrict__ Xp,
-                                                      float* __restrict__ ctx_out) {
-    const int job = blockIdx.x / g.nKV, kvh = blockIdx.x % g.nKV;
-    const JobDev jb = jobs[job];
-    const int D = g.D;
-    const int R = jb.n * group;
-    const int per = R * (D / 8);
-    for (int e = threadIdx.x; e < per; e += 256) {
-        const int rho = e / (D / 8), d0 = (e % (D / 8)) * 8;
-        float M = -INFINITY;
-        for (int c = 0; c < jb.nchunk; c++) {
-            const AttnItem it = items[jb.item0 + kvh * jb.nchunk + c];
-            M = fmaxf(M, part[it.part + (size_t)rho * (D + 2)]);
-        }
-        float L = 0.0f, O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        for (int c = 0; c < jb.nchunk; c++) {
-            const AttnItem it = items[jb.item0 + kvh * jb.nchunk + c];
-            const float* src = part + it.part + (size_t)rho * (D + 2);
-            const float mc = src[0];
-            if (mc == -INFINITY) continue;
-            const float f = expf(mc - M);
-            L += src[1] * f;
-#pragma unroll
-            for (int j = 0; j < 8; j++) O[j] += src[2 + d0 + j] * f;
-        }
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = O[j] / L;
-        const int i = rho / group, gi = rho % group;
-        const int r = jb.row0 + i;
-        const int k = (kvh * group + gi) * D + d0;
-        if (ctx_out) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) ctx_out[(size_t)r * nH * D + k + j] = v[j];
-        }
-        write_hilo(Xp, r, k / 8, KU, v);
-    }
-}
-
-void launch_attn_combine(hipStream_t st, const JobDev* jobs, int njobs, const AttnItem* items,
-                         const float* part, const KVGeom& g, int nH, int group, int M, int Mpad, int KU,
-                         uint4* Xp, float* ctx_out) {
-    (void)M;
-    (void)Mpad;
-    hipLaunchKernelGGL(k_attn_combine, dim3(njobs * g.nKV), dim3(256), 0, st, jobs, items, part, g, nH,
-                       group, KU, Xp, ctx_out);
     CHECK_LAUNCH();
 }
 
