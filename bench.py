@@ -31,6 +31,37 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per k_gemm_lx launch, from the FETCH_SIZE and WRITE_SIZE counter
+# runs (each calibrated on a plain copy of known size); written by hand into
+# this summary after those runs, read here so the JSON line carries it.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_gemm_lx_c3_traffic.md")
+
+
+def measured_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(mib):
+    """A plain device-to-device copy of `mib` MiB, three times, for scaling
+    the FETCH_SIZE / WRITE_SIZE counters: each copy reads and writes exactly
+    mib MiB."""
+    import torch
+    n = mib << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(f"[bench] copied {mib} MiB three times", file=sys.stderr, flush=True)
 
 
 def contexts(n, lo, hi, seed):
@@ -86,11 +117,16 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-layers", type=int, default=1)
     ap.add_argument("--layers", type=int, default=None, help="fewer layers (debug only; not a valid bench)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain copy of MIB MiB (for scaling the HBM byte counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: every box here has one GPU and this build has no multi-GPU path "
               "(the pass would scale as one data-parallel replica per GPU, with no exchange).", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
 
     from chattorrent_amd import configs
     from chattorrent_amd.ccdecode import Context
@@ -138,8 +174,11 @@ def main():
           file=sys.stderr, flush=True)
 
     # The dominant kernel: the q8 projection GEMM (every block's q|k|v, o,
-    # gate|up and down, and the LM head) — timed per launch with HIP events on
-    # the library's stream over a second region of the same steps.
+    # gate|up and down, and the LM head), timed with HIP events on the
+    # library's stream over a second region of the same steps: in profile
+    # mode each step relaunches each class for all 64 blocks back-to-back
+    # between one event pair (a marker beside every launch would add a few
+    # microseconds of gap to each), so ms / launches is a launch's duration.
     ctx.profile(True)
     for _ in range(args.steps):
         ids = step(pasts, ids)
@@ -151,7 +190,7 @@ def main():
     g_b = sum(prof[k][2] for k in ("qkv", "o", "gate_up", "down", "head"))
     achieved = g_b / (g_ms / 1000.0) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "kernel": "k_gemm_lx (all q8 projections + LM head)",
             "avg_launch_us": round(g_ms * 1000.0 / max(g_n, 1), 2),
             "bytes_per_launch": round(g_b / max(g_n, 1)),

@@ -61,7 +61,6 @@ struct cc_ctx {
     float* part = nullptr;
     size_t part_floats = 0;
     int ncu = 0;                   // compute units: the matmul's workgroup count
-    float* cut = nullptr;          // matmul pairs cut between waves
     uint4* qp = nullptr;
     size_t qp_units = 0;
     float* apart = nullptr;
@@ -93,7 +92,7 @@ struct cc_ctx {
     // opt-in per-kernel profile (cc_profile)
     bool prof = false;
     std::vector<hipEvent_t> pev;               // event pool, pairs
-    struct Mark { int kind; int e0, e1; double bytes; };
+    struct Mark { int kind; int e0, e1; int n; double bytes; };
     std::vector<Mark> marks;
     double prof_ms[CC_K_COUNT] = {0};
     int64_t prof_n[CC_K_COUNT] = {0};
@@ -236,24 +235,22 @@ MetaLayout meta_layout(const cc_ctx* ctx) {
     return m;
 }
 
-// Profile marks: an event pair around one launch, resolved after the step's
-// synchronisation.
-int prof_begin(cc_ctx* ctx) {
-    if (!ctx->prof) return -1;
+// Profile marks: one event pair around n back-to-back launches of one class,
+// resolved after the step's synchronisation. The events are for timing only
+// (no system-scope fence, whose cache writeback would stall the kernels next
+// to them).
+template <class F>
+void prof_mark(cc_ctx* ctx, int kind, int n, double bytes, F&& launches) {
     const int e = (int)ctx->marks.size() * 2;
     while ((int)ctx->pev.size() < e + 2) {
         hipEvent_t ev;
-        if (hipEventCreate(&ev) != hipSuccess) return -1;
+        if (hipEventCreateWithFlags(&ev, hipEventDisableSystemFence) != hipSuccess) return;
         ctx->pev.push_back(ev);
     }
     hipEventRecord(ctx->pev[e], ctx->stream);
-    return e;
-}
-
-void prof_end(cc_ctx* ctx, int e, int kind, double bytes) {
-    if (e < 0) return;
+    launches();
     hipEventRecord(ctx->pev[e + 1], ctx->stream);
-    ctx->marks.push_back(cc_ctx::Mark{kind, e, e + 1, bytes});
+    ctx->marks.push_back(cc_ctx::Mark{kind, e, e + 1, n, bytes});
 }
 
 void prof_collect(cc_ctx* ctx) {
@@ -261,7 +258,7 @@ void prof_collect(cc_ctx* ctx) {
         float ms = 0;
         if (hipEventElapsedTime(&ms, ctx->pev[m.e0], ctx->pev[m.e1]) == hipSuccess) {
             ctx->prof_ms[m.kind] += ms;
-            ctx->prof_n[m.kind] += 1;
+            ctx->prof_n[m.kind] += m.n;
             ctx->prof_bytes[m.kind] += m.bytes;
         }
     }
@@ -398,7 +395,6 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         }
         ctx->part_floats = pf;
         HIPCHK(dalloc(ctx, &ctx->part, pf * 4, &ctx->scratch_bytes));
-        HIPCHK(dalloc(ctx, &ctx->cut, lx_cut_floats(T, ctx->ncu) * 4, &ctx->scratch_bytes));
         // Q operands: sum over jobs of nKV * ceil(n*group/16) * ng * 2 * 64 uint4.
         ctx->qp_units = (size_t)(ceil_div(T * ctx->group, 16) + o.max_jobs) * nKV * (D / 32) * 128;
         HIPCHK(dalloc(ctx, &ctx->qp, ctx->qp_units * 16, &ctx->scratch_bytes));
@@ -762,32 +758,22 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
             launch_resid_norm(st, ctx->x, nullptr, nullptr, 0, T, Mpad, H, 0, L.ln1, d.rms_eps, L.qkv.KU, ctx->xp_h,
                               nullptr, ctx->ssq);
         const int sq = L.qkv.P;
-        int e = prof_begin(ctx);
-        launch_gemm(st, L.qkv, ctx->xp_h, ctx->part, T, ctx->cut, ctx->ncu);
-        prof_end(ctx, e, CC_K_QKV, qbytes(L.qkv));
+        launch_gemm(st, L.qkv, ctx->xp_h, ctx->part, T, ctx->ncu);
         launch_fin_qkv(st, ctx->part, sq, T, drow_job, djobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
                        L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 1);
-        e = prof_begin(ctx);
         launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
                      ctx->ppw, ctx->apart);
-        prof_end(ctx, e, CC_K_ATTN, p.kv_bytes);
         launch_attn_combine(st, djobs, (int)p.jobs.size(), ditems, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU,
                              ctx->xp_o, nullptr, dcwg, p.ncwg);
         const int so = L.o.P;
-        e = prof_begin(ctx);
-        launch_gemm(st, L.o, ctx->xp_o, ctx->part, T, ctx->cut, ctx->ncu);
-        prof_end(ctx, e, CC_K_O, qbytes(L.o));
+        launch_gemm(st, L.o, ctx->xp_o, ctx->part, T, ctx->ncu);
         launch_resid_norm(st, ctx->x, nullptr, ctx->part, so, T, Mpad, H, 0, L.ln2, d.rms_eps, L.gu.KU, ctx->xp_h,
                           nullptr, ctx->ssq);
         const int sg = L.gu.P;
-        e = prof_begin(ctx);
-        launch_gemm(st, L.gu, ctx->xp_h, ctx->part, T, ctx->cut, ctx->ncu);
-        prof_end(ctx, e, CC_K_GU, qbytes(L.gu));
+        launch_gemm(st, L.gu, ctx->xp_h, ctx->part, T, ctx->ncu);
         launch_fin_swiglu(st, ctx->part, sg, T, Mpad, d.ffn, L.down.KU, ctx->xp_f);
         const int sd = L.down.P;
-        e = prof_begin(ctx);
-        launch_gemm(st, L.down, ctx->xp_f, ctx->part, T, ctx->cut, ctx->ncu);
-        prof_end(ctx, e, CC_K_DOWN, qbytes(L.down));
+        launch_gemm(st, L.down, ctx->xp_f, ctx->part, T, ctx->ncu);
         const bool next = b + 1 < b1;
         launch_resid_norm(st, ctx->x, nullptr, ctx->part, sd, T, Mpad, H, 1,
                           next ? ctx->layers[b + 1 - ctx->L0].ln1 : nullptr, d.rms_eps,
@@ -795,6 +781,47 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
                           ctx->ssq);
     }
     (void)D;
+}
+
+// Profile replay (cc_profile): after the step's own work, each class's
+// launches of that step run again back-to-back between one event pair, with
+// every block's own weights and pools and the step's shapes. Launches queued
+// back-to-back on one stream start as the previous one ends, so the pair's
+// interval over n launches is n kernel durations with no marker between them
+// (a marker next to every launch costs each a few microseconds of gap). The
+// replays write only scratch the step has consumed (matmul planes, attention
+// partials) or, for the head, the same logits again from the same operand.
+static void prof_replay(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int b0, int b1, bool head) {
+    const cc_dims& d = ctx->d;
+    hipStream_t st = ctx->stream;
+    const int T = p.T;
+    const JobDev* djobs = (const JobDev*)(ctx->d_meta + ml.jobs);
+    const AttnItem* ditems = (const AttnItem*)(ctx->d_meta + ml.items);
+    auto blocks = [&](int kind, QTensor Layer::*w, const uint4* xp) {
+        double bytes = 0;
+        for (int b = b0; b < b1; b++) bytes += qbytes(ctx->layers[b - ctx->L0].*w);
+        prof_mark(ctx, kind, b1 - b0, bytes, [&] {
+            for (int b = b0; b < b1; b++) launch_gemm(st, ctx->layers[b - ctx->L0].*w, xp, ctx->part, T, ctx->ncu);
+        });
+    };
+    if (b1 > b0) {
+        blocks(CC_K_QKV, &Layer::qkv, ctx->xp_h);
+        if (p.nitems > 0)
+            prof_mark(ctx, CC_K_ATTN, b1 - b0, p.kv_bytes * (b1 - b0), [&] {
+                for (int b = b0; b < b1; b++) {
+                    const Layer& L = ctx->layers[b - ctx->L0];
+                    launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom,
+                                ctx->group, ctx->ppw, ctx->apart);
+                }
+            });
+        blocks(CC_K_O, &Layer::o, ctx->xp_o);
+        blocks(CC_K_GU, &Layer::gu, ctx->xp_h);
+        blocks(CC_K_DOWN, &Layer::down, ctx->xp_f);
+    }
+    if (head) {
+        const QTensor& hw = d.tied ? ctx->wte : ctx->lm_head;
+        prof_mark(ctx, CC_K_HEAD, 1, qbytes(hw), [&] { launch_gemm(st, hw, ctx->xp_h, ctx->logits, p.S, ctx->ncu); });
+    }
 }
 
 cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, int32_t to, int32_t topk,
@@ -917,9 +944,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         const int Mpad = 32 * ceil_div(S, 32);
         launch_resid_norm(st, ctx->x, (const int32_t*)(ctx->d_meta + ml.head_rows), nullptr, 0, S, Mpad, d.hidden, 0,
                           ctx->norm, d.rms_eps, hw.KU, ctx->xp_h, nullptr, ctx->ssq);
-        const int e = prof_begin(ctx);
-        launch_gemm(st, hw, ctx->xp_h, ctx->logits, S, ctx->cut, ctx->ncu);
-        prof_end(ctx, e, CC_K_HEAD, qbytes(hw));
+        launch_gemm(st, hw, ctx->xp_h, ctx->logits, S, ctx->ncu);
         ctx->head_rows = S;
         launch_topk(st, ctx->logits, hw.P, S, d.vocab, topk, ctx->tk_a, ctx->tk_b, ctx->d_vals, ctx->d_ids);
         HIPCHK(hipMemcpyAsync(hout, ctx->d_vals, (size_t)S * topk * 4, hipMemcpyDeviceToHost, st));
@@ -930,6 +955,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         HIPCHK(hipMemcpyAsync(hout, ctx->d_hbits, (size_t)T * d.hidden * 2, hipMemcpyDeviceToHost, st));
     }
     HIPCHK(hipEventRecord(ctx->ev1, st));
+    if (ctx->prof) prof_replay(ctx, p, ml, b0, b1, head);
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(take_launch_error());
     float ms = 0;
@@ -962,10 +988,8 @@ cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K, con
     const int sp = q.P;
     int8_t* dW = nullptr; uint16_t* dS = nullptr; float* dX = nullptr; float* dP = nullptr; float* dY = nullptr;
     uint4* dXp = nullptr;
-    float* dC = nullptr;
     HIPCHK(hipMalloc(&q.codes, (size_t)q.Nt * q.KU * (LX_REC / 2)));
     HIPCHK(hipMemsetAsync(q.codes, 0, (size_t)q.Nt * q.KU * (LX_REC / 2), ctx->stream));
-    HIPCHK(hipMalloc(&dC, lx_cut_floats(M, ctx->ncu) * 4));
     HIPCHK(hipMalloc(&dW, (size_t)N * K));
     HIPCHK(hipMalloc(&dS, (size_t)N * ng * 2));
     HIPCHK(hipMalloc(&dX, (size_t)M * K * 4));
@@ -978,12 +1002,12 @@ cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K, con
     hipStream_t st = ctx->stream;
     launch_tile_q8(st, dW, dS, N, K, 32, q, 0);
     launch_prep_rows(st, dX, K, M, Mt * 16, K, q.KU, dXp);
-    launch_gemm(st, q, dXp, dP, M, dC, ctx->ncu);
+    launch_gemm(st, q, dXp, dP, M, ctx->ncu);
     launch_sum_splits(st, dP, sp, M, N, dY);
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(take_launch_error());
     HIPCHK(hipMemcpy(Y, dY, (size_t)M * N * 4, hipMemcpyDeviceToHost));
-    for (void* v : {(void*)q.codes, (void*)dC, (void*)dW, (void*)dS, (void*)dX, (void*)dXp, (void*)dP, (void*)dY})
+    for (void* v : {(void*)q.codes, (void*)dW, (void*)dS, (void*)dX, (void*)dXp, (void*)dP, (void*)dY})
         hipFree(v);
     return CC_OK;
 }

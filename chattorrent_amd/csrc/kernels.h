@@ -50,9 +50,8 @@ struct KVGeom {
     int max_pages;
 };
 
-// Y planes: out[(r*M + m)*N + n], r < w.P; `cut` holds lx_cut_floats(..) floats.
-void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, float* cut, int ncu);
-size_t lx_cut_floats(int M, int ncu);
+// Y planes: out[(r*M + m)*N + n], r < w.P.
+void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, int ncu);
 int lx_groups(const QTensor& w, int ncu);
 void launch_prep_rows(hipStream_t st, const float* x, int ldx, int M, int Mpad, int K, int KU,
                       uint4* Xp);

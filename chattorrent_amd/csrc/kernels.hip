@@ -41,8 +41,9 @@ hipError_t take_launch_error() {
 // record; the workgroup's steps are split evenly over its waves in record
 // order, so each wave reads one forward run of memory. A pair cut between
 // waves is finished by the wave holding its first units, adding the others'
-// parts in unit order. Every split point depends on N, K and the CU count,
-// never on M, so a row's result is the same in any batch.
+// parts in unit order; the parts meet in LDS once every wave is past its last
+// step (the activations are dead by then). Every split point depends on N, K
+// and the CU count, never on M, so a row's result is the same in any batch.
 // Output: plane r to out[(r*M + m)*N + n]; consumers add planes 0..P-1 in order.
 constexpr int LX_WAVES = 8;
 constexpr int LX_R = 4;
@@ -52,8 +53,7 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 template <int MT>
 __global__ __launch_bounds__(64 * LX_WAVES) void k_gemm_lx(const uint8_t* __restrict__ Wr,
                                                            const uint4* __restrict__ Xp, float* __restrict__ out,
-                                                           float* __restrict__ cut, int KU, int M, int N, int Nt,
-                                                           int P, int Gm) {
+                                                           int KU, int M, int N, int Nt, int P, int Gm) {
     constexpr int NT = 2, R = LX_R, PW = R - 1, WAVES = LX_WAVES;
     extern __shared__ __attribute__((aligned(1024))) u32x4 xs[];
     const int lane = threadIdx.x & 63;
@@ -71,9 +71,6 @@ __global__ __launch_bounds__(64 * LX_WAVES) void k_gemm_lx(const uint8_t* __rest
     const auto rx = __builtin_amdgcn_make_buffer_rsrc((void*)Xp, 0, 0x7fffffff, 0x00020000);
     // Plane r's rows only: stores of rows >= M fall outside and are dropped.
     const auto ro = __builtin_amdgcn_make_buffer_rsrc((void*)(out + (size_t)r * M * N), 0, M * N * 4, 0x00020000);
-    const auto rc = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(cut + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * WAVES * MT * NT * 256), 0,
-        WAVES * MT * NT * 1024, 0x00020000);
     const int vw = lane * 16, vs = NT * 1024 + (lane & 15) * NT * 4;
     const int vo = (4 * (lane >> 4) * N + (lane & 15)) * 4;
     const int rec0 = ua * npairs + p0 * len;
@@ -103,11 +100,11 @@ __global__ __launch_bounds__(64 * LX_WAVES) void k_gemm_lx(const uint8_t* __rest
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void_t*)(xs + b * 64), 16, vw, src * 1024, 0, 0);
         }
     }
-    float4_t acc[MT][NT];
+    float4_t acc[MT][NT], tail[MT][NT];   // tail: this wave's part of a pair begun in an earlier wave
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = tail[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
@@ -171,19 +168,18 @@ __global__ __launch_bounds__(64 * LX_WAVES) void k_gemm_lx(const uint8_t* __rest
         pc = sw0 / len;
         uc = sw0 - pc * len;
     }
-    bool head_open = false;
+    bool head_open = false, has_tail = false;
     // After a pair's last unit (or this wave's last step) its partial goes to
-    // `out` (whole pair), to this wave's cut slot (pair began in an earlier
-    // wave), or stays in acc (pair goes on in later waves).
+    // `out` (whole pair), to `tail` (pair began in an earlier wave), or stays
+    // in acc (pair goes on in later waves).
     auto finish_step = [&](int st) {
         if (uc == len - 1 || st == sw1 - 1) {
             if (pc * len < sw0) {
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-                    for (int nt = 0; nt < NT; nt++)
-                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[mt][nt]), rc, vw,
-                                                               ((wave * MT + mt) * NT + nt) * 1024, 0);
+                    for (int nt = 0; nt < NT; nt++) tail[mt][nt] = acc[mt][nt];
+                has_tail = true;
             } else if ((pc + 1) * len <= sw1) {
                 store_plane(pc);
             } else {
@@ -222,6 +218,16 @@ __global__ __launch_bounds__(64 * LX_WAVES) void k_gemm_lx(const uint8_t* __rest
             }
         }
     }
+    // Every wave is past its last step: the LDS activations are dead and hold
+    // the cut parts now, one 1 KiB slot per (wave, m-tile, tile).
+    __syncthreads();
+    if (has_tail) {
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++)
+                xs[((wave * MT + mt) * NT + nt) * 64 + lane] = __builtin_bit_cast(u32x4, tail[mt][nt]);
+    }
     __syncthreads();
     if (head_open) {
         const int pair = (sw1 - 1) / len, pe = (pair + 1) * len;
@@ -233,8 +239,7 @@ __global__ __launch_bounds__(64 * LX_WAVES) void k_gemm_lx(const uint8_t* __rest
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++) {
-                    const float4_t o = __builtin_bit_cast(
-                        float4_t, __builtin_amdgcn_raw_buffer_load_b128(rc, vw, ((w2 * MT + mt) * NT + nt) * 1024, 1));
+                    const float4_t o = __builtin_bit_cast(float4_t, xs[((w2 * MT + mt) * NT + nt) * 64 + lane]);
 #pragma unroll
                     for (int e = 0; e < 4; e++) acc[mt][nt][e] = acc[mt][nt][e] + o[e];
                 }
@@ -248,13 +253,8 @@ int lx_groups(const QTensor& w, int ncu) {
     return w.P * per;
 }
 
-size_t lx_cut_floats(int M, int ncu) {
-    // grid.x <= ncu, grid.y m-blocks of 32 rows; one slot per wave of MT=2 x NT=2 tiles
-    return (size_t)ncu * ((M + 31) / 32) * LX_WAVES * 2 * 2 * 256;
-}
-
 template <int MT>
-static void launch_lx(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, float* cut, int ncu) {
+static void launch_lx(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, int ncu) {
     static bool attr = false;
     if (!attr) {
         attr = true;
@@ -263,14 +263,16 @@ static void launch_lx(hipStream_t st, const QTensor& w, const uint4* Xp, float* 
     }
     const int G = lx_groups(w, ncu), Gm = G / w.P;
     const int lenmax = (w.KU + w.P - 1) / w.P;
+    // the plane's activations, and afterwards the cut parts (1 KiB per wave, m-tile and tile)
+    const size_t lds = std::max((size_t)lenmax * MT * 4096, (size_t)LX_WAVES * MT * 2 * 1024);
     dim3 grid(G, (M + 16 * MT - 1) / (16 * MT));
-    hipLaunchKernelGGL(k_gemm_lx<MT>, grid, dim3(64 * LX_WAVES), (size_t)lenmax * MT * 4096, st, w.codes, Xp, out, cut,
-                       w.KU, M, w.N, w.Nt, w.P, Gm);
+    hipLaunchKernelGGL(k_gemm_lx<MT>, grid, dim3(64 * LX_WAVES), lds, st, (const uint8_t*)w.codes, Xp, out, w.KU, M, w.N,
+                 w.Nt, w.P, Gm);
 }
 
-void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, float* cut, int ncu) {
-    if (M <= 16) launch_lx<1>(st, w, Xp, out, M, cut, ncu);
-    else launch_lx<2>(st, w, Xp, out, M, cut, ncu);
+void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, int ncu) {
+    if (M <= 16) launch_lx<1>(st, w, Xp, out, M, ncu);
+    else launch_lx<2>(st, w, Xp, out, M, ncu);
     CHECK_LAUNCH();
 }
 
@@ -787,11 +789,11 @@ void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev
     if (nitems <= 0) return;
     const int blocks = (nitems + 3) / 4;
     if (g.ng == 4)
-        hipLaunchKernelGGL((k_attn<4>), dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool,
-                           page_table, g, group, ppw, part);
+        hipLaunchKernelGGL(k_attn<4>, dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool, page_table, g,
+                     group, ppw, part);
     else
-        hipLaunchKernelGGL((k_attn<2>), dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool,
-                           page_table, g, group, ppw, part);
+        hipLaunchKernelGGL(k_attn<2>, dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool, page_table, g,
+                     group, ppw, part);
     CHECK_LAUNCH();
 }
 

@@ -163,10 +163,12 @@ cc_status cc_stats_get(const cc_ctx* ctx, cc_stats* out);
 
 /* Per-kernel timing with HIP events on the context's stream (the
  * reference's gpuprof.js level 2, web/model/gpuprof.js:1-12, re-done for
- * HIP). While enabled, every launch of the classes below is bracketed by
- * events; cc_profile_read returns the summed milliseconds, the launch count
- * and the algorithmic HBM bytes of those launches (q8 weights at 1.0625 B
- * per weight; KV rows at D + 4*D/32 B). Enabling resets the sums. */
+ * HIP). While enabled, each cc_step, after its own work, launches each class
+ * below again for every block of the step, back-to-back between one event
+ * pair (so no marker sits between launches); cc_profile_read returns the
+ * summed milliseconds, the launch count and the algorithmic HBM bytes of
+ * those launches (q8 weights at 1.0625 B per weight; KV rows at
+ * D + 4*D/32 B). The step's results are unchanged. Enabling resets the sums. */
 enum { CC_K_QKV = 0, CC_K_O = 1, CC_K_GU = 2, CC_K_DOWN = 3, CC_K_HEAD = 4, CC_K_ATTN = 5, CC_K_COUNT = 6 };
 cc_status cc_profile(cc_ctx* ctx, int32_t enable);
 cc_status cc_profile_read(const cc_ctx* ctx, int32_t kind, double* ms, int64_t* launches, double* bytes);

@@ -180,6 +180,30 @@ def test_deterministic(smol):
     assert np.array_equal(a[0].view(np.uint32), b[0].view(np.uint32)) and np.array_equal(a[1], b[1])
 
 
+def test_profile_replay_keeps_results(smol):
+    """cc_profile's replay (each class relaunched back-to-back after the step)
+    leaves the step's outputs and whole logits rows unchanged and counts one
+    launch per block per class (one head launch)."""
+    d, c, om = smol
+    jobs = [dict(slot=s, past=T, n=1, ids=_ids(1, d["vocab"], 60 + s), sampled=1)
+            for s, T in enumerate([17, 130, 511, 200])]
+    a = c.step(jobs, topk=8)
+    la = c.read_logits(len(jobs))
+    c.profile(True)
+    try:
+        b = c.step(jobs, topk=8)
+        lb = c.read_logits(len(jobs))
+        prof = c.profile_read()
+    finally:
+        c.profile(False)
+    assert np.array_equal(a[0].view(np.uint32), b[0].view(np.uint32)) and np.array_equal(a[1], b[1])
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    L = d["n_layer"]
+    for k in ("qkv", "o", "gate_up", "down", "attn"):
+        assert prof[k][1] == L and prof[k][0] > 0, (k, prof[k])
+    assert prof["head"][1] == 1 and prof["head"][0] > 0
+
+
 def test_prefill_and_verify_match_oracle(gpu):
     """Causal rows inside a job: a prefill chunk from position 0 and a verify
     run on top of a random cache, sampled at every row."""
