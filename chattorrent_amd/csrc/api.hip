@@ -402,8 +402,8 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         // frame (the combine kernel's LDS).
         ctx->ppw = std::max(8, ceil_div(ctx->max_pages, 512));
         ctx->items_cap = max_items_for(ctx);
-        // Attention partials: 16 rows of (D + 2) floats per item.
-        ctx->apart_floats = ctx->items_cap * 16 * (size_t)(D + 2);
+        // Attention partials: 16 rows of (D + 4) floats per item.
+        ctx->apart_floats = ctx->items_cap * 16 * (size_t)(D + 4);
         HIPCHK(dalloc(ctx, &ctx->apart, ctx->apart_floats * 4, &ctx->scratch_bytes));
         HIPCHK(dalloc(ctx, &ctx->ssq, (size_t)T * ceil_div(H, 256) * 4, &ctx->scratch_bytes));
         if (ctx->head) {
@@ -702,7 +702,7 @@ static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, 
             for (int mt = 0; mt < jd.mtq; mt++) {
                 for (int c = 0; c < jd.nchunk; c++) {
                     p.items.push_back(AttnItem{j, h, c, (int32_t)ap, mt});
-                    ap += (size_t)16 * (ctx->D + 2);
+                    ap += (size_t)16 * (ctx->D + 4);
                 }
                 p.cwg.push_back(j);
                 p.cwg.push_back(h);
@@ -763,7 +763,7 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
                        L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 1);
         launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
                      ctx->ppw, ctx->apart);
-        launch_attn_combine(st, djobs, (int)p.jobs.size(), ditems, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU,
+        launch_attn_combine(st, djobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU,
                              ctx->xp_o, nullptr, dcwg, p.ncwg);
         const int so = L.o.P;
         launch_gemm(st, L.o, ctx->xp_o, ctx->part, T, ctx->ncu);
@@ -1161,7 +1161,7 @@ cc_status cc_op_attend(cc_ctx* ctx, int32_t layer, int32_t slot, const float* q,
                    ctx->tbl, ctx->rot, L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 0);
     launch_attn(st, di, p.nitems, dj, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->ppw,
                  ctx->apart);
-    launch_attn_combine(st, dj, 1, di, ctx->apart, ctx->geom, d.n_heads, ctx->group, KU, dXp, dctx,
+    launch_attn_combine(st, dj, ctx->apart, ctx->geom, d.n_heads, ctx->group, KU, dXp, dctx,
                          (const int32_t*)(ctx->d_meta + ml.cwg), p.ncwg);
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(take_launch_error());

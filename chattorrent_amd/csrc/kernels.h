@@ -88,8 +88,7 @@ void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const floa
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
                   const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
                   int ppw, float* part);
-void launch_attn_combine(hipStream_t st, const JobDev* jobs, int njobs, const AttnItem* items, const float* part,
-                          const KVGeom& g, int nH, int group, int KU, uint4* Xp, float* ctx_out,
-                          const int32_t* wg_job, int nwg);
+void launch_attn_combine(hipStream_t st, const JobDev* jobs, const float* part, const KVGeom& g, int nH, int group,
+                         int KU, uint4* Xp, float* ctx_out, const int32_t* wg_job, int nwg);
 void launch_sum_splits(hipStream_t st, const float* part, int splits, int M, int N, float* out);
 void launch_to_half_bits(hipStream_t st, const float* x, int64_t n, uint16_t* out);

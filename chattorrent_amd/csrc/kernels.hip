@@ -411,31 +411,56 @@ void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const floa
 
 // SwiGLU (web/model/kernels.js:1513-1529 silu_mul): act = g * (1/(1+exp(-g)))
 // * up over the fused gate|up projection, straight into the down operand.
-__global__ void k_fin_swiglu(const float* __restrict__ part, int splits, int M, int Mpad, int F, int KU,
-                             uint4* __restrict__ Xp) {
+__global__ __launch_bounds__(256) void k_fin_swiglu(const float* __restrict__ part, int splits, int M, int Mpad,
+                                                    int F, int KU, uint4* __restrict__ Xp) {
+    // one thread per (row, 8 columns); the planes are added in order
     const int per = 8 * KU;
-    const int total = Mpad * per;
-    const size_t N2 = 2 * (size_t)F;
-    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
-        const int m = i / per, c = i % per;
-        float v[8];
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= Mpad * per) return;
+    const int m = i / per, c = i % per, k0 = 8 * c;
+    const size_t N2 = 2 * (size_t)F, plane = (size_t)M * N2;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (m < M && k0 < F) {
+        float g[8], u[8];
+        const float* row = part + (size_t)m * N2 + k0;
+        if (k0 + 8 <= F && (F & 3) == 0) {
+            auto ld8 = [&](const float* p, float* x) {
+                const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+                x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+            };
+            ld8(row, g);
+            ld8(row + F, u);
+#pragma unroll 4
+            for (int s = 1; s < splits; s++) {
+                float gs[8], us[8];
+                ld8(row + s * plane, gs);
+                ld8(row + s * plane + F, us);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    g[j] = g[j] + gs[j];
+                    u[j] = u[j] + us[j];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                g[j] = u[j] = 0.0f;
+                if (k0 + j >= F) continue;
+                g[j] = row[j];
+                u[j] = row[F + j];
+                for (int s = 1; s < splits; s++) {
+                    g[j] = g[j] + row[s * plane + j];
+                    u[j] = u[j] + row[s * plane + F + j];
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int k = 8 * c + j;
-            float a = 0.0f;
-            if (m < M && k < F) {
-                float g = part[(size_t)m * N2 + k], u = part[(size_t)m * N2 + F + k];
-                for (int s = 1; s < splits; s++) {
-                    g = g + part[((size_t)s * M + m) * N2 + k];
-                    u = u + part[((size_t)s * M + m) * N2 + F + k];
-                }
-                const float sc = 1.0f / (1.0f + expf(-g));
-                a = g * sc * u;
-            }
-            v[j] = a;
+            const float sc = 1.0f / (1.0f + expf(-g[j]));
+            v[j] = k0 + j < F ? g[j] * sc * u[j] : 0.0f;
         }
-        write_hilo(Xp, m, c, KU, v);
     }
+    write_hilo(Xp, m, c, KU, v);
 }
 
 void launch_fin_swiglu(hipStream_t st, const float* part, int splits, int M, int Mpad, int F, int KU,
@@ -596,18 +621,21 @@ void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const 
 // Attention, one wave per work item: (job, kv head, query m-tile, chunk of
 // `ppw` pages). The wave walks its pages in order and keeps an online softmax
 // (running max, sum, rescaled O) across them; its (max, sum, O) partial for
-// the 16 query rows goes to `part` (16 x (D + 2) floats, max in natural-log
-// units). Per page: S^T = K . Q^T (hi/lo) scaled per (token, 32-block),
-// masked (token < T_act, token <= past + i) and scaled by 1/sqrt(D);
-// O^T += V^T . (p * sv) (hi/lo).
+// the 16 query rows goes to `part` (16 rows of D + 4 floats: max in
+// natural-log units, sum, two pad floats, O). Per page: S^T = K . Q^T (hi/lo)
+// scaled per (token, 32-block), masked (token < T_act, token <= past + i) and
+// scaled by 1/sqrt(D); O^T += V^T . (p * sv) (hi/lo).
 //
-// Register budget: two waves per SIMD (<= 256 VGPRs). The K fragments of the
-// next page are loaded into the same registers as soon as S is formed, and
-// the next page's V fragments as soon as the PV products are issued, so one
-// page of K and one of V are ever held. Every page is read through a buffer
-// resource whose base is that page's (page, kv head) block in the pool (64-bit
-// address arithmetic, so pools may exceed 4 GB) and whose size is the block:
-// an offset outside the block reads zero instead of faulting.
+// Latency: as soon as S is formed the wave issues the next page's loads — its
+// K and V scale blocks (1 KiB each) straight into this wave's LDS (double
+// buffered), then its K codes into the K registers — and after the PV
+// products the next page's V codes into the V registers. So one page of codes
+// is held in registers (two waves per SIMD), and no scale load waits at its
+// point of use. Scheduling barriers keep the compiler from hoisting the V
+// dequantisation into the S phase, which would make S wait for the V loads.
+// Every page is read through a buffer resource whose base is that page's
+// (page, kv head) block (64-bit address arithmetic, so pools may exceed
+// 4 GB) and whose size is the block: an offset outside it reads zero.
 //
 // Every lane builds its fragments and rescales O on every page, with no
 // branch on row state: MFMA reads all lanes' operands whatever the execution
@@ -620,8 +648,12 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
                                                  float* __restrict__ part) {
     constexpr int D = 32 * NG;
     constexpr int DT = D / 16;
+    // per wave, two pages' K and V scale blocks (64 tokens x NG groups, f32)
+    __shared__ __attribute__((aligned(16))) float ksl[4][2][256];
+    __shared__ __attribute__((aligned(16))) float vsl[4][2][256];
     const int lane = threadIdx.x & 63, j4 = lane >> 4, l16 = lane & 15;
-    const int wid = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wid = blockIdx.x * 4 + wv;
     if (wid >= nitems) return;   // no barriers below: a finished wave may leave
     const AttnItem it = items[wid];
     const JobDev jb = jobs[it.job];
@@ -652,10 +684,9 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
         return __builtin_amdgcn_make_buffer_rsrc((void*)(pool + (size_t)pg * pstride + hoff), 0, g.blk, 0x00020000);
     };
     // Lane offsets inside a block (layout of k_fin_qkv's writes):
-    const int vk = l16 * D + (D / 4) * j4;       // K codes: token row l16 of a 16-token tile, lane's k-block
-    const int vks = 64 * D + (4 * j4 * NG) * 4;  // K scales of tokens 4*j4.. of a tile
-    const int vv = l16 * 64 + 16 * j4;           // V codes: d row l16 of a d-tile, lane's token block
-    const int vvs = 64 * D + 16 * j4 * 4;        // V scales of the lane's tokens; 32-block b at +256*b
+    const int vk = l16 * D + (D / 4) * j4;   // K codes: token row l16 of a 16-token tile, lane's k-block
+    const int vv = l16 * 64 + 16 * j4;       // V codes: d row l16 of a d-tile, lane's token block
+    // Scale blocks sit at 64*D in both blocks: K [64 tokens][NG], V [NG][64 at vpos].
 
     float mrow = -INFINITY, lsum = 0.0f;
     float4_t o[DT];
@@ -663,36 +694,37 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
     for (int dt = 0; dt < DT; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     u32x4 kc[4][NG / 2], vc[DT];
-    auto load_k = [&](__amdgpu_buffer_rsrc_t r) {
+    // the next page's scale blocks into LDS buffer `buf`, then its K codes
+    auto load_k = [&](__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int buf) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)&ksl[wv][buf][0], 16, lane * 16, 64 * D, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void_t*)&vsl[wv][buf][0], 16, lane * 16, 64 * D, 0, 0);
 #pragma unroll
         for (int tt = 0; tt < 4; tt++)
 #pragma unroll
             for (int q = 0; q < NG / 2; q++)
-                kc[tt][q] = __builtin_amdgcn_raw_buffer_load_b128(r, vk, tt * 16 * D + 16 * q, 0);
+                kc[tt][q] = __builtin_amdgcn_raw_buffer_load_b128(rk, vk, tt * 16 * D + 16 * q, 0);
     };
-    auto load_v = [&](__amdgpu_buffer_rsrc_t r) {
+    auto load_v = [&](__amdgpu_buffer_rsrc_t rv) {
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) vc[dt] = __builtin_amdgcn_raw_buffer_load_b128(r, vv, dt * 1024, 0);
+        for (int dt = 0; dt < DT; dt++) vc[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, dt * 1024, 0);
     };
     if (p0 < p1) {
-        auto rk = page_rsrc(kpool, p0);
         auto rv = page_rsrc(vpool, p0);
-        load_k(rk);
+        load_k(page_rsrc(kpool, p0), rv, p0 & 1);
         load_v(rv);
         for (int p = p0; p < p1; p++) {
             // the last page reloads itself instead of branching (an L2 hit)
             const int pn = p + 1 < p1 ? p + 1 : p;
-            const auto rkn = page_rsrc(kpool, pn);
+            const int buf = p & 1;
             float pr[4][4];
             float pm = -INFINITY;
 #pragma unroll
             for (int tt = 0; tt < 4; tt++) {
-                float ks[4 * NG];
+                float ks[4 * NG];   // tokens 16tt + 4j4 + r, groups 0..NG-1
 #pragma unroll
                 for (int q = 0; q < NG; q++) {
-                    const u32x4 f = __builtin_amdgcn_raw_buffer_load_b128(rk, vks, tt * 16 * NG * 4 + 16 * q, 0);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) ks[4 * q + e] = __uint_as_float(f[e]);
+                    const float4 f = *(const float4*)&ksl[wv][buf][(tt * 16 + 4 * j4) * NG + 4 * q];
+                    ks[4 * q] = f.x; ks[4 * q + 1] = f.y; ks[4 * q + 2] = f.z; ks[4 * q + 3] = f.w;
                 }
                 float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -713,7 +745,9 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
                     pm = fmaxf(pm, pr[tt][r]);
                 }
             }
-            load_k(rkn);   // the K registers are free: start the next page
+            const auto rvn = page_rsrc(vpool, pn);
+            load_k(page_rsrc(kpool, pn), rvn, buf ^ 1);   // the K registers are free: start the next page
+            __builtin_amdgcn_sched_barrier(0);
             pm = fmaxf(pm, __shfl_xor(pm, 16));
             pm = fmaxf(pm, __shfl_xor(pm, 32));
             const float mnew = fmaxf(mrow, pm);
@@ -732,14 +766,14 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
                     pr[tt][r] = e;
                     lsum += e;
                 }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int b = 0; b < NG; b++) {
-                float sv[16];
+                float sv[16];   // the lane's 16 tokens of 32-block b
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const u32x4 f = __builtin_amdgcn_raw_buffer_load_b128(rv, vvs, b * 256 + 16 * q, 0);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) sv[4 * q + e] = __uint_as_float(f[e]);
+                    const float4 f = *(const float4*)&vsl[wv][buf][b * 64 + 16 * j4 + 4 * q];
+                    sv[4 * q] = f.x; sv[4 * q + 1] = f.y; sv[4 * q + 2] = f.z; sv[4 * q + 3] = f.w;
                 }
 #pragma unroll
                 for (int ks = 0; ks < 2; ks++) {
@@ -765,22 +799,16 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
                 }
             }
             mrow = mnew;
-            rv = page_rsrc(vpool, pn);
-            load_v(rv);
-            rk = rkn;
+            load_v(rvn);
         }
     }
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
-    float* dst = part + it.part + (size_t)l16 * (D + 2);
+    // partial row: max, sum, two pad floats, then O (16-byte aligned)
+    float* dst = part + it.part + (size_t)l16 * (D + 4);
 #pragma unroll
-    for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) dst[2 + dt * 16 + 4 * j4 + r] = o[dt][r];
-    if (j4 == 0) {
-        dst[0] = mrow;
-        dst[1] = lsum;
-    }
+    for (int dt = 0; dt < DT; dt++) *(float4_t*)(dst + 4 + dt * 16 + 4 * j4) = o[dt];
+    if (j4 == 0) *(float2*)dst = make_float2(mrow, lsum);
 }
 
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
@@ -798,80 +826,84 @@ void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev
 }
 
 // Merge the chunk partials of one (job, kv head, m-tile): log-sum-exp over
-// chunks in order, normalise, and write the merged-heads rows as the o_proj
-// operand (merge_heads, web/model/kernels.js:1315-1329, is this indexing).
-// The chunks' weights exp(m_c - M) sit in LDS.
+// chunks, normalise, and write the merged-heads rows as the o_proj operand
+// (merge_heads, web/model/kernels.js:1315-1329, is this indexing). Work item
+// i's partial sits at part + i*16*(D + 4) (items are built in that order,
+// chunk fastest). One wave per 4 rows takes each row's max and weighted sum
+// across its lanes (a fixed butterfly order, so the bits depend only on the
+// job's chunk count); the weights exp(m_c - M) go to LDS; then each thread
+// merges 8 columns of one row over the chunks in order, eight chunks' loads
+// in flight at a time.
 constexpr int COMBINE_CMAX = 512;
-__global__ __launch_bounds__(256) void k_attn_combine(const JobDev* __restrict__ jobs, int njobs,
-                                                       const AttnItem* __restrict__ items,
-                                                       const float* __restrict__ part, KVGeom g, int nH, int group,
-                                                       int KU, uint4* __restrict__ Xp, float* __restrict__ ctx_out,
-                                                       const int32_t* __restrict__ wg_job) {
-    __shared__ float wgt[16][COMBINE_CMAX + 1];
-    __shared__ float Ms[16], Ls[16];
+__global__ __launch_bounds__(256) void k_attn_combine(const JobDev* __restrict__ jobs, const float* __restrict__ part,
+                                                      KVGeom g, int nH, int group, int KU, uint4* __restrict__ Xp,
+                                                      float* __restrict__ ctx_out,
+                                                      const int32_t* __restrict__ wg_job) {
+    __shared__ float wgt[16][COMBINE_CMAX];
+    __shared__ float Ls[16];
     const int job = wg_job[3 * blockIdx.x], kvh = wg_job[3 * blockIdx.x + 1], mt = wg_job[3 * blockIdx.x + 2];
     const JobDev jb = jobs[job];
-    const int D = g.D;
+    const int D = g.D, W = D + 4;
     const int R = jb.n * group;
     const int nc = jb.nchunk;
-    const int ibase = jb.item0 + (kvh * jb.mtq + mt) * nc;
-    for (int idx = threadIdx.x; idx < 16 * nc; idx += 256) {
-        const int rl = idx / nc, c = idx % nc;
-        wgt[rl][c] = part[items[ibase + c].part + (size_t)rl * (D + 2)];
-    }
-    __syncthreads();
-    if (threadIdx.x < 16) {
-        float M = -INFINITY;
-        for (int c = 0; c < nc; c++) M = fmaxf(M, wgt[threadIdx.x][c]);
-        Ms[threadIdx.x] = M;
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < 16 * nc; idx += 256) {
-        const int rl = idx / nc, c = idx % nc;
-        const float mc = wgt[rl][c];
-        wgt[rl][c] = (mc == -INFINITY) ? 0.0f : expf(mc - Ms[rl]);
-    }
-    __syncthreads();
-    if (threadIdx.x < 16) {
-        float L = 0.0f;
-        for (int c = 0; c < nc; c++) L += part[items[ibase + c].part + (size_t)threadIdx.x * (D + 2) + 1] * wgt[threadIdx.x][c];
-        Ls[threadIdx.x] = L;
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < 16 * (D / 8); idx += 256) {
-        const int rl = idx / (D / 8), d0 = (idx % (D / 8)) * 8;
-        const int rho = mt * 16 + rl;
-        if (rho >= R) continue;
-        float O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        for (int c = 0; c < nc; c++) {
-            const float w = wgt[rl][c];
-            if (w == 0.0f) continue;
-            const float4* src = (const float4*)(part + items[ibase + c].part + (size_t)rl * (D + 2) + 2 + d0);
-            const float4 a = src[0], b = src[1];
-            O[0] += a.x * w; O[1] += a.y * w; O[2] += a.z * w; O[3] += a.w * w;
-            O[4] += b.x * w; O[5] += b.y * w; O[6] += b.z * w; O[7] += b.w * w;
+    const size_t pstride = (size_t)16 * W;
+    const float* base = part + (size_t)(jb.item0 + (kvh * jb.mtq + mt) * nc) * pstride;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int rl = wave * 4; rl < wave * 4 + 4; rl++) {
+        float mloc = -INFINITY;
+        for (int c = lane; c < nc; c += 64) mloc = fmaxf(mloc, base[c * pstride + rl * W]);
+        const float M = wave_max(mloc);
+        float lloc = 0.0f;
+        for (int c = lane; c < nc; c += 64) {
+            const float2 ml = *(const float2*)(base + c * pstride + rl * W);
+            const float w = ml.x == -INFINITY ? 0.0f : expf(ml.x - M);
+            wgt[rl][c] = w;
+            lloc += ml.y * w;
         }
-        float v[8];
-        const float L = Ls[rl];
-#pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = O[j] / L;
-        const int i = rho / group, gi = rho % group;
-        const int r = jb.row0 + i;
-        const int k = (kvh * group + gi) * D + d0;
-        if (ctx_out) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) ctx_out[(size_t)r * nH * D + k + j] = v[j];
-        }
-        write_hilo(Xp, r, k / 8, KU, v);
+        const float L = wave_sum(lloc);
+        if (lane == 0) Ls[rl] = L;
     }
+    __syncthreads();
+    const int rl = threadIdx.x / (D / 8), d0 = (threadIdx.x % (D / 8)) * 8;
+    const int rho = mt * 16 + rl;
+    if (rl >= 16 || rho >= R) return;   // no barrier below
+    const float* src = base + (size_t)rl * W + 4 + d0;
+    float O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    auto add = [&](const float4& a, const float4& b, float w) {
+        O[0] += a.x * w; O[1] += a.y * w; O[2] += a.z * w; O[3] += a.w * w;
+        O[4] += b.x * w; O[5] += b.y * w; O[6] += b.z * w; O[7] += b.w * w;
+    };
+    int c = 0;
+    for (; c + 8 <= nc; c += 8) {
+        float4 a[8], b[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            a[u] = *(const float4*)(src + (c + u) * pstride);
+            b[u] = *(const float4*)(src + (c + u) * pstride + 4);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) add(a[u], b[u], wgt[rl][c + u]);
+    }
+    for (; c < nc; c++) add(*(const float4*)(src + c * pstride), *(const float4*)(src + c * pstride + 4), wgt[rl][c]);
+    float v[8];
+    const float L = Ls[rl];
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = O[j] / L;
+    const int i = rho / group, gi = rho % group;
+    const int r = jb.row0 + i;
+    const int k = (kvh * group + gi) * D + d0;
+    if (ctx_out) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) ctx_out[(size_t)r * nH * D + k + j] = v[j];
+    }
+    write_hilo(Xp, r, k / 8, KU, v);
 }
 
-void launch_attn_combine(hipStream_t st, const JobDev* jobs, int njobs, const AttnItem* items, const float* part,
-                          const KVGeom& g, int nH, int group, int KU, uint4* Xp, float* ctx_out,
-                          const int32_t* wg_job, int nwg) {
+void launch_attn_combine(hipStream_t st, const JobDev* jobs, const float* part, const KVGeom& g, int nH, int group,
+                         int KU, uint4* Xp, float* ctx_out, const int32_t* wg_job, int nwg) {
     if (nwg <= 0) return;
-    hipLaunchKernelGGL(k_attn_combine, dim3(nwg), dim3(256), 0, st, jobs, njobs, items, part, g, nH, group, KU, Xp,
-                       ctx_out, wg_job);
+    hipLaunchKernelGGL(k_attn_combine, dim3(nwg), dim3(256), 0, st, jobs, part, g, nH, group, KU, Xp, ctx_out,
+                       wg_job);
     CHECK_LAUNCH();
 }
 
