@@ -65,7 +65,6 @@ struct cc_ctx {
     size_t qp_units = 0;
     float* apart = nullptr;
     size_t apart_floats = 0;
-    float* ssq = nullptr;          // rmsnorm partial sums [t_max][ceil(H/256)]
     int ppw = 8;                   // pages per attention work item
     AttnItem* d_items = nullptr;
     size_t items_cap = 0;
@@ -181,7 +180,8 @@ cc_status check_dims(cc_ctx* ctx, const cc_dims& d, const cc_opts& o) {
     // Fused q|k|v and gate|up start each part on a tile pair (32 rows).
     if (d.hidden % 64 || d.ffn % 32) return fail(ctx, CC_EARG, "hidden must be a multiple of 64, ffn of 32");
     if ((d.n_kv_heads * d.head_dim) % 32) return fail(ctx, CC_EARG, "n_kv_heads*head_dim must be a multiple of 32");
-    if (d.hidden > 16384) return fail(ctx, CC_EARG, "hidden above 16384 is not supported");
+    if (d.hidden > RESID_NORM_HMAX)
+        return fail(ctx, CC_EARG, "hidden above " + std::to_string(RESID_NORM_HMAX) + " is not supported");
     // The matmul addresses a weight with 32-bit byte offsets.
     const double H = d.hidden, F = d.ffn;
     const double big = std::max({(double)d.vocab * H, 2.0 * F * H, F * H,
@@ -405,7 +405,6 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         // Attention partials: 16 rows of (D + 4) floats per item.
         ctx->apart_floats = ctx->items_cap * 16 * (size_t)(D + 4);
         HIPCHK(dalloc(ctx, &ctx->apart, ctx->apart_floats * 4, &ctx->scratch_bytes));
-        HIPCHK(dalloc(ctx, &ctx->ssq, (size_t)T * ceil_div(H, 256) * 4, &ctx->scratch_bytes));
         if (ctx->head) {
             ctx->head_planes = lx_planes(ceil_div(H, 64));
             HIPCHK(dalloc(ctx, &ctx->logits, (size_t)ctx->head_planes * T * d.vocab * 4, &ctx->scratch_bytes));
@@ -756,7 +755,7 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
         Layer& L = ctx->layers[b - ctx->L0];
         if (b == b0)
             launch_resid_norm(st, ctx->x, nullptr, nullptr, 0, T, Mpad, H, 0, L.ln1, d.rms_eps, L.qkv.KU, ctx->xp_h,
-                              nullptr, ctx->ssq);
+                              nullptr);
         const int sq = L.qkv.P;
         launch_gemm(st, L.qkv, ctx->xp_h, ctx->part, T, ctx->ncu);
         launch_fin_qkv(st, ctx->part, sq, T, drow_job, djobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
@@ -768,7 +767,7 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
         const int so = L.o.P;
         launch_gemm(st, L.o, ctx->xp_o, ctx->part, T, ctx->ncu);
         launch_resid_norm(st, ctx->x, nullptr, ctx->part, so, T, Mpad, H, 0, L.ln2, d.rms_eps, L.gu.KU, ctx->xp_h,
-                          nullptr, ctx->ssq);
+                          nullptr);
         const int sg = L.gu.P;
         launch_gemm(st, L.gu, ctx->xp_h, ctx->part, T, ctx->ncu);
         launch_fin_swiglu(st, ctx->part, sg, T, Mpad, d.ffn, L.down.KU, ctx->xp_f);
@@ -777,8 +776,7 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
         const bool next = b + 1 < b1;
         launch_resid_norm(st, ctx->x, nullptr, ctx->part, sd, T, Mpad, H, 1,
                           next ? ctx->layers[b + 1 - ctx->L0].ln1 : nullptr, d.rms_eps,
-                          next ? ctx->layers[b + 1 - ctx->L0].qkv.KU : 0, next ? ctx->xp_h : nullptr, nullptr,
-                          ctx->ssq);
+                          next ? ctx->layers[b + 1 - ctx->L0].qkv.KU : 0, next ? ctx->xp_h : nullptr, nullptr);
     }
     (void)D;
 }
@@ -943,7 +941,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         const int S = p.S;
         const int Mpad = 32 * ceil_div(S, 32);
         launch_resid_norm(st, ctx->x, (const int32_t*)(ctx->d_meta + ml.head_rows), nullptr, 0, S, Mpad, d.hidden, 0,
-                          ctx->norm, d.rms_eps, hw.KU, ctx->xp_h, nullptr, ctx->ssq);
+                          ctx->norm, d.rms_eps, hw.KU, ctx->xp_h, nullptr);
         launch_gemm(st, hw, ctx->xp_h, ctx->logits, S, ctx->ncu);
         ctx->head_rows = S;
         launch_topk(st, ctx->logits, hw.P, S, d.vocab, topk, ctx->tk_a, ctx->tk_b, ctx->d_vals, ctx->d_ids);
@@ -1045,18 +1043,18 @@ cc_status cc_op_topk(cc_ctx* ctx, const float* logits, int32_t rows, int32_t V, 
 
 cc_status cc_op_rmsnorm(cc_ctx* ctx, const float* x, const float* w, int32_t T, int32_t H, float* y) {
     if (!ctx || !x || !w || !y || T < 1 || H < 1) return CC_EARG;
-    float *dx = nullptr, *dw = nullptr, *dy = nullptr, *dss = nullptr;
+    if (H % 8 || H > RESID_NORM_HMAX) return fail(ctx, CC_EARG, "rmsnorm rows must be a multiple of 8, at most 8192");
+    float *dx = nullptr, *dw = nullptr, *dy = nullptr;
     HIPCHK(hipMalloc(&dx, (size_t)T * H * 4));
     HIPCHK(hipMalloc(&dw, (size_t)H * 4));
     HIPCHK(hipMalloc(&dy, (size_t)T * H * 4));
-    HIPCHK(hipMalloc(&dss, (size_t)T * ceil_div(H, 256) * 4));
     HIPCHK(hipMemcpy(dx, x, (size_t)T * H * 4, hipMemcpyHostToDevice));
     HIPCHK(hipMemcpy(dw, w, (size_t)H * 4, hipMemcpyHostToDevice));
-    launch_resid_norm(ctx->stream, dx, nullptr, nullptr, 0, T, T, H, 0, dw, ctx->d.rms_eps, 0, nullptr, dy, dss);
+    launch_resid_norm(ctx->stream, dx, nullptr, nullptr, 0, T, T, H, 0, dw, ctx->d.rms_eps, 0, nullptr, dy);
     HIPCHK(hipStreamSynchronize(ctx->stream));
     HIPCHK(take_launch_error());
     HIPCHK(hipMemcpy(y, dy, (size_t)T * H * 4, hipMemcpyDeviceToHost));
-    for (void* v : {(void*)dx, (void*)dw, (void*)dy, (void*)dss}) hipFree(v);
+    for (void* v : {(void*)dx, (void*)dw, (void*)dy}) hipFree(v);
     return CC_OK;
 }
 

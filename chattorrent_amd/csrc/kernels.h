@@ -82,9 +82,11 @@ void launch_kv_from_ref(hipStream_t st, uint8_t* pool, const uint32_t* page_tabl
 void launch_tile_q8(hipStream_t st, const int8_t* codes, const uint16_t* scales, int N, int K,
                     int group, const QTensor& w, int row_tile0);
 hipError_t take_launch_error();
+// Residual step (planes added in order, optional f16 round) and rmsnorm into
+// the operand Xp or rows y, one workgroup per row; H % 8 == 0, H <= 8192.
+constexpr int RESID_NORM_HMAX = 8192;
 void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const float* part, int splits, int M,
-                       int Mpad, int H, int round, const float* w, float eps, int KU, uint4* Xp, float* y,
-                       float* ssq);
+                       int Mpad, int H, int round, const float* w, float eps, int KU, uint4* Xp, float* y);
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
                   const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
                   int ppw, float* part);

@@ -318,94 +318,118 @@ void launch_prep_rows(hipStream_t st, const float* x, int ldx, int M, int Mpad, 
     CHECK_LAUNCH();
 }
 
-// Sum over a workgroup of 256 as a pairwise tree in LDS (the order the
-// rmsnorm sum of squares, web/model/kernels.js:930-976, is taken in here).
-__device__ static inline float block_sum_256(float v, float* red) {
-    red[threadIdx.x] = v;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] = red[threadIdx.x] + red[threadIdx.x + s];
-        __syncthreads();
-    }
-    const float r = red[0];
-    __syncthreads();
-    return r;
-}
-
 // ========================================================= finish kernels ===
-// Residual add (web/model/kernels.js:1334-1346 add_inplace) of a projection,
-// the per-block round_f16 (:1356-1383, model.js:619-624) and the next rmsnorm
-// (:930-976) with its operand prep.
-// Spread over the whole chip: grid (column blocks of
-// 256, rows). Each block adds the projection's K splits in order to its 256
-// residual values (add_inplace), optionally rounds them (round_f16), writes
-// them back and stores its partial sum of squares; k_norm_prep then finishes
-// rmsnorm from the partials. With part == nullptr it only computes the
-// partials of x (rows gathered through `rows`), for the first block's norm
-// and the head's.
-__global__ __launch_bounds__(256) void k_resid_ssq(float* __restrict__ x, const int32_t* __restrict__ rows,
-                                                   const float* __restrict__ part, int splits, int M, int H,
-                                                   int round, float* __restrict__ ssq) {
-    __shared__ float red[256];
-    const int m = blockIdx.y;
-    const int h = blockIdx.x * 256 + threadIdx.x;
-    float v = 0.0f;
-    if (h < H) {
-        if (part) {
-            float p = part[(size_t)m * H + h];
-            for (int s = 1; s < splits; s++) p = p + part[((size_t)s * M + m) * H + h];
-            v = x[(size_t)m * H + h] + p;
-            if (round) v = round_f16_value(v);
-            x[(size_t)m * H + h] = v;
-        } else {
-            v = x[(size_t)(rows ? rows[m] : m) * H + h];
-        }
-    }
-    const float t = block_sum_256(v * v, red);
-    if (threadIdx.x == 0) ssq[(size_t)m * gridDim.x + blockIdx.x] = t;
-}
-
-// rmsnorm's scale from the partial sums (added in block order) and the
-// operand prep: y = x * (1/sqrt(ss/H + eps)) * w as f16 hi/lo fragments.
-// Grid (chunk blocks, Mpad); rows m >= M are zero.
-__global__ __launch_bounds__(256) void k_norm_prep(const float* __restrict__ x, const int32_t* __restrict__ rows,
-                                                   const float* __restrict__ ssq, int nb, int M, int H, int KU,
-                                                   const float* __restrict__ w, float eps, uint4* __restrict__ Xp,
-                                                   float* __restrict__ y) {
-    const int m = blockIdx.y;
-    const int c = blockIdx.x * 256 + threadIdx.x;
-    const int per = 8 * KU;
-    if (Xp && c >= per) return;
-    if (!Xp && 8 * c >= H) return;
-    float v[8];
+// Residual step and rmsnorm, one workgroup of 1024 threads per row, the row
+// held in registers (4 columns a thread per pass, H <= 8192):
+//   x = x + the projection's K planes added in order (add_inplace,
+//   web/model/kernels.js:1334-1346), optionally round_f16 (:1356-1383, the
+//   per-block residual round, model.js:619-624), written back;
+//   then, with w: rmsnorm (:930-976), y = x * (1/sqrt(ss/H + eps)) * w, as the
+//   next matmul's f16 hi/lo operand Xp (or as rows y). ss is summed per wave
+//   (butterfly) and then over the waves in order.
+// part == nullptr: the x rows as they are, gathered through `rows` (the entry
+// rows, the head's sampled rows). Rows M .. Mpad-1 get zero operand rows.
+constexpr int RN_THREADS = 1024, RN_PASSES = 2, RN_SPLITS = 16;
+__global__ __launch_bounds__(RN_THREADS) void k_resid_norm(float* __restrict__ x, const int32_t* __restrict__ rows,
+                                                           const float* __restrict__ part, int splits, int M, int H,
+                                                           int round, const float* __restrict__ w, float eps, int KU,
+                                                           uint4* __restrict__ Xp, float* __restrict__ y) {
+    __shared__ float red[RN_THREADS / 64];
+    __shared__ float scale_s;
+    const int m = blockIdx.x, t = threadIdx.x, lane = t & 63;
+    const int n4 = H >> 2;
     if (m >= M) {
+        const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int c8 = t; c8 < 8 * KU; c8 += RN_THREADS) write_hilo(Xp, m, c8, KU, z);
+        return;
+    }
+    const size_t xoff = (size_t)(rows ? rows[m] : m) * H;
+    const float4 zero = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 v[RN_PASSES], wv[RN_PASSES];
+    float ss = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; j++) v[j] = 0.0f;
-    } else {
+    for (int k = 0; k < RN_PASSES; k++) {
+        const int c4 = t + k * RN_THREADS;
+        v[k] = wv[k] = zero;
+        if (c4 >= n4) continue;
+        if (w) wv[k] = *(const float4*)(w + 4 * c4);   // in flight with the row's loads
+        float4 xv = *(const float4*)(x + xoff + 4 * c4);
+        if (part) {
+            // every plane's load in flight at once, through a resource sized
+            // to the planes: a load past the last one reads zero (no branch),
+            // and adding +0 leaves the in-order sum as it is
+            const auto rp = __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, splits * M * H * 4, 0x00020000);
+            float4 pv[RN_SPLITS];
+#pragma unroll
+            for (int s = 0; s < RN_SPLITS; s++) {
+                const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rp, (m * H + 4 * c4) * 4, s * M * H * 4, 0);
+                pv[s] = make_float4(__uint_as_float(q[0]), __uint_as_float(q[1]), __uint_as_float(q[2]),
+                                    __uint_as_float(q[3]));
+            }
+            float4 p = pv[0];
+#pragma unroll
+            for (int s = 1; s < RN_SPLITS; s++)
+                p = make_float4(p.x + pv[s].x, p.y + pv[s].y, p.z + pv[s].z, p.w + pv[s].w);
+            for (int s = RN_SPLITS; s < splits; s++) {
+                const float4 q = *(const float4*)(part + ((size_t)s * M + m) * H + 4 * c4);
+                p = make_float4(p.x + q.x, p.y + q.y, p.z + q.z, p.w + q.w);
+            }
+            xv = make_float4(xv.x + p.x, xv.y + p.y, xv.z + p.z, xv.w + p.w);
+            if (round)
+                xv = make_float4(round_f16_value(xv.x), round_f16_value(xv.y), round_f16_value(xv.z),
+                                 round_f16_value(xv.w));
+            *(float4*)(x + xoff + 4 * c4) = xv;
+        }
+        v[k] = xv;
+        ss = ss + xv.x * xv.x;
+        ss = ss + xv.y * xv.y;
+        ss = ss + xv.z * xv.z;
+        ss = ss + xv.w * xv.w;
+    }
+    if (!w) return;   // the residual step alone (the pass's last block)
+    ss = wave_sum(ss);
+    if (lane == 0) red[t >> 6] = ss;
+    __syncthreads();
+    if (t == 0) {
         float tot = 0.0f;
-        for (int b = 0; b < nb; b++) tot = tot + ssq[(size_t)m * nb + b];
-        const float scale = 1.0f / sqrtf(tot / (float)H + eps);
-        const float* xr = x + (size_t)(rows ? rows[m] : m) * H;
+        for (int i = 0; i < RN_THREADS / 64; i++) tot = tot + red[i];
+        scale_s = 1.0f / sqrtf(tot / (float)H + eps);
+    }
+    __syncthreads();
+    const float scale = scale_s;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int k = 8 * c + j;
-            v[j] = k < H ? xr[k] * scale * w[k] : 0.0f;
-            if (y && k < H) y[(size_t)m * H + k] = v[j];
+    for (int k = 0; k < RN_PASSES; k++) {
+        const int c4 = t + k * RN_THREADS;
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+        if (c4 < n4) {
+            o[0] = v[k].x * scale * wv[k].x;
+            o[1] = v[k].y * scale * wv[k].y;
+            o[2] = v[k].z * scale * wv[k].z;
+            o[3] = v[k].w * scale * wv[k].w;
+            if (y) *(float4*)(y + (size_t)m * H + 4 * c4) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+        if (Xp) {
+            // lanes (2i, 2i+1) hold the two halves of one 8-column operand chunk
+            float e[8];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                e[q] = o[q];
+                e[4 + q] = __shfl_xor(o[q], 1);
+            }
+            if (c4 < n4 && (c4 & 1) == 0) write_hilo(Xp, m, c4 >> 1, KU, e);
         }
     }
-    if (Xp) write_hilo(Xp, m, c, KU, v);
+    if (Xp) {
+        // operand columns past H (K padded to whole 64-column units)
+        const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int c8 = (H >> 3) + t; c8 < 8 * KU; c8 += RN_THREADS) write_hilo(Xp, m, c8, KU, z);
+    }
 }
 
-void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const float* part, int splits, int M,
-                       int Mpad, int H, int round, const float* w, float eps, int KU, uint4* Xp, float* y,
-                       float* ssq) {
-    const int nb = (H + 255) / 256;
-    hipLaunchKernelGGL(k_resid_ssq, dim3(nb, M), dim3(256), 0, st, x, rows, part, splits, M, H, round, ssq);
-    CHECK_LAUNCH();
-    if (!w) return;
-    const int chunks = Xp ? 8 * KU : (H + 7) / 8;
-    hipLaunchKernelGGL(k_norm_prep, dim3((chunks + 255) / 256, Xp ? Mpad : M), dim3(256), 0, st, x, rows, ssq, nb,
-                       M, H, KU, w, eps, Xp, y);
+void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const float* part, int splits, int M, int Mpad,
+                       int H, int round, const float* w, float eps, int KU, uint4* Xp, float* y) {
+    hipLaunchKernelGGL(k_resid_norm, dim3(Xp ? Mpad : M), dim3(RN_THREADS), 0, st, x, rows, part, splits, M, H, round,
+                       w, eps, KU, Xp, y);
     CHECK_LAUNCH();
 }
 
