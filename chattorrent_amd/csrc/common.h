@@ -122,11 +122,6 @@ __device__ static inline half8_t dequant8_biased(uint32_t lo, uint32_t hi) {
     return r;
 }
 
-// Eight signed int8 codes (the KV cache stores true codes) -> exact f16.
-__device__ static inline half8_t dequant8_signed(uint32_t lo, uint32_t hi) {
-    return dequant8_biased(lo ^ 0x80808080u, hi ^ 0x80808080u);
-}
-
 // x ≈ hi + lo with hi = f16(x) (nearest-even) and lo = f16(x - hi); the
 // difference x - hi is exact in f32, so hi + lo carries ~22 significant bits.
 // x is made opaque first: when x is a product, the compiler may otherwise fold
@@ -137,6 +132,18 @@ __device__ static inline void split_hilo(float x, _Float16& hi, _Float16& lo) {
     asm("" : "+v"(x));
     hi = (_Float16)x;
     lo = (_Float16)(x - (float)hi);
+}
+
+// Two values at once, as split_hilo (nearest-even hi, lo = f16 of the exact
+// remainder), returned packed as two f16 pairs. (Truncating the pair with
+// v_cvt_pkrtz saves two instructions but biases every lo toward zero, and the
+// bias adds up over a long softmax sum.)
+__device__ static inline void split_hilo2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    asm("" : "+v"(x0), "+v"(x1));
+    const half2_t h = {(_Float16)x0, (_Float16)x1};
+    const half2_t l = {(_Float16)(x0 - (float)h[0]), (_Float16)(x1 - (float)h[1])};
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, l);
 }
 
 __device__ static inline float wave_max(float v) {

@@ -11,6 +11,7 @@
 #include "common.h"
 #include "kernels.h"
 #include <algorithm>
+#include <type_traits>
 
 // The first launch error since the last take_launch_error(); cc_step and the
 // other entry points report it as CC_EDEVICE after their synchronisation.
@@ -503,7 +504,9 @@ void launch_fin_swiglu(hipStream_t st, const float* part, int splits, int M, int
 //   V: codes [D][64] with token s at vpos(s) = 16*((s%16)/4) + 4*(s/16) + s%4,
 //      so a lane's P·V fragments are contiguous; then f32 scales [ng][64] at
 //      the same positions.
-// Codes are the true int8 values (bit-exact with the reference's store_kv).
+// Codes are stored biased (code ^ 0x80, i.e. code + 128) so the MFMA dequant
+// puts them under an f16 exponent directly; they are the reference's store_kv
+// codes bit for bit once converted back (k_kv_ref: cc_read_kv, cc_write_kv).
 __host__ __device__ static inline int kpos(int d, int D) { return (D / 4) * ((d & 31) >> 3) + 8 * (d >> 5) + (d & 7); }
 __host__ __device__ static inline int vpos(int s) { return 16 * ((s & 15) >> 2) + 4 * (s >> 4) + (s & 3); }
 
@@ -606,10 +609,10 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
         const int8_t code = (int8_t)(int)q;
         const int b = d >> 5;
         if (which == 0) {
-            blk[(size_t)s * D + kpos(d, D)] = (uint8_t)code;
+            blk[(size_t)s * D + kpos(d, D)] = (uint8_t)((uint8_t)code ^ 0x80u);
             if ((d & 31) == 0) *(float*)(blk + 64 * D + ((size_t)s * g.ng + b) * 4) = scale;
         } else {
-            blk[(size_t)d * 64 + vpos(s)] = (uint8_t)code;
+            blk[(size_t)d * 64 + vpos(s)] = (uint8_t)((uint8_t)code ^ 0x80u);
             if ((d & 31) == 0) *(float*)(blk + 64 * D + ((size_t)b * 64 + vpos(s)) * 4) = scale;
         }
     }
@@ -645,18 +648,21 @@ void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const 
 // Attention, one wave per work item: (job, kv head, query m-tile, chunk of
 // `ppw` pages). The wave walks its pages in order and keeps an online softmax
 // (running max, sum, rescaled O) across them; its (max, sum, O) partial for
-// the 16 query rows goes to `part` (16 rows of D + 4 floats: max in
-// natural-log units, sum, two pad floats, O). Per page: S^T = K . Q^T (hi/lo)
+// the 16 query rows goes to `part` (16 rows of D + 4 floats: max in log2
+// units, sum, two pad floats, O). Per page: S^T = K . Q^T (hi/lo)
 // scaled per (token, 32-block), masked (token < T_act, token <= past + i) and
 // scaled by 1/sqrt(D); O^T += V^T . (p * sv) (hi/lo).
 //
 // Latency: as soon as S is formed the wave issues the next page's loads — its
-// K and V scale blocks (1 KiB each) straight into this wave's LDS (double
-// buffered), then its K codes into the K registers — and after the PV
-// products the next page's V codes into the V registers. So one page of codes
-// is held in registers (two waves per SIMD), and no scale load waits at its
-// point of use. Scheduling barriers keep the compiler from hoisting the V
-// dequantisation into the S phase, which would make S wait for the V loads.
+// K and V scale blocks (1 KiB each, 16 B a lane into registers, written to
+// the wave's LDS slice when that page starts), then its K codes into the K
+// registers — and after the PV products the next page's V codes into the V
+// registers. So one page of codes is held in registers (two waves per SIMD),
+// and no load waits at its point of use. (Loading the scales straight into
+// LDS instead makes the compiler wait for those in-flight loads before any
+// LDS read it cannot prove apart from them.) Scheduling barriers keep the
+// compiler from hoisting the V dequantisation into the S phase, which would
+// make S wait for the V loads.
 // Every page is read through a buffer resource whose base is that page's
 // (page, kv head) block (64-bit address arithmetic, so pools may exceed
 // 4 GB) and whose size is the block: an offset outside it reads zero.
@@ -672,9 +678,9 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
                                                  float* __restrict__ part) {
     constexpr int D = 32 * NG;
     constexpr int DT = D / 16;
-    // per wave, two pages' K and V scale blocks (64 tokens x NG groups, f32)
-    __shared__ __attribute__((aligned(16))) float ksl[4][2][256];
-    __shared__ __attribute__((aligned(16))) float vsl[4][2][256];
+    // per wave, the current page's K and V scale blocks (64 tokens x NG groups, f32)
+    __shared__ __attribute__((aligned(16))) float ksl[4][256];
+    __shared__ __attribute__((aligned(16))) float vsl[4][256];
     const int lane = threadIdx.x & 63, j4 = lane >> 4, l16 = lane & 15;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wid = blockIdx.x * 4 + wv;
@@ -687,7 +693,8 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
     const int p0 = it.chunk * ppw;
     const int p1 = min(npg, p0 + ppw);
     const int mtq = it.mt;
-    const float inv_sqrt_d = 1.0f / sqrtf((float)D);
+    // scores in log2 units: exp(s/sqrt(D)) = exp2(s * log2(e)/sqrt(D)), one v_exp_f32 each
+    const float score_scale = 1.4426950408889634f / sqrtf((float)D);
 
     uint4 qh[NG], ql[NG];
     {
@@ -718,10 +725,11 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
     for (int dt = 0; dt < DT; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     u32x4 kc[4][NG / 2], vc[DT];
-    // the next page's scale blocks into LDS buffer `buf`, then its K codes
-    auto load_k = [&](__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv, int buf) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void_t*)&ksl[wv][buf][0], 16, lane * 16, 64 * D, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void_t*)&vsl[wv][buf][0], 16, lane * 16, 64 * D, 0, 0);
+    u32x4 kst, vst;   // the next page's scale blocks, 16 B a lane, on their way to LDS
+    // the next page's scale blocks, then its K codes
+    auto load_k = [&](__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv) {
+        kst = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16, 64 * D, 0);
+        vst = __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 64 * D, 0);
 #pragma unroll
         for (int tt = 0; tt < 4; tt++)
 #pragma unroll
@@ -732,29 +740,31 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) vc[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, dt * 1024, 0);
     };
-    if (p0 < p1) {
-        auto rv = page_rsrc(vpool, p0);
-        load_k(page_rsrc(kpool, p0), rv, p0 & 1);
-        load_v(rv);
-        for (int p = p0; p < p1; p++) {
-            // the last page reloads itself instead of branching (an L2 hit)
-            const int pn = p + 1 < p1 ? p + 1 : p;
-            const int buf = p & 1;
+    // One page. Its scale blocks arrived in kst/vst during the previous page;
+    // they go to this wave's LDS slice first (a wave's LDS accesses run in
+    // order, so the previous page's reads of the slice are done).
+    auto page = [&](int p) {
+        // the last page reloads itself instead of branching (an L2 hit)
+        const int pn = p + 1 < p1 ? p + 1 : p;
+        *(u32x4*)&ksl[wv][lane * 4] = kst;
+        *(u32x4*)&vsl[wv][lane * 4] = vst;
+        {
             float pr[4][4];
+            uint32_t keep[4][4];   // all ones for a visible token, zero for a masked one
             float pm = -INFINITY;
 #pragma unroll
             for (int tt = 0; tt < 4; tt++) {
                 float ks[4 * NG];   // tokens 16tt + 4j4 + r, groups 0..NG-1
 #pragma unroll
                 for (int q = 0; q < NG; q++) {
-                    const float4 f = *(const float4*)&ksl[wv][buf][(tt * 16 + 4 * j4) * NG + 4 * q];
+                    const float4 f = *(const float4*)&ksl[wv][(tt * 16 + 4 * j4) * NG + 4 * q];
                     ks[4 * q] = f.x; ks[4 * q + 1] = f.y; ks[4 * q + 2] = f.z; ks[4 * q + 3] = f.w;
                 }
                 float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int gg = 0; gg < NG; gg++) {
                     const u32x4 c = kc[tt][gg >> 1];
-                    const half8_t kf = (gg & 1) ? dequant8_signed(c[2], c[3]) : dequant8_signed(c[0], c[1]);
+                    const half8_t kf = (gg & 1) ? dequant8_biased(c[2], c[3]) : dequant8_biased(c[0], c[1]);
                     float4_t pp = {0.f, 0.f, 0.f, 0.f};
                     pp = mfma16x16x32(kf, __builtin_bit_cast(half8_t, qh[gg]), pp);
                     pp = mfma16x16x32(kf, __builtin_bit_cast(half8_t, ql[gg]), pp);
@@ -765,17 +775,18 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
                 for (int r = 0; r < 4; r++) {
                     const int tok = p * 64 + tt * 16 + 4 * j4 + r;
                     const bool ok = tok < T_act && tok <= lim;
-                    pr[tt][r] = ok ? acc[r] * inv_sqrt_d : -INFINITY;
+                    keep[tt][r] = ok ? 0xffffffffu : 0u;
+                    pr[tt][r] = ok ? acc[r] * score_scale : -INFINITY;
                     pm = fmaxf(pm, pr[tt][r]);
                 }
             }
             const auto rvn = page_rsrc(vpool, pn);
-            load_k(page_rsrc(kpool, pn), rvn, buf ^ 1);   // the K registers are free: start the next page
+            load_k(page_rsrc(kpool, pn), rvn);   // the K registers are free: start the next page
             __builtin_amdgcn_sched_barrier(0);
             pm = fmaxf(pm, __shfl_xor(pm, 16));
             pm = fmaxf(pm, __shfl_xor(pm, 32));
             const float mnew = fmaxf(mrow, pm);
-            const float alpha = mrow == -INFINITY ? 0.0f : expf(mrow - mnew);
+            const float alpha = mrow == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrow - mnew);
             lsum *= alpha;
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
@@ -786,7 +797,7 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
             for (int tt = 0; tt < 4; tt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const float e = expf(pr[tt][r] - msub);   // masked: exp(-inf) = 0
+                    const float e = __builtin_amdgcn_exp2f(pr[tt][r] - msub);   // masked: exp2(-inf) = 0
                     pr[tt][r] = e;
                     lsum += e;
                 }
@@ -796,27 +807,31 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
                 float sv[16];   // the lane's 16 tokens of 32-block b
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const float4 f = *(const float4*)&vsl[wv][buf][b * 64 + 16 * j4 + 4 * q];
+                    const float4 f = *(const float4*)&vsl[wv][b * 64 + 16 * j4 + 4 * q];
                     sv[4 * q] = f.x; sv[4 * q + 1] = f.y; sv[4 * q + 2] = f.z; sv[4 * q + 3] = f.w;
                 }
 #pragma unroll
                 for (int ks = 0; ks < 2; ks++) {
-                    half8_t ph, pl;
+                    u32x4 phw, plw;
 #pragma unroll
-                    for (int ii = 0; ii < 8; ii++) {
+                    for (int ii = 0; ii < 8; ii += 2) {
                         const int tt = 2 * ks + (ii >> 2), r = ii & 3;
-                        // a masked token's scale may be another session's stale value: p = 0 stays 0
-                        const float pv = pr[tt][r] == 0.0f ? 0.0f : pr[tt][r] * sv[4 * tt + r];
-                        _Float16 a, c;
-                        split_hilo(pv, a, c);
-                        ph[ii] = a;
-                        pl[ii] = c;
+                        // a masked token's scale may be another session's stale value (even
+                        // NaN): its product is cleared by bits, with no branch
+                        const float p0 = __uint_as_float(__float_as_uint(pr[tt][r] * sv[4 * tt + r]) & keep[tt][r]);
+                        const float p1 =
+                            __uint_as_float(__float_as_uint(pr[tt][r + 1] * sv[4 * tt + r + 1]) & keep[tt][r + 1]);
+                        uint32_t h, l;
+                        split_hilo2(p0, p1, h, l);
+                        phw[ii >> 1] = h;
+                        plw[ii >> 1] = l;
                     }
+                    const half8_t ph = __builtin_bit_cast(half8_t, phw), pl = __builtin_bit_cast(half8_t, plw);
 #pragma unroll
                     for (int dd = 0; dd < 2; dd++) {
                         const int dt = 2 * b + dd;
                         const u32x4 c = vc[dt];
-                        const half8_t vf = ks ? dequant8_signed(c[2], c[3]) : dequant8_signed(c[0], c[1]);
+                        const half8_t vf = ks ? dequant8_biased(c[2], c[3]) : dequant8_biased(c[0], c[1]);
                         o[dt] = mfma16x16x32(vf, ph, o[dt]);
                         o[dt] = mfma16x16x32(vf, pl, o[dt]);
                     }
@@ -825,6 +840,12 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
             mrow = mnew;
             load_v(rvn);
         }
+    };
+    if (p0 < p1) {
+        const auto rv = page_rsrc(vpool, p0);
+        load_k(page_rsrc(kpool, p0), rv);
+        load_v(rv);
+        for (int p = p0; p < p1; p++) page(p);
     }
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
@@ -880,7 +901,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const JobDev* __restrict__
         float lloc = 0.0f;
         for (int c = lane; c < nc; c += 64) {
             const float2 ml = *(const float2*)(base + c * pstride + rl * W);
-            const float w = ml.x == -INFINITY ? 0.0f : expf(ml.x - M);
+            const float w = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
             wgt[rl][c] = w;
             lloc += ml.y * w;
         }
@@ -1274,8 +1295,9 @@ __global__ void k_fill_kv(uint8_t* __restrict__ pool, const uint32_t* __restrict
         const uint32_t page = page_table[(size_t)slot * g.max_pages + t / g.page];
         const int s = t % g.page;
         uint8_t* blk = pool + ((size_t)page * g.nKV + n) * g.blk;
-        if (which == 0) blk[(size_t)s * D + kpos(d, D)] = (uint8_t)code;
-        else blk[(size_t)d * 64 + vpos(s)] = (uint8_t)code;
+        const uint8_t biased = (uint8_t)((uint8_t)code ^ 0x80u);
+        if (which == 0) blk[(size_t)s * D + kpos(d, D)] = biased;
+        else blk[(size_t)d * 64 + vpos(s)] = biased;
         if ((d & 31) == 0) {
             const float sc = half_value(gen_scale_f16(seed, stream ^ 0x5ca1eull, base, 0.005, 0.02));
             const int b = d >> 5;
@@ -1297,7 +1319,8 @@ void launch_fill_kv(hipStream_t st, uint8_t* pool, const uint32_t* page_table, i
 }
 
 // Device block layout <-> the reference's rows (kernels.js:999-1022): row
-// word w < D/4 packs codes 4w..4w+3 (low byte first); then D/32 f32 scales.
+// word w < D/4 packs codes 4w..4w+3 (low byte first, signed: the pool's
+// biased bytes ^ 0x80); then D/32 f32 scales.
 __global__ void k_kv_ref(uint8_t* __restrict__ pool, const uint32_t* __restrict__ page_table, int slot, int head,
                          int t0, int t1, KVGeom g, int which, uint32_t* __restrict__ rows, int to_ref) {
     const int D = g.D, RW = D / 4 + g.ng;
@@ -1316,11 +1339,11 @@ __global__ void k_kv_ref(uint8_t* __restrict__ pool, const uint32_t* __restrict_
             }
             if (to_ref) {
                 uint32_t word = 0;
-                for (int j = 0; j < 4; j++) word |= (uint32_t)(*p[j]) << (8 * j);
+                for (int j = 0; j < 4; j++) word |= (uint32_t)(*p[j] ^ 0x80u) << (8 * j);
                 rows[i] = word;
             } else {
                 const uint32_t word = rows[i];
-                for (int j = 0; j < 4; j++) *p[j] = (uint8_t)(word >> (8 * j));
+                for (int j = 0; j < 4; j++) *p[j] = (uint8_t)((word >> (8 * j)) ^ 0x80u);
             }
         } else {
             const int b = w - D / 4;
