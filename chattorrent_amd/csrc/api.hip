@@ -195,6 +195,8 @@ cc_status check_dims(cc_ctx* ctx, const cc_dims& d, const cc_opts& o) {
         return fail(ctx, CC_EARG, "n_max, t_max, slots, sessions and max_jobs must be positive");
     if (o.page_tokens != 64) return fail(ctx, CC_EARG, "page_tokens must be 64 (web/split.js:75)");
     if (o.t_max > 4096) return fail(ctx, CC_EARG, "t_max above 4096 rows is not supported");
+    // attention chunks of ceil(pages/512) pages, at most 64 (one page index a lane)
+    if ((int64_t)o.n_max > (int64_t)64 * 512 * 64) return fail(ctx, CC_EARG, "n_max above 2097152 tokens is not supported");
     return CC_OK;
 }
 
@@ -400,7 +402,7 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         HIPCHK(dalloc(ctx, &ctx->qp, ctx->qp_units * 16, &ctx->scratch_bytes));
         // Attention work items: `ppw` pages each, at most COMBINE_CMAX chunks a
         // frame (the combine kernel's LDS).
-        ctx->ppw = std::max(8, ceil_div(ctx->max_pages, 512));
+        ctx->ppw = std::max(8, ceil_div(ctx->max_pages, 512));   // <= 64 (check_dims)
         ctx->items_cap = max_items_for(ctx);
         // Attention partials: 16 rows of (D + 4) floats per item.
         ctx->apart_floats = ctx->items_cap * 16 * (size_t)(D + 4);

@@ -710,8 +710,11 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
     const uint32_t* pt = page_table + (size_t)jb.slot * g.max_pages;
     const size_t hoff = (size_t)it.kvh * g.blk;
     const size_t pstride = (size_t)g.nKV * g.blk;
+    // The chunk's page indices, one a lane (ppw <= 64): a page reads its own
+    // with v_readlane, so no memory access sits on the page-to-page path.
+    const uint32_t pgv = lane < p1 - p0 ? pt[p0 + lane] : 0u;
     auto page_rsrc = [&](const uint8_t* pool, int p) {
-        const uint32_t pg = __builtin_amdgcn_readfirstlane(pt[p]);
+        const uint32_t pg = __builtin_amdgcn_readlane(pgv, p - p0);
         return __builtin_amdgcn_make_buffer_rsrc((void*)(pool + (size_t)pg * pstride + hoff), 0, g.blk, 0x00020000);
     };
     // Lane offsets inside a block (layout of k_fin_qkv's writes):
