@@ -877,18 +877,20 @@ void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev
 // chunks, normalise, and write the merged-heads rows as the o_proj operand
 // (merge_heads, web/model/kernels.js:1315-1329, is this indexing). Work item
 // i's partial sits at part + i*16*(D + 4) (items are built in that order,
-// chunk fastest). One wave per 4 rows takes each row's max and weighted sum
+// chunk fastest). One wave per row takes the row's max and weighted sum
 // across its lanes (a fixed butterfly order, so the bits depend only on the
-// job's chunk count); the weights exp(m_c - M) go to LDS; then each thread
-// merges 8 columns of one row over the chunks in order, eight chunks' loads
-// in flight at a time.
-constexpr int COMBINE_CMAX = 512;
-__global__ __launch_bounds__(256) void k_attn_combine(const JobDev* __restrict__ jobs, const float* __restrict__ part,
-                                                      KVGeom g, int nH, int group, int KU, uint4* __restrict__ Xp,
-                                                      float* __restrict__ ctx_out,
-                                                      const int32_t* __restrict__ wg_job) {
+// job's chunk count); the weights exp2(m_c - M) go to LDS. Then four groups
+// of 256 threads each merge a quarter of the chunks (in order, eight chunks'
+// loads in flight), one row's 8 columns a thread, and the quarters are added
+// in order through LDS.
+constexpr int COMBINE_CMAX = 512, COMBINE_SPLIT = 4;
+__global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict__ jobs, const float* __restrict__ part,
+                                                       KVGeom g, int nH, int group, int KU, uint4* __restrict__ Xp,
+                                                       float* __restrict__ ctx_out,
+                                                       const int32_t* __restrict__ wg_job) {
     __shared__ float wgt[16][COMBINE_CMAX];
     __shared__ float Ls[16];
+    __shared__ float4 red[COMBINE_SPLIT - 1][256][2];
     const int job = wg_job[3 * blockIdx.x], kvh = wg_job[3 * blockIdx.x + 1], mt = wg_job[3 * blockIdx.x + 2];
     const JobDev jb = jobs[job];
     const int D = g.D, W = D + 4;
@@ -897,7 +899,8 @@ __global__ __launch_bounds__(256) void k_attn_combine(const JobDev* __restrict__
     const size_t pstride = (size_t)16 * W;
     const float* base = part + (size_t)(jb.item0 + (kvh * jb.mtq + mt) * nc) * pstride;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int rl = wave * 4; rl < wave * 4 + 4; rl++) {
+    {
+        const int rl = wave;   // 16 waves, one row each
         float mloc = -INFINITY;
         for (int c = lane; c < nc; c += 64) mloc = fmaxf(mloc, base[c * pstride + rl * W]);
         const float M = wave_max(mloc);
@@ -912,27 +915,43 @@ __global__ __launch_bounds__(256) void k_attn_combine(const JobDev* __restrict__
         if (lane == 0) Ls[rl] = L;
     }
     __syncthreads();
-    const int rl = threadIdx.x / (D / 8), d0 = (threadIdx.x % (D / 8)) * 8;
-    const int rho = mt * 16 + rl;
-    if (rl >= 16 || rho >= R) return;   // no barrier below
-    const float* src = base + (size_t)rl * W + 4 + d0;
+    const int sub = threadIdx.x >> 8, t = threadIdx.x & 255;
+    const int rl = t / (D / 8), d0 = (t % (D / 8)) * 8;
+    const bool live = rl < 16;
     float O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    auto add = [&](const float4& a, const float4& b, float w) {
-        O[0] += a.x * w; O[1] += a.y * w; O[2] += a.z * w; O[3] += a.w * w;
-        O[4] += b.x * w; O[5] += b.y * w; O[6] += b.z * w; O[7] += b.w * w;
-    };
-    int c = 0;
-    for (; c + 8 <= nc; c += 8) {
-        float4 a[8], b[8];
+    if (live) {
+        const float* src = base + (size_t)rl * W + 4 + d0;
+        auto add = [&](const float4& a, const float4& b, float w) {
+            O[0] += a.x * w; O[1] += a.y * w; O[2] += a.z * w; O[3] += a.w * w;
+            O[4] += b.x * w; O[5] += b.y * w; O[6] += b.z * w; O[7] += b.w * w;
+        };
+        const int c1 = ((sub + 1) * nc) / COMBINE_SPLIT;
+        int c = (sub * nc) / COMBINE_SPLIT;
+        for (; c + 8 <= c1; c += 8) {
+            float4 a[8], b[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            a[u] = *(const float4*)(src + (c + u) * pstride);
-            b[u] = *(const float4*)(src + (c + u) * pstride + 4);
+            for (int u = 0; u < 8; u++) {
+                a[u] = *(const float4*)(src + (c + u) * pstride);
+                b[u] = *(const float4*)(src + (c + u) * pstride + 4);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) add(a[u], b[u], wgt[rl][c + u]);
         }
-#pragma unroll
-        for (int u = 0; u < 8; u++) add(a[u], b[u], wgt[rl][c + u]);
+        for (; c < c1; c++) add(*(const float4*)(src + c * pstride), *(const float4*)(src + c * pstride + 4), wgt[rl][c]);
+        if (sub > 0) {
+            red[sub - 1][t][0] = make_float4(O[0], O[1], O[2], O[3]);
+            red[sub - 1][t][1] = make_float4(O[4], O[5], O[6], O[7]);
+        }
     }
-    for (; c < nc; c++) add(*(const float4*)(src + c * pstride), *(const float4*)(src + c * pstride + 4), wgt[rl][c]);
+    __syncthreads();
+    const int rho = mt * 16 + rl;
+    if (sub > 0 || !live || rho >= R) return;   // no barrier below
+#pragma unroll
+    for (int q = 0; q < COMBINE_SPLIT - 1; q++) {
+        const float4 a = red[q][t][0], b = red[q][t][1];
+        O[0] += a.x; O[1] += a.y; O[2] += a.z; O[3] += a.w;
+        O[4] += b.x; O[5] += b.y; O[6] += b.z; O[7] += b.w;
+    }
     float v[8];
     const float L = Ls[rl];
 #pragma unroll
@@ -950,7 +969,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(const JobDev* __restrict__
 void launch_attn_combine(hipStream_t st, const JobDev* jobs, const float* part, const KVGeom& g, int nH, int group,
                          int KU, uint4* Xp, float* ctx_out, const int32_t* wg_job, int nwg) {
     if (nwg <= 0) return;
-    hipLaunchKernelGGL(k_attn_combine, dim3(nwg), dim3(256), 0, st, jobs, part, g, nH, group, KU, Xp, ctx_out,
+    hipLaunchKernelGGL(k_attn_combine, dim3(nwg), dim3(1024), 0, st, jobs, part, g, nH, group, KU, Xp, ctx_out,
                        wg_job);
     CHECK_LAUNCH();
 }
