@@ -551,17 +551,31 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
     const int hidx = blockIdx.x * 4 + wave;
     const bool live = hidx < nall;
     const int N = nall * D;
-    if (live)
-        for (int d = lane; d < D; d += 64) {
-            const size_t e = (size_t)hidx * D + d;
-            float p = part[(size_t)m * N + e];
-            for (int s = 1; s < splits; s++) p = p + part[((size_t)s * M + m) * N + e];
-            buf[wave][d] = p;
-        }
-    __syncthreads();
+    // the row's job and its page, looked up while the planes load
     const JobDev jb = jobs[row_job[m]];
     const int i = m - jb.row0;
     const int pos = jb.past + i;
+    const uint32_t page = page_table[(size_t)jb.slot * g.max_pages + pos / g.page];
+    if (live) {
+        // every plane's load in flight at once, through a resource sized to the
+        // planes: past the last one a load reads zero (no branch), and adding
+        // +0 leaves the in-order sum as it is
+        constexpr int SU = 16;
+        const auto rp = __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, splits * M * N * 4, 0x00020000);
+#pragma unroll
+        for (int d0 = 0; d0 < D; d0 += 64) {
+            const int at = (m * N + hidx * D + d0 + lane) * 4;
+            float pv[SU];
+#pragma unroll
+            for (int s = 0; s < SU; s++) pv[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, at, s * M * N * 4, 0));
+            float p = pv[0];
+#pragma unroll
+            for (int s = 1; s < SU; s++) p = p + pv[s];
+            for (int s = SU; s < splits; s++) p = p + part[((size_t)s * M + m) * N + hidx * D + d0 + lane];
+            buf[wave][d0 + lane] = p;
+        }
+    }
+    __syncthreads();
     if (live && hidx < nH) {
         if (do_q) {
             for (int d = lane; d < D; d += 64) rq[wave][d] = rope_at(buf[wave], d, rot, tbl, pos);
@@ -593,7 +607,6 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
     if (!do_kv) return;
     const int which = hidx < nH + nKV ? 0 : 1;
     const int n = hidx - nH - which * nKV;
-    const uint32_t page = page_table[(size_t)jb.slot * g.max_pages + pos / g.page];
     const int s = pos % g.page;
     uint8_t* blk = (which ? vpool : kpool) + ((size_t)page * nKV + n) * g.blk;
 #pragma unroll
