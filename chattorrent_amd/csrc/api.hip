@@ -58,6 +58,7 @@ struct cc_ctx {
     uint4* xp_h = nullptr;         // operand for K = hidden
     uint4* xp_o = nullptr;         // operand for K = nH*D
     uint4* xp_f = nullptr;         // operand for K = ffn
+    float* ssp = nullptr;          // rmsnorm partial sums of squares [rows][RW_SMAX]
     float* part = nullptr;
     size_t part_floats = 0;
     int ncu = 0;                   // compute units: the matmul's workgroup count
@@ -390,6 +391,7 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         HIPCHK(dalloc(ctx, &ctx->xp_h, xp_bytes(H), &ctx->scratch_bytes));
         HIPCHK(dalloc(ctx, &ctx->xp_o, xp_bytes(nH * D), &ctx->scratch_bytes));
         HIPCHK(dalloc(ctx, &ctx->xp_f, xp_bytes(F), &ctx->scratch_bytes));
+        HIPCHK(dalloc(ctx, &ctx->ssp, (size_t)16 * ctx->mt_alloc * RW_SMAX * 4, &ctx->scratch_bytes));
         size_t pf = 16;
         if (!ctx->layers.empty()) {
             const Layer& L = ctx->layers[0];
@@ -740,10 +742,11 @@ static cc_status grow(cc_ctx* ctx, const StepPlan& p) {
 
 // The blocks [p0, p1) (model indices) over the packed rows: blockSegs
 // (web/model/model.js:619-624) per layer, with the reference's dispatches
-// fused into: operand prep, q|k|v GEMM, finish (RoPE + KV store + Q operand),
-// attention, combine (o_proj operand), o GEMM, finish (residual + rmsnorm),
-// gate|up GEMM, finish (SwiGLU), down GEMM, finish (residual + round_f16 +
-// the next block's rmsnorm).
+// fused into: operand prep, q|k|v GEMM, finish (rmsnorm's row factor + RoPE +
+// KV store + Q operand), attention, combine (o_proj operand), o GEMM,
+// residual (+ operand x*ln2 and the row's sum of squares), gate|up GEMM,
+// finish (row factor + SwiGLU), down GEMM, residual (+ round_f16 + the next
+// block's operand x*ln1 and sum of squares).
 static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int b0, int b1) {
     const cc_dims& d = ctx->d;
     hipStream_t st = ctx->stream;
@@ -753,32 +756,34 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
     const AttnItem* ditems = (const AttnItem*)(ctx->d_meta + ml.items);
     const int32_t* drow_job = (const int32_t*)(ctx->d_meta + ml.row_job);
     const int32_t* dcwg = (const int32_t*)(ctx->d_meta + ml.cwg);
+    // rmsnorm's row factor, applied by the finish after each normed matmul
+    RowScale rs;
+    rs.ssp = ctx->ssp;
+    rs.nsl = ceil_div(H / 4, RW_THREADS);
+    rs.H = H;
+    rs.eps = d.rms_eps;
     for (int b = b0; b < b1; b++) {
         Layer& L = ctx->layers[b - ctx->L0];
-        if (b == b0)
-            launch_resid_norm(st, ctx->x, nullptr, nullptr, 0, T, Mpad, H, 0, L.ln1, d.rms_eps, L.qkv.KU, ctx->xp_h,
-                              nullptr);
+        if (b == b0) launch_resid_w(st, ctx->x, nullptr, 0, T, Mpad, H, 0, L.ln1, L.qkv.KU, ctx->xp_h, ctx->ssp);
         const int sq = L.qkv.P;
         launch_gemm(st, L.qkv, ctx->xp_h, ctx->part, T, ctx->ncu);
         launch_fin_qkv(st, ctx->part, sq, T, drow_job, djobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
-                       L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 1);
+                       L.kpool, L.vpool, ctx->page_table, ctx->qp, rs, 1, 1);
         launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
                      ctx->ppw, ctx->apart);
         launch_attn_combine(st, djobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU,
                              ctx->xp_o, nullptr, dcwg, p.ncwg);
         const int so = L.o.P;
         launch_gemm(st, L.o, ctx->xp_o, ctx->part, T, ctx->ncu);
-        launch_resid_norm(st, ctx->x, nullptr, ctx->part, so, T, Mpad, H, 0, L.ln2, d.rms_eps, L.gu.KU, ctx->xp_h,
-                          nullptr);
+        launch_resid_w(st, ctx->x, ctx->part, so, T, Mpad, H, 0, L.ln2, L.gu.KU, ctx->xp_h, ctx->ssp);
         const int sg = L.gu.P;
         launch_gemm(st, L.gu, ctx->xp_h, ctx->part, T, ctx->ncu);
-        launch_fin_swiglu(st, ctx->part, sg, T, Mpad, d.ffn, L.down.KU, ctx->xp_f);
+        launch_fin_swiglu(st, ctx->part, sg, T, Mpad, d.ffn, L.down.KU, ctx->xp_f, rs);
         const int sd = L.down.P;
         launch_gemm(st, L.down, ctx->xp_f, ctx->part, T, ctx->ncu);
         const bool next = b + 1 < b1;
-        launch_resid_norm(st, ctx->x, nullptr, ctx->part, sd, T, Mpad, H, 1,
-                          next ? ctx->layers[b + 1 - ctx->L0].ln1 : nullptr, d.rms_eps,
-                          next ? ctx->layers[b + 1 - ctx->L0].qkv.KU : 0, next ? ctx->xp_h : nullptr, nullptr);
+        launch_resid_w(st, ctx->x, ctx->part, sd, T, Mpad, H, 1, next ? ctx->layers[b + 1 - ctx->L0].ln1 : nullptr,
+                       next ? ctx->layers[b + 1 - ctx->L0].qkv.KU : 0, next ? ctx->xp_h : nullptr, ctx->ssp);
     }
     (void)D;
 }
@@ -1121,7 +1126,7 @@ cc_status cc_op_store_kv(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot
     Layer& L = ctx->layers[layer - ctx->L0];
     launch_fin_qkv(ctx->stream, dr, 1, T_new, (const int32_t*)(ctx->d_meta + ml.row_job),
                    (const JobDev*)(ctx->d_meta + ml.jobs), d.n_heads, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
-                   L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 0, 1);
+                   L.kpool, L.vpool, ctx->page_table, ctx->qp, RowScale{}, 0, 1);
     HIPCHK(hipStreamSynchronize(ctx->stream));
     hipFree(dr);
     for (int h = 0; h < d.n_kv_heads; h++) {
@@ -1158,7 +1163,7 @@ cc_status cc_op_attend(cc_ctx* ctx, int32_t layer, int32_t slot, const float* q,
     const JobDev* dj = (const JobDev*)(ctx->d_meta + ml.jobs);
     const AttnItem* di = (const AttnItem*)(ctx->d_meta + ml.items);
     launch_fin_qkv(st, dr, 1, n, (const int32_t*)(ctx->d_meta + ml.row_job), dj, d.n_heads, ctx->group, ctx->geom,
-                   ctx->tbl, ctx->rot, L.kpool, L.vpool, ctx->page_table, ctx->qp, nullptr, 1, 0);
+                   ctx->tbl, ctx->rot, L.kpool, L.vpool, ctx->page_table, ctx->qp, RowScale{}, 1, 0);
     launch_attn(st, di, p.nitems, dj, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->ppw,
                  ctx->apart);
     launch_attn_combine(st, dj, ctx->apart, ctx->geom, d.n_heads, ctx->group, KU, dXp, dctx,

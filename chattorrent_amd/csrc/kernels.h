@@ -50,17 +50,28 @@ struct KVGeom {
     int max_pages;
 };
 
+constexpr int RESID_NORM_HMAX = 8192;
+// rmsnorm's per-row factor 1/sqrt(ss/H + eps), from the slices' partial sums
+// of squares ssp[m*RW_SMAX + s], s < nsl (added in slice order). With ssp
+// null the factor is 1.
+constexpr int RW_THREADS = 128, RW_SMAX = RESID_NORM_HMAX / 4 / RW_THREADS;
+struct RowScale {
+    const float* ssp = nullptr;
+    int nsl = 0, H = 1;
+    float eps = 0.f;
+};
+
 // Y planes: out[(r*M + m)*N + n], r < w.P.
 void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, int ncu);
 int lx_groups(const QTensor& w, int ncu);
 void launch_prep_rows(hipStream_t st, const float* x, int ldx, int M, int Mpad, int K, int KU,
                       uint4* Xp);
 void launch_fin_swiglu(hipStream_t st, const float* part, int splits, int M, int Mpad, int F,
-                       int KU, uint4* Xp);
+                       int KU, uint4* Xp, const RowScale& rs);
 void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const int32_t* row_job,
                     const JobDev* jobs, int nH, int group, const KVGeom& g, const float* tbl,
                     int rot, uint8_t* kpool, uint8_t* vpool, const uint32_t* page_table,
-                    uint4* Qp, float* qkv_out, int do_q, int do_kv);
+                    uint4* Qp, const RowScale& rs, int do_q, int do_kv);
 void launch_embed(hipStream_t st, const int32_t* ids, const uint16_t* hidden, int T, const QTensor& wte,
                   float* x);
 void launch_topk(hipStream_t st, const float* logits, int planes, int rows, int V, int M, uint64_t* a,
@@ -84,7 +95,11 @@ void launch_tile_q8(hipStream_t st, const int8_t* codes, const uint16_t* scales,
 hipError_t take_launch_error();
 // Residual step (planes added in order, optional f16 round) and rmsnorm into
 // the operand Xp or rows y, one workgroup per row; H % 8 == 0, H <= 8192.
-constexpr int RESID_NORM_HMAX = 8192;
+// Residual step and the next matmul's operand x*w (rmsnorm without its row
+// factor, which the matmul's consumer applies: RowScale), over (slice, row)
+// workgroups; H % 64 == 0. With w null only the residual step runs.
+void launch_resid_w(hipStream_t st, float* x, const float* part, int splits, int M, int Mpad, int H, int round,
+                    const float* w, int KU, uint4* Xp, float* ssp);
 void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const float* part, int splits, int M,
                        int Mpad, int H, int round, const float* w, float eps, int KU, uint4* Xp, float* y);
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,

@@ -434,10 +434,113 @@ void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const floa
     CHECK_LAUNCH();
 }
 
+// rmsnorm (web/model/kernels.js:930-976) is y = x * f * w with the row factor
+// f = 1/sqrt(ss/H + eps); the matmul that follows is linear in its operand,
+// so (x*f*w) . W^T = f * ((x*w) . W^T). The residual kernel below writes the
+// operand x*w and the row's partial sums of squares; the matmul's consumer
+// multiplies the summed planes by f (row_scale). This takes the row-wide
+// reduction off the path between the residual step and the matmul, so the
+// residual step spreads over (slice, row) workgroups instead of one per row.
+__device__ static inline float row_scale(const RowScale& rs, int m) {
+    if (!rs.ssp) return 1.0f;
+    const float* q = rs.ssp + (size_t)m * RW_SMAX;
+    float tot = 0.0f;
+    for (int s = 0; s < rs.nsl; s++) tot = tot + q[s];
+    return 1.0f / sqrtf(tot / (float)rs.H + rs.eps);
+}
+
+// Residual step (add_inplace, web/model/kernels.js:1334-1346: x plus the
+// projection's planes added in order; optional round_f16, :1356-1383, the
+// per-block round of model.js:619-624), then, with w, the next matmul's
+// operand x*w as f16 hi/lo and this slice's sum of squares of x (each
+// thread's 4 values in order, a wave butterfly, the two waves in order) at
+// ssp[m*RW_SMAX + slice]. Workgroup (slice, row): 128 threads, a float4 of
+// the row each. part == nullptr: x as it is. Rows M .. Mpad-1 get zero
+// operand rows. H % 64 == 0, so the operand has no padding columns.
+__global__ __launch_bounds__(RW_THREADS) void k_resid_w(float* __restrict__ x, const float* __restrict__ part,
+                                                      int splits, int M, int H, int round,
+                                                      const float* __restrict__ w, int KU, uint4* __restrict__ Xp,
+                                                      float* __restrict__ ssp) {
+    __shared__ float red[RW_THREADS / 64];
+    const int m = blockIdx.y, sl = blockIdx.x, t = threadIdx.x, lane = t & 63;
+    const int n4 = H >> 2, c4 = sl * RW_THREADS + t;
+    const bool live = c4 < n4;
+    if (m >= M) {
+        if (Xp && live && (c4 & 1) == 0) {
+            const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            write_hilo(Xp, m, c4 >> 1, KU, z);
+        }
+        return;
+    }
+    const size_t xoff = (size_t)m * H + 4 * (size_t)c4;
+    float4 xv = make_float4(0.f, 0.f, 0.f, 0.f), wv = xv;
+    if (live) {
+        if (w) wv = *(const float4*)(w + 4 * c4);
+        xv = *(const float4*)(x + xoff);
+        if (part) {
+            // every plane's load in flight at once, through a resource sized
+            // to the planes: a load past the last one reads zero (no branch),
+            // and adding +0 leaves the in-order sum as it is
+            const auto rp = __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, splits * M * H * 4, 0x00020000);
+            float4 pv[RN_SPLITS];
+#pragma unroll
+            for (int s = 0; s < RN_SPLITS; s++) {
+                const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rp, (int)xoff * 4, s * M * H * 4, 0);
+                pv[s] = make_float4(__uint_as_float(q[0]), __uint_as_float(q[1]), __uint_as_float(q[2]),
+                                    __uint_as_float(q[3]));
+            }
+            float4 pp = pv[0];
+#pragma unroll
+            for (int s = 1; s < RN_SPLITS; s++)
+                pp = make_float4(pp.x + pv[s].x, pp.y + pv[s].y, pp.z + pv[s].z, pp.w + pv[s].w);
+            for (int s = RN_SPLITS; s < splits; s++) {
+                const float4 q = *(const float4*)(part + (size_t)s * M * H + xoff);
+                pp = make_float4(pp.x + q.x, pp.y + q.y, pp.z + q.z, pp.w + q.w);
+            }
+            xv = make_float4(xv.x + pp.x, xv.y + pp.y, xv.z + pp.z, xv.w + pp.w);
+            if (round)
+                xv = make_float4(round_f16_value(xv.x), round_f16_value(xv.y), round_f16_value(xv.z),
+                                 round_f16_value(xv.w));
+            *(float4*)(x + xoff) = xv;
+        }
+    }
+    if (!w) return;   // the residual step alone (the pass's last block)
+    float ss = 0.0f;
+    ss = ss + xv.x * xv.x;
+    ss = ss + xv.y * xv.y;
+    ss = ss + xv.z * xv.z;
+    ss = ss + xv.w * xv.w;
+    ss = wave_sum(ss);
+    if (lane == 0) red[t >> 6] = ss;
+    // lanes (2i, 2i+1) hold the two halves of one 8-column operand chunk
+    float o[4] = {xv.x * wv.x, xv.y * wv.y, xv.z * wv.z, xv.w * wv.w};
+    float e[8];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        e[q] = o[q];
+        e[4 + q] = __shfl_xor(o[q], 1);
+    }
+    if (live && (c4 & 1) == 0) write_hilo(Xp, m, c4 >> 1, KU, e);
+    __syncthreads();
+    if (t == 0) {
+        float tot = 0.0f;
+        for (int i = 0; i < RW_THREADS / 64; i++) tot = tot + red[i];
+        ssp[(size_t)m * RW_SMAX + sl] = tot;
+    }
+}
+
+void launch_resid_w(hipStream_t st, float* x, const float* part, int splits, int M, int Mpad, int H, int round,
+                    const float* w, int KU, uint4* Xp, float* ssp) {
+    const int nsl = (H / 4 + RW_THREADS - 1) / RW_THREADS;
+    hipLaunchKernelGGL(k_resid_w, dim3(nsl, w ? Mpad : M), dim3(RW_THREADS), 0, st, x, part, splits, M, H, round, w,
+                       KU, Xp, ssp);
+    CHECK_LAUNCH();
+}
+
 // SwiGLU (web/model/kernels.js:1513-1529 silu_mul): act = g * (1/(1+exp(-g)))
 // * up over the fused gate|up projection, straight into the down operand.
 __global__ __launch_bounds__(256) void k_fin_swiglu(const float* __restrict__ part, int splits, int M, int Mpad,
-                                                    int F, int KU, uint4* __restrict__ Xp) {
+                                                    int F, int KU, uint4* __restrict__ Xp, RowScale rs) {
     // one thread per (row, 8 columns); the planes are added in order
     const int per = 8 * KU;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -479,6 +582,13 @@ __global__ __launch_bounds__(256) void k_fin_swiglu(const float* __restrict__ pa
                 }
             }
         }
+        // the gate|up operand carried x*w: rmsnorm's row factor goes on here
+        const float f = row_scale(rs, m);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            g[j] = g[j] * f;
+            u[j] = u[j] * f;
+        }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const float sc = 1.0f / (1.0f + expf(-g[j]));
@@ -489,10 +599,10 @@ __global__ __launch_bounds__(256) void k_fin_swiglu(const float* __restrict__ pa
 }
 
 void launch_fin_swiglu(hipStream_t st, const float* part, int splits, int M, int Mpad, int F, int KU,
-                       uint4* Xp) {
+                       uint4* Xp, const RowScale& rs) {
     const int total = Mpad * 8 * KU;
     hipLaunchKernelGGL(k_fin_swiglu, dim3((total + 255) / 256), dim3(256), 0, st, part, splits, M, Mpad, F,
-                       KU, Xp);
+                       KU, Xp, rs);
     CHECK_LAUNCH();
 }
 
@@ -541,7 +651,7 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
                                                   const float* __restrict__ tbl, int rot, uint8_t* __restrict__ kpool,
                                                   uint8_t* __restrict__ vpool,
                                                   const uint32_t* __restrict__ page_table, uint4* __restrict__ Qp,
-                                                  int do_q, int do_kv) {
+                                                  RowScale rs, int do_q, int do_kv) {
     __shared__ float buf[4][D];
     __shared__ float rq[4][D];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -556,6 +666,8 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
     const int i = m - jb.row0;
     const int pos = jb.past + i;
     const uint32_t page = page_table[(size_t)jb.slot * g.max_pages + pos / g.page];
+    // the q|k|v operand carried x*w: rmsnorm's row factor goes on here
+    const float f = row_scale(rs, m);
     if (live) {
         // every plane's load in flight at once, through a resource sized to the
         // planes: past the last one a load reads zero (no branch), and adding
@@ -572,7 +684,7 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
 #pragma unroll
             for (int s = 1; s < SU; s++) p = p + pv[s];
             for (int s = SU; s < splits; s++) p = p + part[((size_t)s * M + m) * N + hidx * D + d0 + lane];
-            buf[wave][d0 + lane] = p;
+            buf[wave][d0 + lane] = p * f;
         }
     }
     __syncthreads();
@@ -633,17 +745,16 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
 
 void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const int32_t* row_job,
                     const JobDev* jobs, int nH, int group, const KVGeom& g, const float* tbl, int rot,
-                    uint8_t* kpool, uint8_t* vpool, const uint32_t* page_table, uint4* Qp, float* qkv_out,
+                    uint8_t* kpool, uint8_t* vpool, const uint32_t* page_table, uint4* Qp, const RowScale& rs,
                     int do_q, int do_kv) {
-    (void)qkv_out;
     const int nall = nH + 2 * g.nKV;
     dim3 grid((nall + 3) / 4, M);
     if (g.D == 128)
         hipLaunchKernelGGL(k_fin_qkv<128>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
-                           rot, kpool, vpool, page_table, Qp, do_q, do_kv);
+                           rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv);
     else
         hipLaunchKernelGGL(k_fin_qkv<64>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
-                           rot, kpool, vpool, page_table, Qp, do_q, do_kv);
+                           rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv);
     CHECK_LAUNCH();
 }
 
