@@ -443,9 +443,16 @@ void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const floa
 // residual step spreads over (slice, row) workgroups instead of one per row.
 __device__ static inline float row_scale(const RowScale& rs, int m) {
     if (!rs.ssp) return 1.0f;
-    const float* q = rs.ssp + (size_t)m * RW_SMAX;
+    // all RW_SMAX loads in flight at once through a resource sized to the nsl
+    // partials (past them a load reads zero, and adding +0 changes nothing)
+    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void*)(rs.ssp + (size_t)m * RW_SMAX), 0, rs.nsl * 4,
+                                                      0x00020000);
+    float q[RW_SMAX];
+#pragma unroll
+    for (int s = 0; s < RW_SMAX; s++) q[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rq, 4 * s, 0, 0));
     float tot = 0.0f;
-    for (int s = 0; s < rs.nsl; s++) tot = tot + q[s];
+#pragma unroll
+    for (int s = 0; s < RW_SMAX; s++) tot = tot + q[s];
     return 1.0f / sqrtf(tot / (float)rs.H + rs.eps);
 }
 
@@ -549,6 +556,9 @@ __global__ __launch_bounds__(256) void k_fin_swiglu(const float* __restrict__ pa
     const size_t N2 = 2 * (size_t)F, plane = (size_t)M * N2;
     float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (m < M && k0 < F) {
+        // the gate|up operand carried x*w: rmsnorm's row factor goes on below
+        // (its loads issued here, beside the planes')
+        const float f = row_scale(rs, m);
         float g[8], u[8];
         const float* row = part + (size_t)m * N2 + k0;
         if (k0 + 8 <= F && (F & 3) == 0) {
@@ -582,8 +592,6 @@ __global__ __launch_bounds__(256) void k_fin_swiglu(const float* __restrict__ pa
                 }
             }
         }
-        // the gate|up operand carried x*w: rmsnorm's row factor goes on here
-        const float f = row_scale(rs, m);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             g[j] = g[j] * f;
