@@ -766,7 +766,7 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
         Layer& L = ctx->layers[b - ctx->L0];
         if (b == b0) launch_resid_w(st, ctx->x, nullptr, 0, T, Mpad, H, 0, L.ln1, L.qkv.KU, ctx->xp_h, ctx->ssp);
         const int sq = L.qkv.P;
-        launch_gemm(st, L.qkv, ctx->xp_h, ctx->part, T, ctx->ncu);
+        launch_gemm(st, L.qkv, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
         launch_fin_qkv(st, ctx->part, sq, T, drow_job, djobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
                        L.kpool, L.vpool, ctx->page_table, ctx->qp, rs, 1, 1);
         launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
@@ -774,13 +774,13 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
         launch_attn_combine(st, djobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU,
                              ctx->xp_o, nullptr, dcwg, p.ncwg);
         const int so = L.o.P;
-        launch_gemm(st, L.o, ctx->xp_o, ctx->part, T, ctx->ncu);
+        launch_gemm(st, L.o, ctx->xp_o, ctx->mt_alloc, ctx->part, T, ctx->ncu);
         launch_resid_w(st, ctx->x, ctx->part, so, T, Mpad, H, 0, L.ln2, L.gu.KU, ctx->xp_h, ctx->ssp);
         const int sg = L.gu.P;
-        launch_gemm(st, L.gu, ctx->xp_h, ctx->part, T, ctx->ncu);
+        launch_gemm(st, L.gu, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
         launch_fin_swiglu(st, ctx->part, sg, T, Mpad, d.ffn, L.down.KU, ctx->xp_f, rs);
         const int sd = L.down.P;
-        launch_gemm(st, L.down, ctx->xp_f, ctx->part, T, ctx->ncu);
+        launch_gemm(st, L.down, ctx->xp_f, ctx->mt_alloc, ctx->part, T, ctx->ncu);
         const bool next = b + 1 < b1;
         launch_resid_w(st, ctx->x, ctx->part, sd, T, Mpad, H, 1, next ? ctx->layers[b + 1 - ctx->L0].ln1 : nullptr,
                        next ? ctx->layers[b + 1 - ctx->L0].qkv.KU : 0, next ? ctx->xp_h : nullptr, ctx->ssp);
@@ -806,7 +806,7 @@ static void prof_replay(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, in
         double bytes = 0;
         for (int b = b0; b < b1; b++) bytes += qbytes(ctx->layers[b - ctx->L0].*w);
         prof_mark(ctx, kind, b1 - b0, bytes, [&] {
-            for (int b = b0; b < b1; b++) launch_gemm(st, ctx->layers[b - ctx->L0].*w, xp, ctx->part, T, ctx->ncu);
+            for (int b = b0; b < b1; b++) launch_gemm(st, ctx->layers[b - ctx->L0].*w, xp, ctx->mt_alloc, ctx->part, T, ctx->ncu);
         });
     };
     if (b1 > b0) {
@@ -825,7 +825,7 @@ static void prof_replay(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, in
     }
     if (head) {
         const QTensor& hw = d.tied ? ctx->wte : ctx->lm_head;
-        prof_mark(ctx, CC_K_HEAD, 1, qbytes(hw), [&] { launch_gemm(st, hw, ctx->xp_h, ctx->logits, p.S, ctx->ncu); });
+        prof_mark(ctx, CC_K_HEAD, 1, qbytes(hw), [&] { launch_gemm(st, hw, ctx->xp_h, ctx->mt_alloc, ctx->logits, p.S, ctx->ncu); });
     }
 }
 
@@ -949,7 +949,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         const int Mpad = 32 * ceil_div(S, 32);
         launch_resid_norm(st, ctx->x, (const int32_t*)(ctx->d_meta + ml.head_rows), nullptr, 0, S, Mpad, d.hidden, 0,
                           ctx->norm, d.rms_eps, hw.KU, ctx->xp_h, nullptr);
-        launch_gemm(st, hw, ctx->xp_h, ctx->logits, S, ctx->ncu);
+        launch_gemm(st, hw, ctx->xp_h, ctx->mt_alloc, ctx->logits, S, ctx->ncu);
         ctx->head_rows = S;
         launch_topk(st, ctx->logits, hw.P, S, d.vocab, topk, ctx->tk_a, ctx->tk_b, ctx->d_vals, ctx->d_ids);
         HIPCHK(hipMemcpyAsync(hout, ctx->d_vals, (size_t)S * topk * 4, hipMemcpyDeviceToHost, st));
@@ -1007,7 +1007,7 @@ cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K, con
     hipStream_t st = ctx->stream;
     launch_tile_q8(st, dW, dS, N, K, 32, q, 0);
     launch_prep_rows(st, dX, K, M, Mt * 16, K, q.KU, dXp);
-    launch_gemm(st, q, dXp, dP, M, ctx->ncu);
+    launch_gemm(st, q, dXp, Mt, dP, M, ctx->ncu);
     launch_sum_splits(st, dP, sp, M, N, dY);
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(take_launch_error());

@@ -62,7 +62,9 @@ struct RowScale {
 };
 
 // Y planes: out[(r*M + m)*N + n], r < w.P.
-void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, int ncu);
+// Xp holds xp_mtiles m-tiles (16 rows each) of the operand; M > 32 reads
+// those past M only as zeros.
+void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtiles, float* out, int M, int ncu);
 int lx_groups(const QTensor& w, int ncu);
 void launch_prep_rows(hipStream_t st, const float* x, int ldx, int M, int Mpad, int K, int KU,
                       uint4* Xp);

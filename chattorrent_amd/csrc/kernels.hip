@@ -271,9 +271,217 @@ static void launch_lx(hipStream_t st, const QTensor& w, const uint4* Xp, float* 
                  w.Nt, w.P, Gm);
 }
 
-void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, int ncu) {
+// ------------------------------------------------- many rows (M > 32) ---
+// Above 32 rows k_gemm_lx would stream every weight once per 32-row block.
+// k_gemm_tm reuses each weight record across 64 rows instead: a workgroup
+// serves plane r (the same planes as k_gemm_lx), TM_PAIRS tile pairs and 64
+// rows (4 m-tiles); wave (h, i) computes rows 32h .. 32h+31 of pair i, so
+// each record feeds two waves. The activations of one unit of K for the 64
+// rows (16 KiB) are staged through registers into a double-buffered LDS
+// block, one barrier a unit, while each wave streams its pair's records
+// TM_R-1 units ahead. Small enough for four waves a SIMD.
+//
+// Bits: a row's result is bit-identical to k_gemm_lx's at any M. Within a
+// plane k_gemm_lx sums a pair's units in order but in segments, cut where
+// its workgroup's steps are split between waves, and adds the segments in
+// order; the cut points depend only on N, K and the CU count (lx_cuts), and
+// k_gemm_tm folds its running sum at the same units. Each MFMA pair, scale
+// FMA and addition is the same operation on the same operands.
+constexpr int TM_MT = 4, TM_WAVES = 8, TM_PAIRS = 8, TM_R = 4;
+
+// Unit offsets inside pair p (of a plane of `len` <= 32 units) where
+// k_gemm_lx starts a new partial sum, as a bit mask: the wave boundaries of
+// the lx workgroup holding p (workgroup j of Gm covers pairs
+// [j*npairs/Gm, (j+1)*npairs/Gm)) that fall strictly inside the pair.
+__device__ static inline uint32_t lx_cuts(int p, int npairs, int Gm, int len) {
+    int j = (int)(((long long)p * Gm) / npairs);
+    while (j > 0 && (int)(((long long)j * npairs) / Gm) > p) j--;
+    while (j + 1 < Gm && (int)(((long long)(j + 1) * npairs) / Gm) <= p) j++;
+    const int p0 = (int)(((long long)j * npairs) / Gm), p1 = (int)(((long long)(j + 1) * npairs) / Gm);
+    const int steps = (p1 - p0) * len, s0 = (p - p0) * len;
+    uint32_t m = 0;
+#pragma unroll
+    for (int w = 1; w < LX_WAVES; w++) {
+        const int b = (w * steps) / LX_WAVES - s0;
+        if (b > 0 && b < len) m |= 1u << b;
+    }
+    return m;
+}
+
+__global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm(const uint8_t* __restrict__ Wr,
+                                                              const uint4* __restrict__ Xp, int xp_mtiles,
+                                                              float* __restrict__ out, int KU, int M, int N, int Nt,
+                                                              int P, int Gm) {
+    constexpr int NT = 2, R = TM_R, PW = R - 1, MTL = TM_MT, MTW = MTL * TM_PAIRS / TM_WAVES;
+    static_assert(MTW * TM_WAVES == MTL * TM_PAIRS, "waves cover pairs x m-tiles");
+    __shared__ u32x4 xs[2][MTL * 4][64];   // two units: block (m-tile, q = 2h + hl) of 1 KiB
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = blockIdx.x % P, pb = blockIdx.x / P;
+    const int npairs = Nt / NT;
+    const int pair = pb * TM_PAIRS + wave % TM_PAIRS, mw = (wave / TM_PAIRS) * MTW;   // m-tiles mw .. mw+MTW-1
+    const bool has = pair < npairs;
+    const int ua = lx_plane_start(r, KU, P), len = lx_plane_start(r + 1, KU, P) - ua;
+    const int mt0 = blockIdx.y * MTL;
+    const int G2 = 2 * KU;
+    const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)Wr, 0, 0x7fffffff, 0x00020000);
+    // activation m-tiles past the operand's allocation read zero
+    const uint32_t xbytes = (uint32_t)min((unsigned long long)xp_mtiles * G2 * 2048ull, 0xffffffffull);
+    const auto rx = __builtin_amdgcn_make_buffer_rsrc((void*)Xp, 0, xbytes, 0x00020000);
+    const auto ro = __builtin_amdgcn_make_buffer_rsrc((void*)(out + (size_t)r * M * N), 0, M * N * 4, 0x00020000);
+    const int vw = lane * 16, vs = NT * 1024 + (lane & 15) * NT * 4;
+    const int vo = (4 * (lane >> 4) * N + (lane & 15)) * 4;
+    const int rec0 = (ua * npairs + (has ? pair : 0) * len) * LX_REC;
+    const uint32_t cuts = has ? lx_cuts(pair, npairs, Gm, len) : 0u;
+
+    // this wave's share of a unit's activations: blocks BPW*wave .. +BPW-1
+    constexpr int BPW = MTL * 4 / TM_WAVES;
+    static_assert(BPW * TM_WAVES == MTL * 4, "activation blocks split evenly over the waves");
+    u32x4 st[BPW];
+    auto load_x = [&](int u) {
+        const int Uk = ua + (u < len ? u : len - 1);
+#pragma unroll
+        for (int k = 0; k < BPW; k++) {
+            const int b = BPW * wave + k, mt = b >> 2, q = b & 3;
+            const int src = ((mt0 + mt) * G2 + 2 * Uk + (q >> 1)) * 2 + (q & 1);
+            st[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, vw, src * 1024, 0);
+        }
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < BPW; k++) xs[buf][BPW * wave + k][lane] = st[k];
+    };
+    u32x4 w[R][NT];
+    uint32_t sc[R][NT];
+    auto load_w = [&](int u, u32x4 (&wv)[NT], uint32_t (&sv)[NT]) {
+        const int off = rec0 + (u < len ? u : len - 1) * LX_REC;
+        wv[0] = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, off, 2);
+        wv[1] = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, off + 1024, 2);
+        const auto s2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vs, off, 0);
+        sv[0] = s2[0];
+        sv[1] = s2[1];
+    };
+    float4_t seg[MTW][NT], tot[MTW][NT];
+#pragma unroll
+    for (int mt = 0; mt < MTW; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) seg[mt][nt] = tot[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    bool started = false;   // tot holds the first segment(s)
+
+    load_x(0);
+#pragma unroll
+    for (int i = 0; i < PW; i++) load_w(i, w[i], sc[i]);
+    store_x(0);
+    load_x(1);
+    __syncthreads();
+
+    auto unit = [&](int u, const u32x4 (&wc)[NT], const uint32_t (&sv)[NT]) {
+        const int buf = u & 1;
+        // the unit k_gemm_lx begins a new partial sum at: fold the running one
+        if ((cuts >> u) & 1u) {
+#pragma unroll
+            for (int mt = 0; mt < MTW; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    if (started)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) tot[mt][nt][e] = tot[mt][nt][e] + seg[mt][nt][e];
+                    else
+                        tot[mt][nt] = seg[mt][nt];
+                    seg[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+                }
+            started = true;
+        }
+        half8_t b[2][NT];
+        float scale[2][NT];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                b[h][nt] = h ? dequant8_biased(wc[nt][2], wc[nt][3]) : dequant8_biased(wc[nt][0], wc[nt][1]);
+                const uint16_t s16 = h ? (uint16_t)(sv[nt] >> 16) : (uint16_t)(sv[nt] & 0xffffu);
+                scale[h][nt] = (float)__builtin_bit_cast(_Float16, s16);
+            }
+#pragma unroll
+        for (int mt = 0; mt < MTW; mt++) {
+            u32x4 xv[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) xv[q] = xs[buf][(mw + mt) * 4 + q][lane];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                float4_t pp[NT];
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h]), b[h][nt], float4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h + 1]), b[h][nt], pp[nt]);
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) seg[mt][nt][e] = __builtin_fmaf(scale[h][nt], pp[nt][e], seg[mt][nt][e]);
+            }
+        }
+    };
+    int u = 0;
+    for (; u + R <= len; u += R) {
+#pragma unroll
+        for (int I = 0; I < R; I++) {
+            load_w(u + I + PW, w[(I + PW) % R], sc[(I + PW) % R]);
+            unit(u + I, w[I], sc[I]);
+            // the next unit's activations go in the other buffer: every wave
+            // finished reading it (one unit ago) before the last barrier
+            store_x((I + 1) & 1);
+            load_x(u + I + 2);
+            __syncthreads();
+        }
+    }
+    // at most PW units remain, their records in ring slots 0 .. PW-1
+#pragma unroll
+    for (int I = 0; I < PW; I++) {
+        if (u + I < len) {
+            unit(u + I, w[I], sc[I]);
+            store_x((I + 1) & 1);
+            load_x(u + I + 2);
+            __syncthreads();
+        }
+    }
+    if (!has) return;
+#pragma unroll
+    for (int mt = 0; mt < MTW; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) {
+            if (started)
+#pragma unroll
+                for (int e = 0; e < 4; e++) tot[mt][nt][e] = tot[mt][nt][e] + seg[mt][nt][e];
+            else
+                tot[mt][nt] = seg[mt][nt];
+        }
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int tile = pair * NT + nt;
+        if (tile * 16 >= N) continue;
+        if (tile * 16 + 16 > N && tile * 16 + (lane & 15) >= N) continue;
+#pragma unroll
+        for (int mt = 0; mt < MTW; mt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(tot[mt][nt][e]), ro,
+                                                      vo + (((mt0 + mw + mt) * 16 + e) * N + tile * 16) * 4, 0, 0);
+    }
+}
+
+void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtiles, float* out, int M, int ncu) {
     if (M <= 16) launch_lx<1>(st, w, Xp, out, M, ncu);
-    else launch_lx<2>(st, w, Xp, out, M, ncu);
+    else if (M <= 32) launch_lx<2>(st, w, Xp, out, M, ncu);
+    else {
+        // the same planes and cut points as k_gemm_lx (lx_groups)
+        const int Gm = lx_groups(w, ncu) / w.P;
+        const int npairs = w.Nt / 2;
+        dim3 grid(w.P * ((npairs + TM_PAIRS - 1) / TM_PAIRS), (M + 16 * TM_MT - 1) / (16 * TM_MT));
+        hipLaunchKernelGGL(k_gemm_tm, grid, dim3(64 * TM_WAVES), 0, st, (const uint8_t*)w.codes, Xp, xp_mtiles, out,
+                           w.KU, M, w.N, w.Nt, w.P, Gm);
+    }
     CHECK_LAUNCH();
 }
 

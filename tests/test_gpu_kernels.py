@@ -43,7 +43,8 @@ def test_round_f16_bit_exact(ctx):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 576, 70), (5, 1000, 77), (12, 5120, 256), (17, 576, 1024),
-                                   (32, 1536, 96), (33, 576, 64), (64, 320, 48)])
+                                   (32, 1536, 96), (33, 576, 64), (64, 320, 48), (100, 5120, 512),
+                                   (130, 1536, 2048)])
 def test_matmul_q8_vs_oracle(ctx, M, K, N):
     """matmul_gemv_q8 family (web/model/kernels.js:449-751): within a bound of
     2^-20 of the sum of |terms| (the MFMA path sums in a different order; the
@@ -77,6 +78,26 @@ def test_matmul_rows_match_one_row_bitwise(ctx):
         for i in range(M):
             one = ctx.op_matmul_q8(X[i:i + 1], W, S16)
             assert np.array_equal(one.view(np.uint32), rows[i:i + 1].view(np.uint32)), (M, i)
+
+
+def test_matmul_many_rows_bitwise(ctx):
+    """Above 32 rows the weights are reused across 64-row blocks (a different
+    kernel), and every row still has the bits of the one-row call: the same
+    K planes and the same partial-sum segments (at K 5120 a pair's 20 units
+    are cut at varying points between the 32-row kernel's waves)."""
+    from oracle import lib as L
+    rng = np.random.default_rng(37)
+    K, N = 5120, 3072
+    W = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    S16 = L.to_f16((rng.random((N, K // 32)) * 2 - 1).astype(np.float32))
+    for M in [33, 70, 129]:
+        X = (rng.random((M, K), np.float32) * 2 - 1).astype(np.float32)
+        rows = ctx.op_matmul_q8(X, W, S16)
+        for i in sorted({0, 1, M // 2, M - 2, M - 1}):
+            one = ctx.op_matmul_q8(X[i:i + 1], W, S16)
+            assert np.array_equal(one.view(np.uint32), rows[i:i + 1].view(np.uint32)), (M, i)
+        few = ctx.op_matmul_q8(X[:32], W, S16)
+        assert np.array_equal(few.view(np.uint32), rows[:32].view(np.uint32)), M
 
 
 @pytest.mark.parametrize("V,M", [(1000, 1), (1000, 5), (49152, 40), (151936, 1), (151936, 256)])
