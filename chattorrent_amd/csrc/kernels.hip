@@ -1192,11 +1192,14 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
     }
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
-    // partial row: max, sum, two pad floats, then O (16-byte aligned)
-    float* dst = part + it.part + (size_t)l16 * (D + 4);
+    // partial row: max, sum, two pad floats, then O (16-byte aligned); rows
+    // past the job's R query rows are neither written nor read
+    if (rho < R) {
+        float* dst = part + it.part + (size_t)l16 * (D + 4);
 #pragma unroll
-    for (int dt = 0; dt < DT; dt++) *(float4_t*)(dst + 4 + dt * 16 + 4 * j4) = o[dt];
-    if (j4 == 0) *(float2*)dst = make_float2(mrow, lsum);
+        for (int dt = 0; dt < DT; dt++) *(float4_t*)(dst + 4 + dt * 16 + 4 * j4) = o[dt];
+        if (j4 == 0) *(float2*)dst = make_float2(mrow, lsum);
+    }
 }
 
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
@@ -1239,7 +1242,8 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
     const size_t pstride = (size_t)16 * W;
     const float* base = part + (size_t)(jb.item0 + (kvh * jb.mtq + mt) * nc) * pstride;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    {
+    // only the m-tile's query rows rho < R were written (k_attn skips the rest)
+    if (mt * 16 + wave < R) {
         const int rl = wave;   // 16 waves, one row each
         float mloc = -INFINITY;
         for (int c = lane; c < nc; c += 64) mloc = fmaxf(mloc, base[c * pstride + rl * W]);
@@ -1257,7 +1261,7 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
     __syncthreads();
     const int sub = threadIdx.x >> 8, t = threadIdx.x & 255;
     const int rl = t / (D / 8), d0 = (t % (D / 8)) * 8;
-    const bool live = rl < 16;
+    const bool live = rl < 16 && mt * 16 + rl < R;
     float O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     if (live) {
         const float* src = base + (size_t)rl * W + 4 + d0;
@@ -1285,7 +1289,7 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
     }
     __syncthreads();
     const int rho = mt * 16 + rl;
-    if (sub > 0 || !live || rho >= R) return;   // no barrier below
+    if (sub > 0 || !live) return;   // no barrier below
 #pragma unroll
     for (int q = 0; q < COMBINE_SPLIT - 1; q++) {
         const float4 a = red[q][t][0], b = red[q][t][1];
