@@ -159,11 +159,16 @@ class Context:
     def fill_random(self, seed):
         self._chk(self.lib.cc_fill_random(self.h, seed))
 
-    def upload_q8(self, layer, tensor, codes, scales_f16):
+    def upload_q8(self, layer, tensor, codes, scales, group=32):
+        """int8 codes [N, K] and scales [N, ceil(K/group)]: uint16 arrays are
+        f16 bits, float32 arrays are f32 (rounded to f16 on the device side)."""
         codes = np.ascontiguousarray(codes, np.int8)
-        scales_f16 = np.ascontiguousarray(scales_f16, np.uint16)
-        self._chk(self.lib.cc_upload(self.h, layer, tensor, _p(codes), codes.size, _p(scales_f16),
-                                     scales_f16.size, 0, 32))
+        if np.asarray(scales).dtype == np.float32:
+            sc, kind = np.ascontiguousarray(scales, np.float32), 1
+        else:
+            sc, kind = np.ascontiguousarray(scales, np.uint16), 0
+        self._chk(self.lib.cc_upload(self.h, layer, tensor, _p(codes), codes.size, _p(sc), sc.size, kind,
+                                     int(group)))
 
     def upload_norm(self, layer, tensor, w):
         w = np.ascontiguousarray(w, np.float32)

@@ -474,13 +474,18 @@ cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data
     int row_tile0 = 0, N = 0, K = 0;
     QTensor* q = tensor_of(ctx, layer, tensor, &row_tile0, &N, &K);
     if (!q) return fail(ctx, CC_EARG, "tensor not held here");
-    if (group != 32) return fail(ctx, CC_EARG, "q8 group must be 32");
-    const int ng = ceil_div(K, 32);
-    if (n != (size_t)N * K || ns != (size_t)N * ng || !scales)
-        return fail(ctx, CC_EARG, "q8 tensor needs N*K codes and N*ceil(K/32) scales");
+    if (group < 32 || group % 32) return fail(ctx, CC_EARG, "q8 group must be a multiple of 32");
+    const int ng = ceil_div(K, 32), ngi = ceil_div(K, group), rep = group / 32;
+    if (n != (size_t)N * K || ns != (size_t)N * ngi || !scales)
+        return fail(ctx, CC_EARG, "q8 tensor needs N*K codes and N*ceil(K/group) scales");
+    // one scale per 32 values along K: a wider group's scale repeats, exactly
     std::vector<uint16_t> s16((size_t)N * ng);
-    if (scale_dtype == CC_SCALES_F16) std::memcpy(s16.data(), scales, s16.size() * 2);
-    else for (size_t i = 0; i < s16.size(); i++) s16[i] = half_bits(((const float*)scales)[i]);
+    for (size_t row = 0; row < (size_t)N; row++)
+        for (int g = 0; g < ng; g++) {
+            const size_t i = row * ngi + g / rep;
+            s16[row * ng + g] = scale_dtype == CC_SCALES_F16 ? ((const uint16_t*)scales)[i]
+                                                             : half_bits(((const float*)scales)[i]);
+        }
     int8_t* dc = nullptr;
     uint16_t* ds = nullptr;
     HIPCHK(hipMalloc(&dc, n));

@@ -214,11 +214,12 @@ napi_value FillRandomKV(napi_env env, napi_callback_info info) {
     return status_result(env, c, cc_fill_random_kv(c->ctx, slot, tokens, u64(env, argv[3]), u64(env, argv[4])));
 }
 
-// upload(ctx, layer, tensor, data, scales|null): data Int8Array [N*K] (or a
-// Float32Array norm), scales Uint16Array (f16 bits) or Float32Array.
+// upload(ctx, layer, tensor, data, scales|null, group = 32): data Int8Array
+// [N*K] (or a Float32Array norm), scales Uint16Array (f16 bits) or
+// Float32Array [N*ceil(K/group)], group a multiple of 32.
 napi_value Upload(napi_env env, napi_callback_info info) {
-    size_t argc = 5;
-    napi_value argv[5];
+    size_t argc = 6;
+    napi_value argv[6];
     NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
     Ctx* c = unwrap(env, argv[0]);
     if (!c) return nullptr;
@@ -236,8 +237,14 @@ napi_value Upload(napi_env env, napi_callback_info info) {
     size_t ns = 0;
     napi_typedarray_type st = napi_uint16_array;
     if (argc > 4) typed(env, argv[4], &sc, &ns, &st);
+    int32_t group = 32;
+    if (argc > 5) {
+        napi_valuetype vt;
+        napi_typeof(env, argv[5], &vt);
+        if (vt == napi_number) napi_get_value_int32(env, argv[5], &group);
+    }
     return status_result(env, c, cc_upload(c->ctx, layer, tensor, data, n, sc, ns,
-                                           st == napi_float32_array ? CC_SCALES_F32 : CC_SCALES_F16, 32));
+                                           st == napi_float32_array ? CC_SCALES_F32 : CC_SCALES_F16, group));
 }
 
 // ---- step (async) ----

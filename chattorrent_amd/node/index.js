@@ -19,4 +19,7 @@ function createRunner(d, opts) {
     return new Runner(backend, d, o);
 }
 
-module.exports = { createRunner, Runner, NativeBackend };
+// loader: the reference's on-disk checkpoint, for Runner.append (node/loader.js)
+const loader = require('./loader');
+
+module.exports = { createRunner, Runner, NativeBackend, loader };

@@ -39,7 +39,9 @@ class NativeBackend {
     readLogits(rows) { return load().readLogits(this.ctx, rows); }
     fillRandom(seed) { load().fillRandom(this.ctx, seed); }
     fillRandomKV(slot, tokens, seed, key) { load().fillRandomKV(this.ctx, slot, tokens, seed, key); }
-    upload(layer, tensor, data, scales) { load().upload(this.ctx, layer, tensor, data, scales || null); }
+    upload(layer, tensor, data, scales, group) {
+        load().upload(this.ctx, layer, tensor, data, scales || null, group || 32);
+    }
     stats() { return load().stats(this.ctx); }
     destroy() {
         if (this.ctx) load().destroy(this.ctx);

@@ -107,14 +107,17 @@ class Runner {
 
     // append(weights) — stage.js:446-468: load position `have`. `weights`
     // holds host tensors by their HF names: q8 ones as {codes: Int8Array
-    // [N*K], scales: Uint16Array (f16 bits) or Float32Array [N*ceil(K/32)]},
-    // norms as Float32Array. Position 0 needs wte; the last, norm (and
-    // lm_head when untied); a block, its seven projections and two norms.
+    // [N*K], scales: Uint16Array (f16 bits) or Float32Array
+    // [N*ceil(K/group)], group (default 32)}, norms as Float32Array (what
+    // node/loader.js's loadBlock / loadClient return). Position 0 needs wte;
+    // the last, norm (and lm_head when untied); a block, its seven
+    // projections and two norms.
     append(weights) {
         const p = this.have;
         const w = weights || {};
         if (p >= this.hi) throw new Error(`nothing left to append: ${this.lo}–${this.hi - 1} is full`);
-        const up = (layer, id, t) => this.backend.upload(layer, id, t.codes || t, t.codes ? t.scales : null);
+        const up = (layer, id, t) => this.backend.upload(layer, id, t.codes || t, t.codes ? t.scales : null,
+                                                         t.codes ? t.group : undefined);
         if (p === 0) {
             if (!w.wte) throw new Error('position 0 is the embedding and needs wte');
             up(-1, TENSOR.wte, w.wte);

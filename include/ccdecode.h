@@ -89,7 +89,10 @@ const char* cc_last_error(const cc_ctx* ctx);
 /* uploadQ8(device, int8Bytes, scales, group) — web/model/kernels.js:122-126;
  * norms (tensor LN1/LN2/NORM) are f32 `data` with n = hidden and no scales.
  * q8 tensors: `data` int8 [N, K] row-major, `scales` [N, ceil(K/group)] as
- * f16 bits or f32 (rounded to the device's f16 scale). */
+ * f16 bits or f32 (rounded to the device's f16 scale). `group` is any
+ * multiple of 32 (the reference's converter writes 64,
+ * tools/convert_hf.py:493): a scale covering group/32 of the device's
+ * 32-wide groups is given to each of them, which is exact. */
 cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data, size_t n,
                     const void* scales, size_t ns, int32_t scale_dtype, int32_t group);
 

@@ -1,0 +1,84 @@
+"""Writes a synthetic checkpoint in the reference's on-disk layout (test
+infrastructure): tools/convert_hf.py:594-649 pack_file puts a q8 tensor's
+int8 block [N, K] and then its f32 scales [N, ceil(K/group)], and a norm
+weight as f32, one after another in a .bin; :768-800 writes the manifest.
+The codes and scales here are drawn directly (no f32 weights quantised)."""
+import json
+import os
+
+import numpy as np
+
+BLOCK_NAMES = ["input_layernorm", "q_proj", "k_proj", "v_proj", "o_proj", "post_attention_layernorm",
+               "gate_proj", "up_proj", "down_proj"]
+
+
+def f16_exact(x):
+    """Values representable in f16 (so the device's f16 scales are exact)."""
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def pack_file(path, filename, tensors):
+    entries, offset = [], 0
+    with open(os.path.join(path, filename), "wb") as f:
+        for name, t in tensors:
+            if isinstance(t, tuple):
+                codes, scales, group = t
+                codes = np.ascontiguousarray(codes, np.int8)
+                scales = np.ascontiguousarray(scales, np.float32)
+                f.write(codes.tobytes())
+                f.write(scales.tobytes())
+                entries.append({"name": name, "shape": list(codes.shape), "offset": offset, "size": codes.nbytes,
+                                "dtype": "q8", "group": group, "scales_offset": offset + codes.nbytes,
+                                "scales_size": scales.nbytes})
+                offset += codes.nbytes + scales.nbytes
+            else:
+                a = np.ascontiguousarray(t, np.float32)
+                f.write(a.tobytes())
+                entries.append({"name": name, "shape": list(a.shape), "offset": offset, "size": a.nbytes,
+                                "dtype": "f32"})
+                offset += a.nbytes
+    return entries
+
+
+def q8(rng, N, K, group):
+    codes = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    scales = f16_exact(rng.uniform(1e-4, 4e-4, (N, -(-K // group))))
+    return codes, scales, group
+
+
+def make(path, d, seed=11, group=64):
+    """A q8 checkpoint of dims `d` (this build's key names) at `path`.
+    Returns {filename: {name: tensor}} with what was written."""
+    os.makedirs(path, exist_ok=True)
+    rng = np.random.default_rng(seed)
+    H, D, F, V = d["hidden"], d["head_dim"], d["ffn"], d["vocab"]
+    q, kv = d["n_heads"] * D, d["n_kv_heads"] * D
+    shapes = {"q_proj": (q, H), "k_proj": (kv, H), "v_proj": (kv, H), "o_proj": (H, q),
+              "gate_proj": (F, H), "up_proj": (F, H), "down_proj": (H, F)}
+    manifest = {"model": "synthetic", "arch": "llama", "hidden": H, "n_layer": d["n_layer"],
+                "n_head": d["n_heads"], "n_kv_head": d["n_kv_heads"], "head_dim": D,
+                "group": d["n_heads"] // d["n_kv_heads"], "ffn": F, "vocab": V, "n_pos": 2048,
+                "rms_eps": d["rms_eps"], "rope_theta": d["rope_theta"], "rope_scaling": d.get("rope_scaling"),
+                "norm": "rmsnorm", "act": "silu", "dtype": "q8", "layout": "row_major",
+                "weight_layout": "out_in", "tied_lm_head": d.get("tied", True), "files": {}}
+    written = {}
+    for i in range(d["n_layer"]):
+        ts = []
+        for name in BLOCK_NAMES:
+            if name.endswith("layernorm"):
+                ts.append((name, f16_exact(rng.uniform(0.5, 1.5, H))))
+            else:
+                ts.append((name, q8(rng, *shapes[name], group)))
+        fn = f"block_{i:02d}.bin"
+        manifest["files"][fn] = pack_file(path, fn, ts)
+        written[fn] = dict(ts)
+    client = [("wte", q8(rng, V, H, group)), ("norm", f16_exact(rng.uniform(0.5, 1.5, H)))]
+    manifest["files"]["client.bin"] = pack_file(path, "client.bin", client)
+    written["client.bin"] = dict(client)
+    if not d.get("tied", True):
+        head = [("lm_head", q8(rng, V, H, group))]
+        manifest["files"]["lm_head.bin"] = pack_file(path, "lm_head.bin", head)
+        written["lm_head.bin"] = dict(head)
+    with open(os.path.join(path, "manifest.json"), "w") as f:
+        json.dump(manifest, f, indent=2)
+    return written

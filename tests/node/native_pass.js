@@ -5,7 +5,7 @@
 // do (web/model/stage.js, docs/architecture.md). Prints the tokens as JSON.
 // Usage: node tests/node/native_pass.js '<json config>'
 
-const { createRunner } = require('../../chattorrent_amd/node');
+const { createRunner, loader } = require('../../chattorrent_amd/node');
 
 async function decode(runners, cfg) {
     const d = cfg.dims;
@@ -38,10 +38,23 @@ async function decode(runners, cfg) {
     const cfg = JSON.parse(process.argv[2]);
     const d = cfg.dims;
     const end = d.n_layer + 2;
+    // weights: the shared generator (cfg.seed), or a checkpoint directory
+    // (cfg.checkpoint) appended position by position as a peer loads them
+    const m = cfg.checkpoint ? loader.loadManifest(cfg.checkpoint) : null;
+    const md = m ? loader.dimsFromManifest(m) : null;
+    if (m) {
+        const problems = loader.checkManifest(m, md);
+        if (problems.length) throw new Error(problems.join('; '));
+    }
+    const client = m ? loader.loadClient(cfg.checkpoint, m, md) : null;
     const mk = (lo, hi) => {
-        const r = createRunner(d, { lo, hi, nMax: cfg.nMax, tMax: cfg.tMax, slots: cfg.chats.length,
-                                    sessions: cfg.chats.length, batchRows: cfg.tMax });
-        r.backend.fillRandom(cfg.seed);
+        const r = createRunner(d, { lo, hi, have: m ? lo : hi, nMax: cfg.nMax, tMax: cfg.tMax,
+                                    slots: cfg.chats.length, sessions: cfg.chats.length, batchRows: cfg.tMax });
+        if (m) {
+            for (let p = lo; p < hi; p++) r.append(loader.weightsFor(cfg.checkpoint, m, md, p, client));
+        } else {
+            r.backend.fillRandom(cfg.seed);
+        }
         return r;
     };
     const whole = mk(0, end);

@@ -1,0 +1,106 @@
+"""A checkpoint in the reference's on-disk layout (q8 at the converter's group
+64 with f32 scales, tools/convert_hf.py:493, :594-649) read into a cc_ctx by
+chattorrent_amd/checkpoint.py, then a decode pass against the oracle holding
+the same weights. The same codes written at group 32 (each scale repeated)
+give bit-identical logits: repeating a scale over 32-wide groups is exact."""
+import numpy as np
+import pytest
+
+import ckpt_writer as W
+from chattorrent_amd import checkpoint as C
+from chattorrent_amd import configs
+from test_gpu_pass import SEED, _check_head, _ids
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_weights(om, written, d):
+    from oracle import model as Mo
+    names = {"q_proj": "q", "k_proj": "k", "v_proj": "v", "o_proj": "o", "gate_proj": "gate", "up_proj": "up",
+             "down_proj": "down"}
+
+    def g32(t):
+        codes, scales, group = t
+        K = codes.shape[1]
+        return codes, np.repeat(scales, group // 32, axis=1)[:, :-(-K // 32)].astype(np.float32)
+
+    om.w = {"layers": []}
+    for i in range(d["n_layer"]):
+        blk = written[C.block_file(i)]
+        lw = {names[n]: g32(t) for n, t in blk.items() if n in names}
+        lw["ln1"] = blk["input_layernorm"]
+        lw["ln2"] = blk["post_attention_layernorm"]
+        om.w["layers"].append(lw)
+    om.w["wte"] = g32(written["client.bin"]["wte"])
+    om.w["norm"] = written["client.bin"]["norm"]
+    if "lm_head.bin" in written:
+        om.w["lm_head"] = g32(written["lm_head.bin"]["lm_head"])
+    assert set(om.w["layers"][0]) == set(Mo.TENSORS) | {"ln1", "ln2"}
+
+
+@pytest.mark.parametrize("tied", [True, False])
+def test_checkpoint_pass_matches_oracle(gpu, tmp_path, tied):
+    from chattorrent_amd.ccdecode import Context
+    from oracle import model as Mo
+    d = dict(configs.with_layers(configs.SMOLLM2, 2), tied=tied)
+    written = W.make(str(tmp_path / "g64"), d, group=64)
+    ctxs = [17, 130, 300]
+    c = Context(d, n_max=512, t_max=16, slots=4)
+    om = Mo.Model(d, n_slots=4, max_pages=8)
+    try:
+        C.upload(c, str(tmp_path / "g64"))
+        _oracle_weights(om, written, d)
+        for s, T in enumerate(ctxs):
+            c.fill_random_kv(s, T, SEED, s + 1)
+            om.fill_random_kv(s, T, SEED, s + 1)
+        jobs = [dict(slot=s, past=T, n=1, ids=_ids(1, d["vocab"], 700 + s), sampled=1, topk=4)
+                for s, T in enumerate(ctxs)]
+        vals, ids = c.step(jobs, topk=4)
+        _check_head(d, vals, ids, om.pass_(jobs), ctx=c)
+        logits64 = c.read_logits(len(jobs))
+    finally:
+        c.close()
+    # the same codes at group 32: each group-64 scale written twice
+    w32 = {fn: {n: ((t[0], np.repeat(t[1], 2, axis=1)[:, :-(-t[0].shape[1] // 32)], 32) if isinstance(t, tuple) else t)
+                for n, t in ts.items()} for fn, ts in written.items()}
+    p32 = tmp_path / "g32"
+    p32.mkdir()
+    m = C.load_manifest(str(tmp_path / "g64"))
+    for fn, ts in w32.items():
+        order = [e["name"] for e in m["files"][fn]]
+        m["files"][fn] = W.pack_file(str(p32), fn, [(n, ts[n]) for n in order])
+    import json
+    with open(p32 / "manifest.json", "w") as f:
+        json.dump(m, f)
+    c = Context(d, n_max=512, t_max=16, slots=4)
+    try:
+        C.upload(c, str(p32))
+        for s, T in enumerate(ctxs):
+            c.fill_random_kv(s, T, SEED, s + 1)
+        c.step(jobs, topk=4)
+        assert np.array_equal(c.read_logits(len(jobs)).view(np.uint32), logits64.view(np.uint32))
+    finally:
+        c.close()
+
+
+def test_checkpoint_split_over_two_contexts(gpu, tmp_path):
+    """Two peers over one checkpoint (positions [0, 2) and [2, 4) of a
+    2-block model): each uploads only its own files' tensors, and the f16
+    hand-off between them gives the single context's tokens."""
+    from chattorrent_amd.ccdecode import Context
+    d = configs.with_layers(configs.SMOLLM2, 2)
+    W.make(str(tmp_path), d, group=64)
+    jobs = [dict(slot=0, past=0, n=5, ids=_ids(5, d["vocab"], 710), sampled=1, topk=2)]
+    whole = Context(d, n_max=256, t_max=8, slots=1)
+    a = Context(d, n_max=256, t_max=8, slots=1, lo=0, hi=2)
+    b = Context(d, n_max=256, t_max=8, slots=1, lo=2, hi=4)
+    try:
+        for c in (whole, a, b):
+            C.upload(c, str(tmp_path))
+        v1, i1 = whole.step(jobs, topk=2)
+        rows = a.step([dict(jobs[0], sampled=0)], at=0, to=2)
+        v2, i2 = b.step([dict(jobs[0], ids=None, hidden=rows)], at=2, to=4, topk=2)
+        assert np.array_equal(i1, i2) and np.array_equal(v1.view(np.uint32), v2.view(np.uint32))
+    finally:
+        for c in (whole, a, b):
+            c.close()

@@ -43,3 +43,42 @@ def test_node_runner_matches_c_abi(gpu):
     assert out["whole"] == hist
     assert out["split"] == hist
     assert out["batched"] >= 1
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(NODE is None, reason="node is not installed")
+def test_node_runner_loads_checkpoint(gpu, tmp_path):
+    """Runner.append over node/loader.js: a q8 checkpoint in the reference's
+    layout (group 64, f32 scales) loaded position by position, whole and split
+    at a block; the tokens equal the C ABI's with the same checkpoint loaded
+    by chattorrent_amd/checkpoint.py."""
+    import ckpt_writer as W
+    from chattorrent_amd import checkpoint as C
+    from chattorrent_amd.ccdecode import Context
+    d = configs.with_layers(configs.SMOLLM2, 3)
+    W.make(str(tmp_path), d, group=64)
+    rng = np.random.default_rng(8)
+    chats = [rng.integers(0, d["vocab"], n).tolist() for n in (4, 7)]
+    cfg = {"dims": d, "seed": 0, "nMax": 256, "tMax": 32, "chats": chats, "steps": 3, "cut": 2,
+           "checkpoint": str(tmp_path)}
+    print("[node] running tests/node/native_pass.js with a checkpoint", flush=True)
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "native_pass.js"), json.dumps(cfg)], cwd=ROOT,
+                       stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    c = Context(d, n_max=256, t_max=32, slots=2)
+    try:
+        C.upload(c, str(tmp_path))
+        _, ids = c.step([{"slot": i, "past": 0, "n": len(p), "ids": p, "sampled": 1} for i, p in enumerate(chats)])
+        hist = [[int(ids[i, 0])] for i in range(len(chats))]
+        past = [len(p) for p in chats]
+        for _ in range(cfg["steps"]):
+            _, ids = c.step([{"slot": i, "past": past[i], "n": 1, "ids": [hist[i][-1]], "sampled": 1}
+                             for i in range(len(chats))])
+            for i in range(len(chats)):
+                hist[i].append(int(ids[i, 0]))
+                past[i] += 1
+    finally:
+        c.close()
+    assert out["whole"] == hist
+    assert out["split"] == hist
