@@ -6,6 +6,17 @@
 // Usage: node tests/node/native_pass.js '<json config>'
 
 const { createRunner, loader } = require('../../chattorrent_amd/node');
+const wire = require('../../chattorrent_amd/node/wire');
+
+// The rows leaving one Runner as the link carries them to the next
+// (web/net.js framing, fragmented at a small limit so multi-fragment
+// messages are exercised).
+function overTheLink(h, rows) {
+    const st = {};
+    let msg = null;
+    for (const f of wire.fragment(wire.pack({ k: 'job', s: h.s, n: h.n }, rows), 4096, 1)) msg = wire.reassemble(st, f);
+    return wire.unpack(msg).payload;
+}
 
 async function decode(runners, cfg) {
     const d = cfg.dims;
@@ -15,7 +26,7 @@ async function decode(runners, cfg) {
         let hidden = null, at = 0, out = null;
         for (const r of runners) {
             out = await r.run(Object.assign({}, h, { pos: at, ids: at === 0 ? ids : undefined }), hidden, r.hi);
-            hidden = out.hidden;
+            hidden = out.hidden && cfg.wire ? overTheLink(h, out.hidden) : out.hidden;
             at = out.at;
         }
         if (at !== end) throw new Error(`stopped at ${at}`);

@@ -50,8 +50,9 @@ def test_node_runner_matches_c_abi(gpu):
 def test_node_runner_loads_checkpoint(gpu, tmp_path):
     """Runner.append over node/loader.js: a q8 checkpoint in the reference's
     layout (group 64, f32 scales) loaded position by position, whole and split
-    at a block; the tokens equal the C ABI's with the same checkpoint loaded
-    by chattorrent_amd/checkpoint.py."""
+    at a block with the rows crossing in the peers' message format
+    (node/wire.js); the tokens equal the C ABI's with the same checkpoint
+    loaded by chattorrent_amd/checkpoint.py."""
     import ckpt_writer as W
     from chattorrent_amd import checkpoint as C
     from chattorrent_amd.ccdecode import Context
@@ -60,7 +61,7 @@ def test_node_runner_loads_checkpoint(gpu, tmp_path):
     rng = np.random.default_rng(8)
     chats = [rng.integers(0, d["vocab"], n).tolist() for n in (4, 7)]
     cfg = {"dims": d, "seed": 0, "nMax": 256, "tMax": 32, "chats": chats, "steps": 3, "cut": 2,
-           "checkpoint": str(tmp_path)}
+           "checkpoint": str(tmp_path), "wire": True}
     print("[node] running tests/node/native_pass.js with a checkpoint", flush=True)
     r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "native_pass.js"), json.dumps(cfg)], cwd=ROOT,
                        stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=120)

@@ -60,3 +60,11 @@ def test_loader_reads_reference_checkpoint(tmp_path):
             else:
                 assert got["kind"] == "f32" and got["n"] == t.size
                 assert abs(got["sum"] - float(t.astype(np.float64).sum())) <= 1e-9 * t.size
+
+
+def test_wire_format():
+    """node/wire.js: the peers' message framing and fragmentation (web/net.js:73-207)."""
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "wire.test.js")], cwd=ROOT,
+                       stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=60)
+    assert r.returncode == 0, r.stdout
+    assert r.stdout.strip().endswith("passed")
