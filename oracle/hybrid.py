@@ -1,0 +1,193 @@
+"""Oracle restatement of the hybrid (Qwen3.5-architecture) blocks — test
+infrastructure only: the parity tests compare the HIP path with these
+functions; nothing in the product imports them.
+
+Follows:
+
+* ``web/model/kernels.js:1538-1580`` causal_conv1d (depthwise, SiLU fused,
+  the job's window reaching before row 0 reads the history ring);
+* ``web/model/kernels.js:1582-1620`` update_conv_history;
+* ``web/model/kernels.js:1622-1670`` l2norm_heads (sum of squares + 1e-6,
+  repeat_interleave by ``group``);
+* ``web/model/kernels.js:1672-1805`` gated_delta_net_step (gates from the raw
+  projections and the packed A_log / dt_bias, one pass over the old state per
+  token with the readout ``qScale·(Σ(g·S)q + delta·(k·q))``);
+* ``web/model/kernels.js:1822-1839`` sigmoid_mul;
+* ``web/model/model.js:418-444`` linearCore and ``:472-527`` linearBlockSegs
+  (the per-session recurrence, gated rmsnorm, out_proj);
+* ``web/model/model.js:368-410`` fullBlockSegs's hybrid extras: attn_gate,
+  q_norm / k_norm over head_dim, partial rotary, the output gate before
+  o_proj.
+
+All arithmetic is float32, in the reference's order where it fixes one.
+
+Parity pins (``tests/test_oracle_hybrid.py``): every function is checked
+against the reference's own dumps of a small Qwen3.5 model
+(``oracle/qwen3.8-27b-spike`` of the reference: f32 weights of one
+linear_attention and one full_attention layer with every intermediate), the
+recurrence also against the textbook delta rule in float64, and the conv
+history against a sliding window over the whole sequence.
+"""
+import numpy as np
+
+from . import lib as L
+
+F32 = np.float32
+
+
+def silu(x):
+    """x·sigmoid(x) as causal_conv1d and silu_mul write it: s = 1/(1+exp(-x)), x·s."""
+    x = np.asarray(x, F32)
+    s = (F32(1.0) / (F32(1.0) + np.exp(-x))).astype(F32)
+    return (x * s).astype(F32)
+
+
+def sigmoid_mul(gate, a):
+    """kernels.js:1822-1839: sigmoid(gate)·a."""
+    s = (F32(1.0) / (F32(1.0) + np.exp(-np.asarray(gate, F32)))).astype(F32)
+    return (s * np.asarray(a, F32)).astype(F32)
+
+
+def causal_conv1d(x, w, hist=None):
+    """kernels.js:1538-1580. x [T, C] (this job's rows), w [C, K]; hist
+    [K-1, C] holds the K-1 rows before x's row 0 (zeros for a new session).
+    out[t, c] = silu(Σ_k w[c, k]·x[t-(K-1)+k, c]), k in order."""
+    x = np.asarray(x, F32)
+    T, C = x.shape
+    K = w.shape[1]
+    if hist is None:
+        hist = np.zeros((K - 1, C), F32)
+    full = np.concatenate([hist.astype(F32), x], axis=0)   # row K-1 is x's row 0
+    acc = np.zeros((T, C), F32)
+    for k in range(K):
+        acc = (acc + w[:, k].astype(F32)[None, :] * full[k:k + T]).astype(F32)
+    return silu(acc)
+
+
+def update_conv_history(hist, new):
+    """kernels.js:1582-1620: the ring after a chunk of rows `new` [T, C]: the
+    last K-1 rows of old ++ new."""
+    Kh = hist.shape[0]
+    return np.ascontiguousarray(np.concatenate([hist, np.asarray(new, F32)], axis=0)[-Kh:]) if Kh else hist
+
+
+def l2norm_heads(x, src_heads, D, group=1):
+    """kernels.js:1622-1670: per (row, source head) x·(1/sqrt(Σx² + 1e-6)),
+    written to heads src*group + g for g < group. x [T, src_heads*D] ->
+    [T, src_heads*group, D]."""
+    x = np.asarray(x, F32).reshape(-1, src_heads, D)
+    ss = np.sum((x * x).astype(F32), axis=2, dtype=F32)
+    scale = (F32(1.0) / np.sqrt(ss + F32(1e-6))).astype(F32)
+    y = (x * scale[:, :, None]).astype(F32)
+    return np.repeat(y, group, axis=1)
+
+
+def gdn_gates(a_raw, b_raw, params, heads):
+    """kernels.js:1736-1741: a = a_raw + dt_bias; softplus (a > 20 form for
+    large a); g = exp(-exp(A_log)·sp); beta = sigmoid(b_raw)."""
+    a = (np.asarray(a_raw, F32) + params[heads:2 * heads].astype(F32)).astype(F32)
+    with np.errstate(over="ignore"):
+        sp_small = np.log(F32(1.0) + np.exp(a)).astype(F32)
+    sp_big = (a + np.log(F32(1.0) + np.exp(-a))).astype(F32)
+    sp = np.where(a > 20.0, sp_big, sp_small).astype(F32)
+    g = np.exp(-np.exp(params[:heads].astype(F32)) * sp).astype(F32)
+    beta = (F32(1.0) / (F32(1.0) + np.exp(-np.asarray(b_raw, F32)))).astype(F32)
+    return g, beta
+
+
+def gdn_step(q, k, v, a_raw, b_raw, params, S):
+    """kernels.js:1672-1805 over the rows of one session, in place on S
+    [heads, Dk, Dv]. q, k [T, heads, Dk] (l2-normed, repeated), v [T, heads,
+    Dv], a_raw / b_raw [T, heads]. Returns out [T, heads, Dv]."""
+    T, heads, Dk = q.shape
+    Dv = v.shape[2]
+    q_scale = F32(1.0) / np.sqrt(F32(Dk))
+    out = np.zeros((T, heads, Dv), F32)
+    g, beta = gdn_gates(a_raw, b_raw, params, heads)
+    for t in range(T):
+        for h in range(heads):
+            s = (S[h] * g[t, h]).astype(F32)                       # decay
+            kv = (s * k[t, h][:, None]).astype(F32).sum(axis=0, dtype=F32)
+            qo = (s * q[t, h][:, None]).astype(F32).sum(axis=0, dtype=F32)
+            kq = np.sum((k[t, h] * q[t, h]).astype(F32), dtype=F32)
+            delta = ((v[t, h] - kv) * beta[t, h]).astype(F32)
+            S[h] = (s + (k[t, h][:, None] * delta[None, :]).astype(F32)).astype(F32)
+            out[t, h] = ((qo + delta * kq) * q_scale).astype(F32)
+    return out
+
+
+def gated_rmsnorm(core, w, z, eps):
+    """model.js:523-524: rmsnorm over each head's Dv values with gated_norm,
+    then silu(z)·normed (RMSNormGated). core, z [T, nV*Dv]."""
+    T = core.shape[0]
+    Dv = w.shape[0]
+    rows = np.ascontiguousarray(core.reshape(-1, Dv), F32)
+    normed = L.rmsnorm(rows, np.asarray(w, F32), eps).reshape(T, -1)
+    return L.silu_mul(np.ascontiguousarray(z, F32), np.ascontiguousarray(normed, F32))
+
+
+class LinearState:
+    """One session's recurrent state for one linear_attention layer
+    (model.js:46-58 makeRecurrentState): S [nV, Dk, Dv] and the conv rings
+    of the q, k and v channels (kept here as one [K-1, convDim] ring; the
+    conv is depthwise, so the channel split changes nothing)."""
+
+    def __init__(self, lin):
+        self.S = np.zeros((lin["nV"], lin["Dk"], lin["Dv"]), F32)
+        self.hist = np.zeros((lin["K4"] - 1, 2 * lin["keyDim"] + lin["valueDim"]), F32)
+
+    def copy(self):
+        c = LinearState.__new__(LinearState)
+        c.S = self.S.copy()
+        c.hist = self.hist.copy()
+        return c
+
+
+def lin_dims(d):
+    nK, nV, Dk, Dv = d["lin_nk"], d["lin_nv"], d["lin_dk"], d["lin_dv"]
+    return {"nK": nK, "nV": nV, "Dk": Dk, "Dv": Dv, "K4": d["lin_conv"], "keyDim": nK * Dk,
+            "valueDim": nV * Dv, "group": nV // nK}
+
+
+def linear_core(lin, lw, state, q, k, v, a, b):
+    """model.js:418-444 linearCore for one session's rows: conv (with the
+    ring), l2norm with the value-head repeat, the recurrence, then the ring
+    advanced by the raw projections. Returns core [T, nV*Dv]."""
+    T = q.shape[0]
+    raw = np.concatenate([q, k, v], axis=1).astype(F32)
+    conv = causal_conv1d(raw, lw["conv"], state.hist)
+    kd = lin["keyDim"]
+    cq, ck, cv = conv[:, :kd], conv[:, kd:2 * kd], conv[:, 2 * kd:]
+    ql = l2norm_heads(cq, lin["nK"], lin["Dk"], lin["group"])
+    kl = l2norm_heads(ck, lin["nK"], lin["Dk"], lin["group"])
+    vv = cv.reshape(T, lin["nV"], lin["Dv"])
+    out = gdn_step(ql, kl, vv, a, b, lw["gate_params"], state.S)
+    state.hist = update_conv_history(state.hist, raw)
+    return out.reshape(T, lin["nV"] * lin["Dv"])
+
+
+def linear_block(d, lw, x, segs, states, matmul, rms_eps):
+    """model.js:472-527 linearBlockSegs (no speculation): x [T, H] updated in
+    place through attention and the SwiGLU MLP. `matmul(h, name)` gives the
+    projection of rows h by weight `name`; `states[s]` is segment s's
+    LinearState."""
+    lin = lin_dims(d)
+    h = L.rmsnorm(x, lw["ln1"], rms_eps)
+    q, k, v = matmul(h, "in_q"), matmul(h, "in_k"), matmul(h, "in_v")
+    z, bb, aa = matmul(h, "in_z"), matmul(h, "in_b"), matmul(h, "in_a")
+    core = np.zeros((x.shape[0], lin["valueDim"]), F32)
+    for s, st in zip(segs, states):
+        r0, r1 = s["row"], s["row"] + s["n"]
+        core[r0:r1] = linear_core(lin, lw, st, q[r0:r1], k[r0:r1], v[r0:r1], aa[r0:r1], bb[r0:r1])
+    gated = gated_rmsnorm(core, lw["gated_norm"], z, rms_eps)
+    L.add_inplace(x, matmul(gated, "out"))
+    return x
+
+
+def qk_norm_rope(q, k, qn, kn, nH, nKV, D, eps):
+    """fullBlockSegs's q_norm / k_norm (model.js:388-394): rmsnorm over each
+    head's D values. RoPE is applied afterwards by attend as for any model."""
+    T = q.shape[0]
+    qo = L.rmsnorm(np.ascontiguousarray(q.reshape(T * nH, D), F32), qn, eps).reshape(T, nH * D)
+    ko = L.rmsnorm(np.ascontiguousarray(k.reshape(T * nKV, D), F32), kn, eps).reshape(T, nKV * D)
+    return np.ascontiguousarray(qo), np.ascontiguousarray(ko)
