@@ -16,6 +16,10 @@ CC_OK, CC_BUSY, CC_COLD, CC_STALE, CC_NOSPEC, CC_EARG, CC_EPOOL, CC_EOOM, CC_EDE
 STATUS_NAMES = ["ok", "busy", "cold", "stale", "nospec", "bad-job", "pool-too-small", "out-of-memory",
                 "device"]
 (T_Q, T_K, T_V, T_O, T_GATE, T_UP, T_DOWN, T_LN1, T_LN2, T_WTE, T_NORM, T_LM_HEAD) = range(12)
+# a hybrid checkpoint's full_attention extras and linear_attention tensors
+(T_ATTN_GATE, T_Q_NORM, T_K_NORM, T_IN_Q, T_IN_K, T_IN_V, T_IN_Z, T_IN_B, T_IN_A, T_CONV_Q, T_CONV_K, T_CONV_V,
+ T_GATE_PARAMS, T_GATED_NORM, T_OUT_PROJ) = range(12, 27)
+FULL_ATTENTION, LINEAR_ATTENTION = 0, 1
 EXPORTS = [
     "cc_create", "cc_destroy", "cc_last_error", "cc_upload", "cc_fill_random", "cc_step", "cc_release",
     "cc_slot_pages", "cc_free_pages", "cc_fill_random_kv", "cc_read_kv", "cc_write_kv", "cc_read_pages",
@@ -29,7 +33,10 @@ class Dims(C.Structure):
                 ("n_kv_heads", C.c_int32), ("head_dim", C.c_int32), ("ffn", C.c_int32), ("vocab", C.c_int32),
                 ("q8_group", C.c_int32), ("rms_eps", C.c_float), ("rope_theta", C.c_double),
                 ("rope_scaling", C.c_int32), ("rs_factor", C.c_double), ("rs_low_freq", C.c_double),
-                ("rs_high_freq", C.c_double), ("rs_orig_max_pos", C.c_double), ("tied", C.c_int32)]
+                ("rs_high_freq", C.c_double), ("rs_orig_max_pos", C.c_double), ("tied", C.c_int32),
+                ("rot_dim", C.c_int32), ("hybrid", C.c_int32), ("layer_kinds", C.POINTER(C.c_uint8)),
+                ("lin_nk", C.c_int32), ("lin_nv", C.c_int32), ("lin_dk", C.c_int32), ("lin_dv", C.c_int32),
+                ("lin_conv", C.c_int32)]
 
 
 class Opts(C.Structure):
@@ -108,15 +115,31 @@ class CCError(RuntimeError):
         self.kind = STATUS_NAMES[status] if 0 <= status < len(STATUS_NAMES) else str(status)
 
 
+def layer_kinds(d):
+    """Block kinds from `layer_types` (the manifest's strings), or None (all full)."""
+    lt = d.get("layer_types")
+    if not lt:
+        return None
+    return [LINEAR_ATTENTION if t == "linear_attention" else FULL_ATTENTION for t in lt]
+
+
 def make_dims(d):
     sc = d.get("rope_scaling")
-    return Dims(hidden=d["hidden"], n_layer=d["n_layer"], n_heads=d["n_heads"], n_kv_heads=d["n_kv_heads"],
+    dims = Dims(hidden=d["hidden"], n_layer=d["n_layer"], n_heads=d["n_heads"], n_kv_heads=d["n_kv_heads"],
                 head_dim=d["head_dim"], ffn=d["ffn"], vocab=d["vocab"], q8_group=d.get("group_q8", 32),
                 rms_eps=d["rms_eps"], rope_theta=d["rope_theta"], rope_scaling=1 if sc else 0,
                 rs_factor=sc["factor"] if sc else 0.0, rs_low_freq=sc["low_freq_factor"] if sc else 0.0,
                 rs_high_freq=sc["high_freq_factor"] if sc else 0.0,
                 rs_orig_max_pos=sc["original_max_position_embeddings"] if sc else 0.0,
-                tied=1 if d.get("tied", True) else 0)
+                tied=1 if d.get("tied", True) else 0, rot_dim=d.get("rot_dim", 0) or 0,
+                hybrid=1 if d.get("hybrid") else 0, lin_nk=d.get("lin_nk", 0), lin_nv=d.get("lin_nv", 0),
+                lin_dk=d.get("lin_dk", 0), lin_dv=d.get("lin_dv", 0), lin_conv=d.get("lin_conv", 0))
+    kinds = layer_kinds(d)
+    if kinds is not None:
+        arr = (C.c_uint8 * len(kinds))(*kinds)
+        dims._kinds = arr   # kept alive with the struct; cc_create copies it
+        dims.layer_kinds = C.cast(arr, C.POINTER(C.c_uint8))
+    return dims
 
 
 class Context:
@@ -171,6 +194,8 @@ class Context:
                                      int(group)))
 
     def upload_norm(self, layer, tensor, w):
+        """An f32 tensor: a norm weight, or a hybrid block's q_norm, k_norm,
+        conv1d_q/k/v ([channels, 4]), gate_params or gated_norm."""
         w = np.ascontiguousarray(w, np.float32)
         self._chk(self.lib.cc_upload(self.h, layer, tensor, _p(w), w.size, None, 0, 0, 32))
 

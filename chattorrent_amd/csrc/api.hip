@@ -25,11 +25,22 @@ namespace {
 constexpr int TOPK_MAX = 256;   // web/model/sampling.js:125
 
 struct Layer {
+    int kind = CC_FULL_ATTENTION;
     QTensor qkv, o, gu, down;
     float* ln1 = nullptr;
     float* ln2 = nullptr;
     uint8_t* kpool = nullptr;
     uint8_t* vpool = nullptr;
+    // a hybrid checkpoint's full_attention extras (attn_gate rides in qkv)
+    float* qn = nullptr;
+    float* kn = nullptr;
+    // linear_attention: fused in_proj (q|k|v|z|b|a), out_proj, conv weights
+    // [convDim][4], gate_params [2*nV], gated_norm [Dv], per-session state
+    QTensor lin, out;
+    float* conv = nullptr;
+    float* gp = nullptr;
+    float* gnorm = nullptr;
+    float* state = nullptr;
 };
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
@@ -41,6 +52,16 @@ struct cc_ctx {
     cc_opts o{};
     int group = 0, D = 0, rot = 0, L0 = 0, L1 = 0;
     bool embed = false, head = false;
+    // hybrid checkpoints: block kinds (model numbering), Gated DeltaNet shape,
+    // q width n_heads*head_dim, and the linear blocks' scratch
+    bool hybrid = false;
+    std::vector<uint8_t> kinds;
+    LinGeom lg{};
+    int qdim = 0;
+    float* lraw = nullptr;         // [t_max][lg.W] conv outputs, z, b, a
+    float* lcore = nullptr;        // [t_max][valueDim] recurrence output
+    uint4* xp_v = nullptr;         // operand for K = valueDim
+    float* gbuf = nullptr;         // [t_max][qdim] output-gate values
     std::vector<Layer> layers;
     QTensor wte, lm_head;
     float* norm = nullptr;
@@ -171,9 +192,33 @@ cc_status check_dims(cc_ctx* ctx, const cc_dims& d, const cc_opts& o) {
     if (d.hidden <= 0 || d.n_layer <= 0 || d.n_heads <= 0 || d.n_kv_heads <= 0 || d.head_dim <= 0 ||
         d.ffn <= 0 || d.vocab <= 0)
         return fail(ctx, CC_EARG, "every dimension must be positive");
-    if (d.n_heads * d.head_dim != d.hidden)
+    const bool hyb = d.hybrid != 0;
+    if (!hyb && d.n_heads * d.head_dim != d.hidden)
         return fail(ctx, CC_EARG, "n_heads*head_dim (" + std::to_string(d.n_heads * d.head_dim) +
                                       ") != hidden (" + std::to_string(d.hidden) + ")");
+    const int rot = d.rot_dim ? d.rot_dim : d.head_dim;
+    if (rot < 2 || rot > d.head_dim || rot % 2)
+        return fail(ctx, CC_EARG, "rot_dim must be even and at most head_dim (RoPE's split-half pairing)");
+    bool any_linear = false;
+    if (d.layer_kinds) {
+        for (int i = 0; i < d.n_layer; i++) {
+            if (d.layer_kinds[i] > CC_LINEAR_ATTENTION)
+                return fail(ctx, CC_EARG, "layer_kinds holds a kind other than full or linear attention");
+            any_linear = any_linear || d.layer_kinds[i] == CC_LINEAR_ATTENTION;
+        }
+    }
+    if (any_linear && !hyb) return fail(ctx, CC_EARG, "linear_attention blocks need a hybrid checkpoint");
+    if (any_linear) {
+        // loader.js:225-230, plus the Gated DeltaNet kernels' shapes
+        if (d.lin_nk <= 0 || d.lin_nv <= 0 || d.lin_nv % d.lin_nk)
+            return fail(ctx, CC_EARG, "linear_num_value_heads (" + std::to_string(d.lin_nv) +
+                                          ") not divisible by linear_num_key_heads (" + std::to_string(d.lin_nk) + ")");
+        if (d.lin_dk != 16 && d.lin_dk != 32 && d.lin_dk != 64 && d.lin_dk != 128)
+            return fail(ctx, CC_EARG, "linear_key_head_dim must be 16, 32, 64 or 128");
+        if (d.lin_dv <= 0 || d.lin_dv % 16 || d.lin_dv > 512)
+            return fail(ctx, CC_EARG, "linear_value_head_dim must be a multiple of 16, at most 512");
+        if (d.lin_conv != LIN_CONV_K) return fail(ctx, CC_EARG, "linear_conv_kernel_dim must be 4");
+    }
     if (d.n_heads % d.n_kv_heads != 0) return fail(ctx, CC_EARG, "n_heads not divisible by n_kv_heads");
     if (d.head_dim != 64 && d.head_dim != 128)
         return fail(ctx, CC_EARG, "head_dim must be 64 or 128 (the int8 KV blocks are 32 wide)");
@@ -185,8 +230,11 @@ cc_status check_dims(cc_ctx* ctx, const cc_dims& d, const cc_opts& o) {
         return fail(ctx, CC_EARG, "hidden above " + std::to_string(RESID_NORM_HMAX) + " is not supported");
     // The matmul addresses a weight with 32-bit byte offsets.
     const double H = d.hidden, F = d.ffn;
+    const double qd = (double)d.n_heads * d.head_dim;
     const double big = std::max({(double)d.vocab * H, 2.0 * F * H, F * H,
-                                 (H + 2.0 * d.n_kv_heads * d.head_dim) * H}) * 1.0625;
+                                 (2.0 * qd + 2.0 * d.n_kv_heads * d.head_dim) * H,
+                                 (2.0 * d.lin_nk * d.lin_dk + 2.0 * d.lin_nv * d.lin_dv + 2.0 * d.lin_nv + 32) * H}) *
+                       1.0625;
     if (big > 2.0e9) return fail(ctx, CC_EARG, "a weight above 2 GB is not supported");
     if ((double)o.t_max * std::max(d.vocab, 2 * d.ffn) * 4.0 > 2.0e9)
         return fail(ctx, CC_EARG, "t_max rows of logits must stay under 2 GB");
@@ -301,11 +349,15 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
     cc_ctx* ctx = new cc_ctx();
     ctx->d = *dims;
     ctx->o = *opts;
+    ctx->d.layer_kinds = nullptr;   // the caller's array is copied below, once checked
     cc_status st = check_dims(ctx, *dims, *opts);
     if (st != CC_OK) {
         *out = ctx;   // the caller reads the message, then destroys
         return st;
     }
+    ctx->kinds.assign(dims->n_layer, (uint8_t)CC_FULL_ATTENTION);
+    if (dims->layer_kinds) ctx->kinds.assign(dims->layer_kinds, dims->layer_kinds + dims->n_layer);
+    ctx->d.layer_kinds = ctx->kinds.data();
     const cc_dims& d = ctx->d;
     const cc_opts& o = ctx->o;
     {
@@ -326,7 +378,27 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         HIPCHK(hipEventCreate(&ctx->ev1));
         ctx->group = d.n_heads / d.n_kv_heads;
         ctx->D = d.head_dim;
-        ctx->rot = d.head_dim;
+        ctx->rot = d.rot_dim ? d.rot_dim : d.head_dim;
+        ctx->hybrid = d.hybrid != 0;
+        ctx->qdim = d.n_heads * d.head_dim;
+        {
+            // Gated DeltaNet geometry (loader.js:185-195 d.linear)
+            LinGeom& lg = ctx->lg;
+            lg.nK = d.lin_nk;
+            lg.nV = d.lin_nv;
+            lg.Dk = d.lin_dk;
+            lg.Dv = d.lin_dv;
+            lg.K4 = LIN_CONV_K;
+            lg.group = d.lin_nk > 0 ? d.lin_nv / d.lin_nk : 1;
+            lg.keyDim = d.lin_nk * d.lin_dk;
+            lg.valueDim = d.lin_nv * d.lin_dv;
+            lg.convDim = 2 * lg.keyDim + lg.valueDim;
+            lg.nVp = 16 * ceil_div(std::max(d.lin_nv, 0), 16);
+            lg.W = lg.convDim + lg.valueDim + 2 * lg.nV;
+            lg.N = 2 * lg.keyDim + 2 * lg.valueDim + 2 * lg.nVp;
+            lg.hist_off = (size_t)lg.nV * lg.Dk * lg.Dv;
+            lg.sstride = lg.hist_off + (size_t)(LIN_CONV_K - 1) * lg.convDim;
+        }
         const int positions = d.n_layer + 2;
         ctx->embed = o.lo == 0;
         ctx->head = o.hi == positions;
@@ -356,18 +428,43 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         }
         const size_t pool_bytes = (size_t)ctx->n_pages * nKV * ctx->geom.blk;
         ctx->layers.resize(ctx->L1 - ctx->L0);
-        for (auto& L : ctx->layers) {
-            HIPCHK(alloc_q(ctx, L.qkv, (nH + 2 * nKV) * D, H));
-            HIPCHK(alloc_q(ctx, L.o, H, nH * D));
+        bool any_full = false, any_linear = false;
+        const LinGeom& lg = ctx->lg;
+        for (int li = 0; li < (int)ctx->layers.size(); li++) {
+            Layer& L = ctx->layers[li];
+            L.kind = ctx->kinds[ctx->L0 + li];
+            if (L.kind == CC_LINEAR_ATTENTION) {
+                any_linear = true;
+                HIPCHK(alloc_q(ctx, L.lin, lg.N, H));
+                HIPCHK(alloc_q(ctx, L.out, H, lg.valueDim));
+                HIPCHK(dalloc(ctx, &L.conv, (size_t)lg.convDim * LIN_CONV_K * 4, &ctx->weight_bytes));
+                HIPCHK(dalloc(ctx, &L.gp, (size_t)2 * lg.nV * 4, &ctx->weight_bytes));
+                HIPCHK(dalloc(ctx, &L.gnorm, (size_t)lg.Dv * 4, &ctx->weight_bytes));
+                launch_fill(ctx->stream, L.gnorm, lg.Dv, 1.0f);
+                // recurrent state, one block per session frame (model.js:46-58)
+                HIPCHK(dalloc(ctx, &L.state, (size_t)o.sessions * lg.sstride * 4, &ctx->kv_bytes));
+            } else {
+                any_full = true;
+                // q | k | v, and on a hybrid checkpoint the output gate's rows after v
+                HIPCHK(alloc_q(ctx, L.qkv, (nH + 2 * nKV) * D + (ctx->hybrid ? nH * D : 0), H));
+                HIPCHK(alloc_q(ctx, L.o, H, nH * D));
+                if (ctx->hybrid) {
+                    HIPCHK(dalloc(ctx, &L.qn, (size_t)D * 4, &ctx->weight_bytes));
+                    HIPCHK(dalloc(ctx, &L.kn, (size_t)D * 4, &ctx->weight_bytes));
+                    launch_fill(ctx->stream, L.qn, D, 1.0f);
+                    launch_fill(ctx->stream, L.kn, D, 1.0f);
+                }
+                HIPCHK(dalloc(ctx, &L.kpool, pool_bytes, &ctx->kv_bytes));
+                HIPCHK(dalloc(ctx, &L.vpool, pool_bytes, &ctx->kv_bytes));
+            }
             HIPCHK(alloc_q(ctx, L.gu, 2 * F, H));
             HIPCHK(alloc_q(ctx, L.down, H, F));
             HIPCHK(dalloc(ctx, &L.ln1, (size_t)H * 4, &ctx->weight_bytes));
             HIPCHK(dalloc(ctx, &L.ln2, (size_t)H * 4, &ctx->weight_bytes));
             launch_fill(ctx->stream, L.ln1, H, 1.0f);
             launch_fill(ctx->stream, L.ln2, H, 1.0f);
-            HIPCHK(dalloc(ctx, &L.kpool, pool_bytes, &ctx->kv_bytes));
-            HIPCHK(dalloc(ctx, &L.vpool, pool_bytes, &ctx->kv_bytes));
         }
+        (void)any_full;
         if (ctx->embed || (ctx->head && d.tied)) HIPCHK(alloc_q(ctx, ctx->wte, d.vocab, H));
         if (ctx->head) {
             HIPCHK(dalloc(ctx, &ctx->norm, (size_t)H * 4, &ctx->weight_bytes));
@@ -392,11 +489,16 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         HIPCHK(dalloc(ctx, &ctx->xp_o, xp_bytes(nH * D), &ctx->scratch_bytes));
         HIPCHK(dalloc(ctx, &ctx->xp_f, xp_bytes(F), &ctx->scratch_bytes));
         HIPCHK(dalloc(ctx, &ctx->ssp, (size_t)16 * ctx->mt_alloc * RW_SMAX * 4, &ctx->scratch_bytes));
-        size_t pf = 16;
-        if (!ctx->layers.empty()) {
-            const Layer& L = ctx->layers[0];
-            for (const QTensor* q : {&L.qkv, &L.o, &L.gu, &L.down}) pf = std::max(pf, (size_t)q->P * T * q->N);
+        if (any_linear) {
+            HIPCHK(dalloc(ctx, &ctx->xp_v, xp_bytes(lg.valueDim), &ctx->scratch_bytes));
+            HIPCHK(dalloc(ctx, &ctx->lraw, (size_t)T * lg.W * 4, &ctx->scratch_bytes));
+            HIPCHK(dalloc(ctx, &ctx->lcore, (size_t)T * lg.valueDim * 4, &ctx->scratch_bytes));
         }
+        if (ctx->hybrid) HIPCHK(dalloc(ctx, &ctx->gbuf, (size_t)T * nH * D * 4, &ctx->scratch_bytes));
+        size_t pf = 16;
+        for (const Layer& L : ctx->layers)
+            for (const QTensor* q : {&L.qkv, &L.o, &L.gu, &L.down, &L.lin, &L.out})
+                if (q->codes) pf = std::max(pf, (size_t)q->P * T * q->N);
         ctx->part_floats = pf;
         HIPCHK(dalloc(ctx, &ctx->part, pf * 4, &ctx->scratch_bytes));
         // Q operands: sum over jobs of nKV * ceil(n*group/16) * ng * 2 * 64 uint4.
@@ -441,7 +543,28 @@ static QTensor* tensor_of(cc_ctx* ctx, int layer, int tensor, int* row_tile0, in
     const int li = layer - ctx->L0;
     if (li < 0 || li >= (int)ctx->layers.size()) return nullptr;
     Layer& L = ctx->layers[li];
+    if (L.kind == CC_LINEAR_ATTENTION) {
+        // fused in_proj rows: q | k | v | z | b (nVp) | a (nVp)
+        const LinGeom& lg = ctx->lg;
+        const int kd = lg.keyDim, vd = lg.valueDim;
+        switch (tensor) {
+            case CC_T_IN_Q: *row_tile0 = 0; *N = kd; *K = H; return &L.lin;
+            case CC_T_IN_K: *row_tile0 = kd / 16; *N = kd; *K = H; return &L.lin;
+            case CC_T_IN_V: *row_tile0 = 2 * kd / 16; *N = vd; *K = H; return &L.lin;
+            case CC_T_IN_Z: *row_tile0 = (2 * kd + vd) / 16; *N = vd; *K = H; return &L.lin;
+            case CC_T_IN_B: *row_tile0 = (2 * kd + 2 * vd) / 16; *N = lg.nV; *K = H; return &L.lin;
+            case CC_T_IN_A: *row_tile0 = (2 * kd + 2 * vd + lg.nVp) / 16; *N = lg.nV; *K = H; return &L.lin;
+            case CC_T_OUT_PROJ: *row_tile0 = 0; *N = H; *K = vd; return &L.out;
+            case CC_T_GATE: *row_tile0 = 0; *N = F; *K = H; return &L.gu;
+            case CC_T_UP: *row_tile0 = F / 16; *N = F; *K = H; return &L.gu;
+            case CC_T_DOWN: *row_tile0 = 0; *N = H; *K = F; return &L.down;
+        }
+        return nullptr;
+    }
     switch (tensor) {
+        case CC_T_ATTN_GATE:
+            if (!ctx->hybrid) return nullptr;
+            *row_tile0 = (nH + 2 * nKV) * D / 16; *N = nH * D; *K = H; return &L.qkv;
         case CC_T_Q: *row_tile0 = 0; *N = nH * D; *K = H; return &L.qkv;
         case CC_T_K: *row_tile0 = nH * D / 16; *N = nKV * D; *K = H; return &L.qkv;
         case CC_T_V: *row_tile0 = (nH + nKV) * D / 16; *N = nKV * D; *K = H; return &L.qkv;
@@ -457,16 +580,41 @@ cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data
                     size_t ns, int32_t scale_dtype, int32_t group) {
     if (!ctx || !data) return fail(ctx, CC_EARG, "null argument");
     const cc_dims& d = ctx->d;
-    if (tensor == CC_T_LN1 || tensor == CC_T_LN2 || tensor == CC_T_NORM) {
+    const bool f32_tensor = tensor == CC_T_LN1 || tensor == CC_T_LN2 || tensor == CC_T_NORM ||
+                            (tensor >= CC_T_Q_NORM && tensor <= CC_T_K_NORM) ||
+                            (tensor >= CC_T_CONV_Q && tensor <= CC_T_GATED_NORM);
+    if (f32_tensor) {
         float* dst = nullptr;
+        size_t want = d.hidden;
         if (tensor == CC_T_NORM) dst = ctx->norm;
         else {
             const int li = layer - ctx->L0;
             if (li < 0 || li >= (int)ctx->layers.size()) return fail(ctx, CC_EARG, "layer not held here");
-            dst = tensor == CC_T_LN1 ? ctx->layers[li].ln1 : ctx->layers[li].ln2;
+            Layer& L = ctx->layers[li];
+            const LinGeom& lg = ctx->lg;
+            switch (tensor) {
+                case CC_T_LN1: dst = L.ln1; break;
+                case CC_T_LN2: dst = L.ln2; break;
+                case CC_T_Q_NORM: dst = L.qn; want = d.head_dim; break;
+                case CC_T_K_NORM: dst = L.kn; want = d.head_dim; break;
+                // conv weights [channels][4], the q, k, v channel ranges in order
+                case CC_T_CONV_Q: dst = L.conv; want = (size_t)lg.keyDim * LIN_CONV_K; break;
+                case CC_T_CONV_K:
+                    dst = L.conv ? L.conv + (size_t)lg.keyDim * LIN_CONV_K : nullptr;
+                    want = (size_t)lg.keyDim * LIN_CONV_K;
+                    break;
+                case CC_T_CONV_V:
+                    dst = L.conv ? L.conv + (size_t)2 * lg.keyDim * LIN_CONV_K : nullptr;
+                    want = (size_t)lg.valueDim * LIN_CONV_K;
+                    break;
+                case CC_T_GATE_PARAMS: dst = L.gp; want = (size_t)2 * lg.nV; break;
+                case CC_T_GATED_NORM: dst = L.gnorm; want = lg.Dv; break;
+            }
         }
         if (!dst) return fail(ctx, CC_EARG, "tensor not held here");
-        if (n != (size_t)d.hidden) return fail(ctx, CC_EARG, "a norm weight has `hidden` f32 values");
+        if (n != want)
+            return fail(ctx, CC_EARG, "f32 tensor " + std::to_string(tensor) + " has " + std::to_string(want) +
+                                          " values, not " + std::to_string(n));
         HIPCHK(hipMemcpyAsync(dst, data, n * 4, hipMemcpyHostToDevice, ctx->stream));
         HIPCHK(hipStreamSynchronize(ctx->stream));
         return CC_OK;
@@ -504,6 +652,7 @@ cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data
 cc_status cc_fill_random(cc_ctx* ctx, uint64_t seed) {
     if (!ctx) return CC_EARG;
     const cc_dims& d = ctx->d;
+    if (ctx->hybrid) return fail(ctx, CC_EARG, "a hybrid model's weights are uploaded, not generated");
     for (int li = 0; li < (int)ctx->layers.size(); li++) {
         const int layer = ctx->L0 + li;
         for (int t = CC_T_Q; t <= CC_T_DOWN; t++) {
@@ -584,6 +733,7 @@ cc_status cc_fill_random_kv(cc_ctx* ctx, int32_t slot, int32_t tokens, uint64_t 
     if (st != CC_OK) return st;
     for (int li = 0; li < (int)ctx->layers.size(); li++) {
         const int layer = ctx->L0 + li;
+        if (!ctx->layers[li].kpool) continue;   // a linear_attention block keeps no KV
         for (int which = 0; which < 2; which++)
             launch_fill_kv(ctx->stream, which ? ctx->layers[li].vpool : ctx->layers[li].kpool, ctx->page_table,
                            slot, tokens, ctx->geom, seed, 0x4B560000ull + (uint64_t)layer * 2 + which, key, which);
@@ -599,6 +749,7 @@ static cc_status kv_io(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot, 
         slot >= (int)ctx->owned.size() || head < 0 || head >= ctx->geom.nKV || t0 < 0 || t1 < t0 ||
         ceil_div(t1, ctx->geom.page) > ctx->owned[slot])
         return fail(ctx, CC_EARG, "rows outside the slot's pages");
+    if (!ctx->layers[li].kpool) return fail(ctx, CC_EARG, "a linear_attention block keeps no KV");
     const size_t words = (size_t)(t1 - t0) * (ctx->geom.D / 4 + ctx->geom.ng);
     uint32_t* dbuf = nullptr;
     HIPCHK(hipMalloc(&dbuf, words * 4 + 16));
@@ -767,20 +918,41 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
     rs.nsl = ceil_div(H / 4, RW_THREADS);
     rs.H = H;
     rs.eps = d.rms_eps;
+    const int KUH = ceil_div(H, 64);   // every block's first matmul reads K = hidden
+    const int njobs = (int)p.jobs.size();
     for (int b = b0; b < b1; b++) {
         Layer& L = ctx->layers[b - ctx->L0];
-        if (b == b0) launch_resid_w(st, ctx->x, nullptr, 0, T, Mpad, H, 0, L.ln1, L.qkv.KU, ctx->xp_h, ctx->ssp);
-        const int sq = L.qkv.P;
-        launch_gemm(st, L.qkv, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-        launch_fin_qkv(st, ctx->part, sq, T, drow_job, djobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
-                       L.kpool, L.vpool, ctx->page_table, ctx->qp, rs, 1, 1);
-        launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
-                     ctx->ppw, ctx->apart);
-        launch_attn_combine(st, djobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU,
-                             ctx->xp_o, nullptr, dcwg, p.ncwg);
-        const int so = L.o.P;
-        launch_gemm(st, L.o, ctx->xp_o, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-        launch_resid_w(st, ctx->x, ctx->part, so, T, Mpad, H, 0, L.ln2, L.gu.KU, ctx->xp_h, ctx->ssp);
+        if (b == b0) launch_resid_w(st, ctx->x, nullptr, 0, T, Mpad, H, 0, L.ln1, KUH, ctx->xp_h, ctx->ssp);
+        if (L.kind == CC_LINEAR_ATTENTION) {
+            // linearBlockSegs (model.js:472-527): in_proj, conv + ring, the
+            // recurrence on each session's state, gated norm, out_proj
+            const LinGeom& lg = ctx->lg;
+            launch_gemm(st, L.lin, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
+            launch_lin_conv(st, ctx->part, L.lin.P, T, njobs, djobs, rs, L.conv, lg, L.state, ctx->lraw);
+            launch_gdn(st, ctx->lraw, njobs, djobs, L.gp, lg, L.state, ctx->lcore);
+            launch_lin_norm(st, ctx->lcore, ctx->lraw, L.gnorm, d.rms_eps, T, lg, L.out.KU, ctx->xp_v);
+            launch_gemm(st, L.out, ctx->xp_v, ctx->mt_alloc, ctx->part, T, ctx->ncu);
+            launch_resid_w(st, ctx->x, ctx->part, L.out.P, T, Mpad, H, 0, L.ln2, KUH, ctx->xp_h, ctx->ssp);
+        } else {
+            QkExtras ex;
+            if (ctx->hybrid) {
+                ex.qn = L.qn;
+                ex.kn = L.kn;
+                ex.eps = d.rms_eps;
+                ex.gate = ctx->gbuf;
+            }
+            const int sq = L.qkv.P;
+            launch_gemm(st, L.qkv, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
+            launch_fin_qkv(st, ctx->part, sq, T, drow_job, djobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
+                           L.kpool, L.vpool, ctx->page_table, ctx->qp, rs, 1, 1, ex);
+            launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom,
+                         ctx->group, ctx->ppw, ctx->apart);
+            launch_attn_combine(st, djobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU, ctx->xp_o, nullptr, dcwg,
+                                 p.ncwg, ctx->hybrid ? ctx->gbuf : nullptr);
+            const int so = L.o.P;
+            launch_gemm(st, L.o, ctx->xp_o, ctx->mt_alloc, ctx->part, T, ctx->ncu);
+            launch_resid_w(st, ctx->x, ctx->part, so, T, Mpad, H, 0, L.ln2, KUH, ctx->xp_h, ctx->ssp);
+        }
         const int sg = L.gu.P;
         launch_gemm(st, L.gu, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
         launch_fin_swiglu(st, ctx->part, sg, T, Mpad, d.ffn, L.down.KU, ctx->xp_f, rs);
@@ -788,7 +960,7 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
         launch_gemm(st, L.down, ctx->xp_f, ctx->mt_alloc, ctx->part, T, ctx->ncu);
         const bool next = b + 1 < b1;
         launch_resid_w(st, ctx->x, ctx->part, sd, T, Mpad, H, 1, next ? ctx->layers[b + 1 - ctx->L0].ln1 : nullptr,
-                       next ? ctx->layers[b + 1 - ctx->L0].qkv.KU : 0, next ? ctx->xp_h : nullptr, ctx->ssp);
+                       next ? KUH : 0, next ? ctx->xp_h : nullptr, ctx->ssp);
     }
     (void)D;
 }
@@ -807,19 +979,31 @@ static void prof_replay(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, in
     const int T = p.T;
     const JobDev* djobs = (const JobDev*)(ctx->d_meta + ml.jobs);
     const AttnItem* ditems = (const AttnItem*)(ctx->d_meta + ml.items);
+    // (a linear_attention block has no q|k|v, o or KV: its matmuls are not replayed)
     auto blocks = [&](int kind, QTensor Layer::*w, const uint4* xp) {
         double bytes = 0;
-        for (int b = b0; b < b1; b++) bytes += qbytes(ctx->layers[b - ctx->L0].*w);
-        prof_mark(ctx, kind, b1 - b0, bytes, [&] {
-            for (int b = b0; b < b1; b++) launch_gemm(st, ctx->layers[b - ctx->L0].*w, xp, ctx->mt_alloc, ctx->part, T, ctx->ncu);
+        int n = 0;
+        for (int b = b0; b < b1; b++)
+            if ((ctx->layers[b - ctx->L0].*w).codes) {
+                bytes += qbytes(ctx->layers[b - ctx->L0].*w);
+                n++;
+            }
+        if (n == 0) return;
+        prof_mark(ctx, kind, n, bytes, [&] {
+            for (int b = b0; b < b1; b++)
+                if ((ctx->layers[b - ctx->L0].*w).codes)
+                    launch_gemm(st, ctx->layers[b - ctx->L0].*w, xp, ctx->mt_alloc, ctx->part, T, ctx->ncu);
         });
     };
     if (b1 > b0) {
         blocks(CC_K_QKV, &Layer::qkv, ctx->xp_h);
-        if (p.nitems > 0)
-            prof_mark(ctx, CC_K_ATTN, b1 - b0, p.kv_bytes * (b1 - b0), [&] {
+        int nfull = 0;
+        for (int b = b0; b < b1; b++) nfull += ctx->layers[b - ctx->L0].kpool != nullptr;
+        if (p.nitems > 0 && nfull > 0)
+            prof_mark(ctx, CC_K_ATTN, nfull, p.kv_bytes * nfull, [&] {
                 for (int b = b0; b < b1; b++) {
                     const Layer& L = ctx->layers[b - ctx->L0];
+                    if (!L.kpool) continue;
                     launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom,
                                 ctx->group, ctx->ppw, ctx->apart);
                 }
@@ -1074,6 +1258,7 @@ cc_status cc_op_rmsnorm(cc_ctx* ctx, const float* x, const float* w, int32_t T, 
 static cc_status one_job(cc_ctx* ctx, int32_t layer, int32_t slot, int32_t n, int32_t past, StepPlan& p,
                          MetaLayout& ml) {
     if (layer - ctx->L0 < 0 || layer - ctx->L0 >= (int)ctx->layers.size()) return fail(ctx, CC_EARG, "layer not held");
+    if (!ctx->layers[layer - ctx->L0].kpool) return fail(ctx, CC_EARG, "a linear_attention block keeps no KV");
     if (slot < 0 || slot >= (int)ctx->owned.size() || n < 1 || n > ctx->o.t_max || past < 0 ||
         past + n > ctx->o.n_max)
         return fail(ctx, CC_EARG, "bad job");

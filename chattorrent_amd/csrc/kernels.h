@@ -70,10 +70,44 @@ void launch_prep_rows(hipStream_t st, const float* x, int ldx, int M, int Mpad, 
                       uint4* Xp);
 void launch_fin_swiglu(hipStream_t st, const float* part, int splits, int M, int Mpad, int F,
                        int KU, uint4* Xp, const RowScale& rs);
+// A hybrid checkpoint's full-attention extras (web/model/model.js:368-410):
+// q_norm / k_norm (rmsnorm over each head's D values, applied before RoPE)
+// and the output gate's projection, whose rows follow v in the fused q|k|v
+// matmul and go to `gate` [M][nH*D] (times the row factor).
+struct QkExtras {
+    const float* qn = nullptr;
+    const float* kn = nullptr;
+    float eps = 0.f;
+    float* gate = nullptr;
+};
 void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const int32_t* row_job,
                     const JobDev* jobs, int nH, int group, const KVGeom& g, const float* tbl,
                     int rot, uint8_t* kpool, uint8_t* vpool, const uint32_t* page_table,
-                    uint4* Qp, const RowScale& rs, int do_q, int do_kv);
+                    uint4* Qp, const RowScale& rs, int do_q, int do_kv, const QkExtras& ex = QkExtras{});
+
+// Gated DeltaNet (web/model/kernels.js:1531-1839) over packed jobs. Columns of
+// the fused projection (planes of N = 2*keyDim + 2*valueDim + 2*nVp): q, k, v
+// (the conv channels, convDim = 2*keyDim + valueDim), z, b (nV, padded to
+// nVp), a (nV, padded). `lraw` rows [M][LinGeom::W] hold the conv outputs
+// (after SiLU), then z, b, a. A session's state block (stride `sstride`
+// floats, session `slot`): S [nV][Dk][Dv], then the conv ring [K-1][convDim].
+struct LinGeom {
+    int nK = 0, nV = 0, Dk = 0, Dv = 0, K4 = 4, group = 1;
+    int keyDim = 0, valueDim = 0, convDim = 0, nVp = 0;
+    int W = 0;          // convDim + valueDim + 2*nV
+    int N = 0;          // fused projection rows
+    size_t sstride = 0; // floats per session
+    size_t hist_off = 0;
+};
+constexpr int LIN_CONV_K = 4;
+void launch_lin_conv(hipStream_t st, const float* part, int splits, int M, int njobs, const JobDev* jobs,
+                     const RowScale& rs, const float* conv, const LinGeom& lg, float* state, float* lraw);
+void launch_gdn(hipStream_t st, const float* lraw, int njobs, const JobDev* jobs, const float* gp,
+                const LinGeom& lg, float* state, float* core);
+// RMSNormGated per (row, value head) with the gated_norm weight, times
+// silu(z), into the out_proj operand (K = valueDim).
+void launch_lin_norm(hipStream_t st, const float* core, const float* lraw, const float* gnorm, float eps,
+                     int M, const LinGeom& lg, int KU, uint4* Xp);
 void launch_embed(hipStream_t st, const int32_t* ids, const uint16_t* hidden, int T, const QTensor& wte,
                   float* x);
 void launch_topk(hipStream_t st, const float* logits, int planes, int rows, int V, int M, uint64_t* a,
@@ -107,7 +141,11 @@ void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const floa
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
                   const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
                   int ppw, float* part);
+// `gate` (a hybrid checkpoint's, [rows][nH*D], or null): the output is
+// multiplied by sigmoid(gate) before it becomes the o_proj operand
+// (web/model/kernels.js:1822-1839 sigmoid_mul).
 void launch_attn_combine(hipStream_t st, const JobDev* jobs, const float* part, const KVGeom& g, int nH, int group,
-                         int KU, uint4* Xp, float* ctx_out, const int32_t* wg_job, int nwg);
+                         int KU, uint4* Xp, float* ctx_out, const int32_t* wg_job, int nwg,
+                         const float* gate = nullptr);
 void launch_sum_splits(hipStream_t st, const float* part, int splits, int M, int N, float* out);
 void launch_to_half_bits(hipStream_t st, const float* x, int64_t n, uint16_t* out);

@@ -867,13 +867,14 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
                                                   const float* __restrict__ tbl, int rot, uint8_t* __restrict__ kpool,
                                                   uint8_t* __restrict__ vpool,
                                                   const uint32_t* __restrict__ page_table, uint4* __restrict__ Qp,
-                                                  RowScale rs, int do_q, int do_kv) {
+                                                  RowScale rs, int do_q, int do_kv, QkExtras ex) {
     __shared__ float buf[4][D];
     __shared__ float rq[4][D];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m = blockIdx.y;
     const int nKV = g.nKV;
-    const int nall = nH + 2 * nKV;
+    const int nqkv = nH + 2 * nKV;
+    const int nall = nqkv + (ex.gate ? nH : 0);   // a hybrid block's gate heads follow v
     const int hidx = blockIdx.x * 4 + wave;
     const bool live = hidx < nall;
     const int N = nall * D;
@@ -904,6 +905,18 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
         }
     }
     __syncthreads();
+    // q_norm / k_norm (model.js:388-394): rmsnorm over the head's D values
+    // (lane partials, then a wave reduction), before RoPE reads neighbouring
+    // channels
+    if (ex.qn && live && hidx < nH + nKV) {
+        const float* w = hidx < nH ? ex.qn : ex.kn;
+        float ss = 0.0f;
+        for (int d = lane; d < D; d += 64) ss += buf[wave][d] * buf[wave][d];
+        ss = wave_sum(ss);
+        const float scale = 1.0f / sqrtf(ss / (float)D + ex.eps);
+        for (int d = lane; d < D; d += 64) buf[wave][d] = buf[wave][d] * scale * w[d];
+    }
+    __syncthreads();
     if (live && hidx < nH) {
         if (do_q) {
             for (int d = lane; d < D; d += 64) rq[wave][d] = rope_at(buf[wave], d, rot, tbl, pos);
@@ -911,6 +924,14 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
     }
     __syncthreads();
     if (!live) return;
+    if (hidx >= nqkv) {
+        // the output gate's raw values (times the row factor), for the combine
+        if (do_q) {
+            float* gr = ex.gate + (size_t)m * nH * D + (size_t)(hidx - nqkv) * D;
+            for (int d = lane; d < D; d += 64) gr[d] = buf[wave][d];
+        }
+        return;
+    }
     if (hidx < nH) {
         if (!do_q) return;
         if (lane < D / 8) {
@@ -962,15 +983,227 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
 void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const int32_t* row_job,
                     const JobDev* jobs, int nH, int group, const KVGeom& g, const float* tbl, int rot,
                     uint8_t* kpool, uint8_t* vpool, const uint32_t* page_table, uint4* Qp, const RowScale& rs,
-                    int do_q, int do_kv) {
-    const int nall = nH + 2 * g.nKV;
+                    int do_q, int do_kv, const QkExtras& ex) {
+    const int nall = nH + 2 * g.nKV + (ex.gate ? nH : 0);
     dim3 grid((nall + 3) / 4, M);
     if (g.D == 128)
         hipLaunchKernelGGL(k_fin_qkv<128>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
-                           rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv);
+                           rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv, ex);
     else
         hipLaunchKernelGGL(k_fin_qkv<64>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
-                           rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv);
+                           rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv, ex);
+    CHECK_LAUNCH();
+}
+
+// =========================================================== Gated DeltaNet ===
+// A hybrid checkpoint's linear_attention blocks (web/model/model.js:418-527,
+// web/model/kernels.js:1531-1839) over the packed jobs, each on its own
+// session's state. Three kernels after the fused in_proj matmul:
+//   k_lin_conv  planes summed (times the input rmsnorm's row factor), the
+//               depthwise causal conv + SiLU through the job's rows with the
+//               session's ring, the ring advanced; z, b, a passed through;
+//   k_gdn       the gated delta rule with the q/k l2norm folded in;
+//   k_lin_norm  RMSNormGated times silu(z) into the out_proj operand.
+
+// Plane sum of one column in plane order, times the row factor.
+__device__ static inline float plane_col(const float* part, int splits, int M, int N, int m, int col, float f) {
+    float p = part[(size_t)m * N + col];
+    for (int s = 1; s < splits; s++) p = p + part[((size_t)s * M + m) * N + col];
+    return p * f;
+}
+
+// causal_conv1d (kernels.js:1538-1580) + update_conv_history (:1582-1620).
+// One thread per (job, channel) walks the job's rows in order, so the ring
+// (the K-1 raw rows before the current one) stays in registers: it is read
+// from the session's state first (zeros for a job at position 0, a new
+// session) and written back after the job's last row. Per row: acc = sum over
+// k of w[c][k] * x[t-(K-1)+k] in k order, out = acc * (1/(1+exp(-acc))).
+__global__ __launch_bounds__(256) void k_lin_conv(const float* __restrict__ part, int splits, int M,
+                                                  const JobDev* __restrict__ jobs, RowScale rs,
+                                                  const float* __restrict__ conv, LinGeom lg,
+                                                  float* __restrict__ state, float* __restrict__ lraw) {
+    constexpr int K = LIN_CONV_K;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= lg.W) return;
+    const JobDev jb = jobs[blockIdx.y];
+    // plane column: q|k|v|z in place, b and a each padded to nVp rows
+    const int col = c < lg.convDim + lg.valueDim + lg.nV ? c : c - lg.nV + lg.nVp;
+    if (c >= lg.convDim) {
+        for (int i = 0; i < jb.n; i++) {
+            const int m = jb.row0 + i;
+            lraw[(size_t)m * lg.W + c] = plane_col(part, splits, M, lg.N, m, col, row_scale(rs, m));
+        }
+        return;
+    }
+    float* ring = state + (size_t)jb.slot * lg.sstride + lg.hist_off + c;   // [K-1][convDim]
+    float h[K - 1];
+#pragma unroll
+    for (int r = 0; r < K - 1; r++) h[r] = jb.past > 0 ? ring[(size_t)r * lg.convDim] : 0.0f;
+    float w[K];
+#pragma unroll
+    for (int k = 0; k < K; k++) w[k] = conv[(size_t)c * K + k];
+    for (int i = 0; i < jb.n; i++) {
+        const int m = jb.row0 + i;
+        const float x = plane_col(part, splits, M, lg.N, m, col, row_scale(rs, m));
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < K - 1; k++) acc = acc + w[k] * h[k];
+        acc = acc + w[K - 1] * x;
+        const float sg = 1.0f / (1.0f + expf(-acc));
+        lraw[(size_t)m * lg.W + c] = acc * sg;
+#pragma unroll
+        for (int k = 0; k < K - 2; k++) h[k] = h[k + 1];
+        h[K - 2] = x;
+    }
+#pragma unroll
+    for (int r = 0; r < K - 1; r++) ring[(size_t)r * lg.convDim] = h[r];
+}
+
+void launch_lin_conv(hipStream_t st, const float* part, int splits, int M, int njobs, const JobDev* jobs,
+                     const RowScale& rs, const float* conv, const LinGeom& lg, float* state, float* lraw) {
+    if (njobs <= 0) return;
+    hipLaunchKernelGGL(k_lin_conv, dim3((lg.W + 255) / 256, njobs), dim3(256), 0, st, part, splits, M, jobs, rs,
+                       conv, lg, state, lraw);
+    CHECK_LAUNCH();
+}
+
+// gated_delta_net_step (kernels.js:1672-1805) for every row of a job, on its
+// session's S [nV][Dk][Dv]: one workgroup per (value-column tile, value head,
+// job), GDN_KS k-groups x GDN_TV columns; each thread holds DK/GDN_KS rows of
+// its column for the whole job. Per token, in the reference's arithmetic:
+//   g = exp(-exp(A_log) * softplus(a + dt_bias)), beta = sigmoid(b);
+//   s *= g; kv = s.k, qo = s.q over k; kq = k.q;
+//   delta = (v - kv) * beta; s += k * delta; out = (qo + delta*kq) / sqrt(Dk).
+// l2norm_heads (kernels.js:1622-1670) of the head's q and k (source head
+// h / group, the value-head repeat) is folded in: the raw dot products and
+// the sums of squares share the token's one reduction through LDS (double
+// buffered on token parity, one barrier a token), and the factors
+// 1/sqrt(sum x^2 + 1e-6) are applied after it; the state update uses the
+// normalised k. A job at position 0 starts from a zero state.
+constexpr int GDN_KS = 8, GDN_TV = 32;
+template <int DK>
+__global__ __launch_bounds__(GDN_KS * GDN_TV) void k_gdn(const float* __restrict__ lraw, const JobDev* __restrict__ jobs,
+                                                         const float* __restrict__ gp, LinGeom lg,
+                                                         float* __restrict__ state, float* __restrict__ core) {
+    constexpr int ROWS = DK / GDN_KS;
+    __shared__ float pkv[2][GDN_KS][GDN_TV];
+    __shared__ float pqo[2][GDN_KS][GDN_TV];
+    __shared__ float psc[2][GDN_KS][3];   // k.q, q.q, k.k per k-group
+    const int h = blockIdx.y;
+    const JobDev jb = jobs[blockIdx.z];
+    const int col = threadIdx.x % GDN_TV, kg = threadIdx.x / GDN_TV;
+    const int vv = blockIdx.x * GDN_TV + col;
+    const bool live = vv < lg.Dv;
+    const int vvc = live ? vv : lg.Dv - 1;   // out-of-range columns read a real one and discard it
+    const int k0 = kg * ROWS;
+    const int kh = h / lg.group;
+    float* S = state + (size_t)jb.slot * lg.sstride + (size_t)h * DK * lg.Dv;
+    float s[ROWS];
+#pragma unroll
+    for (int i = 0; i < ROWS; i++) s[i] = (jb.past > 0 && live) ? S[(size_t)(k0 + i) * lg.Dv + vv] : 0.0f;
+    const float A = expf(gp[h]), dtb = gp[lg.nV + h];
+    const float q_scale = 1.0f / sqrtf((float)DK);
+    for (int i = 0; i < jb.n; i++) {
+        const int m = jb.row0 + i;
+        const float* row = lraw + (size_t)m * lg.W;
+        const float* qr = row + kh * DK;
+        const float* kr = row + lg.keyDim + kh * DK;
+        const float a = row[lg.convDim + lg.valueDim + lg.nV + h] + dtb;
+        const float sp = a > 20.0f ? a + logf(1.0f + expf(-a)) : logf(1.0f + expf(a));
+        const float g = expf(-A * sp);
+        const float beta = 1.0f / (1.0f + expf(-row[lg.convDim + lg.valueDim + h]));
+        const int buf = i & 1;
+        float kv = 0.0f, qo = 0.0f, kq = 0.0f, qq = 0.0f, kk = 0.0f;
+        float kx[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) {
+            const float ki = kr[k0 + r], qi = qr[k0 + r];
+            kx[r] = ki;
+            s[r] = s[r] * g;
+            kv = kv + s[r] * ki;
+            qo = qo + s[r] * qi;
+            kq = kq + ki * qi;
+            qq = qq + qi * qi;
+            kk = kk + ki * ki;
+        }
+        pkv[buf][kg][col] = kv;
+        pqo[buf][kg][col] = qo;
+        if (col == 0) {
+            psc[buf][kg][0] = kq;
+            psc[buf][kg][1] = qq;
+            psc[buf][kg][2] = kk;
+        }
+        __syncthreads();
+        float kvT = 0.0f, qoT = 0.0f, kqT = 0.0f, qqT = 0.0f, kkT = 0.0f;
+#pragma unroll
+        for (int j = 0; j < GDN_KS; j++) {
+            kvT = kvT + pkv[buf][j][col];
+            qoT = qoT + pqo[buf][j][col];
+            kqT = kqT + psc[buf][j][0];
+            qqT = qqT + psc[buf][j][1];
+            kkT = kkT + psc[buf][j][2];
+        }
+        const float rq = 1.0f / sqrtf(qqT + 1e-6f), rk = 1.0f / sqrtf(kkT + 1e-6f);
+        const float delta = (row[2 * lg.keyDim + h * lg.Dv + vvc] - kvT * rk) * beta;
+#pragma unroll
+        for (int r = 0; r < ROWS; r++) s[r] = s[r] + (kx[r] * rk) * delta;
+        if (kg == 0 && live) core[(size_t)m * lg.valueDim + h * lg.Dv + vv] = (qoT * rq + delta * (kqT * rq * rk)) * q_scale;
+    }
+    if (live) {
+#pragma unroll
+        for (int i = 0; i < ROWS; i++) S[(size_t)(k0 + i) * lg.Dv + vv] = s[i];
+    }
+}
+
+void launch_gdn(hipStream_t st, const float* lraw, int njobs, const JobDev* jobs, const float* gp, const LinGeom& lg,
+                float* state, float* core) {
+    if (njobs <= 0) return;
+    const dim3 grid((lg.Dv + GDN_TV - 1) / GDN_TV, lg.nV, njobs), blk(GDN_KS * GDN_TV);
+    switch (lg.Dk) {
+        case 16: hipLaunchKernelGGL(k_gdn<16>, grid, blk, 0, st, lraw, jobs, gp, lg, state, core); break;
+        case 32: hipLaunchKernelGGL(k_gdn<32>, grid, blk, 0, st, lraw, jobs, gp, lg, state, core); break;
+        case 64: hipLaunchKernelGGL(k_gdn<64>, grid, blk, 0, st, lraw, jobs, gp, lg, state, core); break;
+        default: hipLaunchKernelGGL(k_gdn<128>, grid, blk, 0, st, lraw, jobs, gp, lg, state, core); break;
+    }
+    CHECK_LAUNCH();
+}
+
+// RMSNormGated (model.js:523-524: rmsnorm over each value head's Dv values
+// with gated_norm, then silu_mul(z, normed)) into the out_proj operand. One
+// wave per (row, value head), 8 columns a lane.
+__global__ __launch_bounds__(256) void k_lin_norm(const float* __restrict__ core, const float* __restrict__ lraw,
+                                                  const float* __restrict__ gnorm, float eps, int M, LinGeom lg,
+                                                  int KU, uint4* __restrict__ Xp) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int h = blockIdx.x * 4 + wave, m = blockIdx.y;
+    if (h >= lg.nV || m >= M) return;
+    const int d0 = 8 * lane;
+    const bool act = d0 < lg.Dv;
+    float v[8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        v[j] = act ? core[(size_t)m * lg.valueDim + h * lg.Dv + d0 + j] : 0.0f;
+        ss += v[j] * v[j];
+    }
+    ss = wave_sum(ss);
+    if (!act) return;
+    const float scale = 1.0f / sqrtf(ss / (float)lg.Dv + eps);
+    const float* z = lraw + (size_t)m * lg.W + lg.convDim + h * lg.Dv + d0;
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float y = v[j] * scale * gnorm[d0 + j];
+        const float sg = 1.0f / (1.0f + expf(-z[j]));
+        o[j] = z[j] * sg * y;
+    }
+    write_hilo(Xp, m, (h * lg.Dv + d0) >> 3, KU, o);
+}
+
+void launch_lin_norm(hipStream_t st, const float* core, const float* lraw, const float* gnorm, float eps, int M,
+                     const LinGeom& lg, int KU, uint4* Xp) {
+    if (M <= 0) return;
+    hipLaunchKernelGGL(k_lin_norm, dim3((lg.nV + 3) / 4, M), dim3(256), 0, st, core, lraw, gnorm, eps, M, lg, KU, Xp);
     CHECK_LAUNCH();
 }
 
@@ -1230,7 +1463,8 @@ constexpr int COMBINE_CMAX = 512, COMBINE_SPLIT = 4;
 __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict__ jobs, const float* __restrict__ part,
                                                        KVGeom g, int nH, int group, int KU, uint4* __restrict__ Xp,
                                                        float* __restrict__ ctx_out,
-                                                       const int32_t* __restrict__ wg_job) {
+                                                       const int32_t* __restrict__ wg_job,
+                                                       const float* __restrict__ gate) {
     __shared__ float wgt[16][COMBINE_CMAX];
     __shared__ float Ls[16];
     __shared__ float4 red[COMBINE_SPLIT - 1][256][2];
@@ -1303,6 +1537,14 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
     const int i = rho / group, gi = rho % group;
     const int r = jb.row0 + i;
     const int k = (kvh * group + gi) * D + d0;
+    if (gate) {
+        // sigmoid_mul (kernels.js:1822-1839): s = 1/(1+exp(-gate)), s*a
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float sg = 1.0f / (1.0f + expf(-gate[(size_t)r * nH * D + k + j]));
+            v[j] = sg * v[j];
+        }
+    }
     if (ctx_out) {
 #pragma unroll
         for (int j = 0; j < 8; j++) ctx_out[(size_t)r * nH * D + k + j] = v[j];
@@ -1311,10 +1553,10 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
 }
 
 void launch_attn_combine(hipStream_t st, const JobDev* jobs, const float* part, const KVGeom& g, int nH, int group,
-                         int KU, uint4* Xp, float* ctx_out, const int32_t* wg_job, int nwg) {
+                         int KU, uint4* Xp, float* ctx_out, const int32_t* wg_job, int nwg, const float* gate) {
     if (nwg <= 0) return;
     hipLaunchKernelGGL(k_attn_combine, dim3(nwg), dim3(1024), 0, st, jobs, part, g, nH, group, KU, Xp, ctx_out,
-                       wg_job);
+                       wg_job, gate);
     CHECK_LAUNCH();
 }
 

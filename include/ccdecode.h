@@ -54,7 +54,21 @@ typedef struct cc_dims {
     int32_t rope_scaling;   /* 0 none, 1 llama3 (kernels.js:1998-2014) */
     double rs_factor, rs_low_freq, rs_high_freq, rs_orig_max_pos;
     int32_t tied;           /* LM head reads the embedding table */
+    /* Hybrid (Qwen3.5-architecture) checkpoints — dimsFromManifest,
+     * web/model/loader.js:146-201. rot_dim: RoPE width (partial rotary,
+     * kernels.js:1080-1129); 0 means head_dim. hybrid != 0: full_attention
+     * blocks also carry attn_gate, q_norm and k_norm (loader.js:543-565), and
+     * n_heads*head_dim may differ from hidden. layer_kinds: n_layer entries,
+     * CC_FULL_ATTENTION or CC_LINEAR_ATTENTION (NULL: every block full; the
+     * array is copied by cc_create). lin_*: Gated DeltaNet's key heads, value
+     * heads, key and value head widths, conv width (linear_num_key_heads ..
+     * linear_conv_kernel_dim). */
+    int32_t rot_dim;
+    int32_t hybrid;
+    const uint8_t* layer_kinds;
+    int32_t lin_nk, lin_nv, lin_dk, lin_dv, lin_conv;
 } cc_dims;
+enum { CC_FULL_ATTENTION = 0, CC_LINEAR_ATTENTION = 1 };
 
 /* Runner options (web/model/stage.js:107-110). lo/hi: the position range
  * held; n_max: context window; t_max: the most rows one pass carries; slots:
@@ -77,7 +91,18 @@ typedef struct cc_ctx cc_ctx;
  * model-level tensors. */
 enum {
     CC_T_Q = 0, CC_T_K = 1, CC_T_V = 2, CC_T_O = 3, CC_T_GATE = 4, CC_T_UP = 5, CC_T_DOWN = 6,
-    CC_T_LN1 = 7, CC_T_LN2 = 8, CC_T_WTE = 9, CC_T_NORM = 10, CC_T_LM_HEAD = 11
+    CC_T_LN1 = 7, CC_T_LN2 = 8, CC_T_WTE = 9, CC_T_NORM = 10, CC_T_LM_HEAD = 11,
+    /* a hybrid checkpoint's full_attention extras (loader.js:543-565):
+     * attn_gate q8 [n_heads*head_dim, hidden]; q_norm, k_norm f32 [head_dim] */
+    CC_T_ATTN_GATE = 12, CC_T_Q_NORM = 13, CC_T_K_NORM = 14,
+    /* linear_attention blocks (loader.js:567-590, tools/convert_hf.py:188-219):
+     * in_proj_q/k q8 [keyDim, hidden], in_proj_v/z q8 [valueDim, hidden],
+     * in_proj_b/a q8 [nV, hidden], conv1d_q/k f32 [keyDim, conv],
+     * conv1d_v f32 [valueDim, conv], gate_params f32 [2*nV] (A_log, then
+     * dt_bias), gated_norm f32 [Dv], out_proj q8 [hidden, valueDim] */
+    CC_T_IN_Q = 15, CC_T_IN_K = 16, CC_T_IN_V = 17, CC_T_IN_Z = 18, CC_T_IN_B = 19, CC_T_IN_A = 20,
+    CC_T_CONV_Q = 21, CC_T_CONV_K = 22, CC_T_CONV_V = 23, CC_T_GATE_PARAMS = 24, CC_T_GATED_NORM = 25,
+    CC_T_OUT_PROJ = 26
 };
 enum { CC_SCALES_F16 = 0, CC_SCALES_F32 = 1 };
 
@@ -87,7 +112,8 @@ void cc_destroy(cc_ctx* ctx);
 const char* cc_last_error(const cc_ctx* ctx);
 
 /* uploadQ8(device, int8Bytes, scales, group) — web/model/kernels.js:122-126;
- * norms (tensor LN1/LN2/NORM) are f32 `data` with n = hidden and no scales.
+ * norms (tensor LN1/LN2/NORM) are f32 `data` with n = hidden and no scales,
+ * and so are the hybrid f32 tensors (Q_NORM .. GATED_NORM, n = their size).
  * q8 tensors: `data` int8 [N, K] row-major, `scales` [N, ceil(K/group)] as
  * f16 bits or f32 (rounded to the device's f16 scale). `group` is any
  * multiple of 32 (the reference's converter writes 64,

@@ -167,8 +167,9 @@ def linear_core(lin, lw, state, q, k, v, a, b):
 
 
 def linear_block(d, lw, x, segs, states, matmul, rms_eps):
-    """model.js:472-527 linearBlockSegs (no speculation): x [T, H] updated in
-    place through attention and the SwiGLU MLP. `matmul(h, name)` gives the
+    """model.js:472-526 linearBlockSegs (no speculation), its attention half:
+    x [T, H] gets out_proj's rows added in place (the SwiGLU MLP and the
+    f16 round follow as in every block). `matmul(h, name)` gives the
     projection of rows h by weight `name`; `states[s]` is segment s's
     LinearState."""
     lin = lin_dims(d)
@@ -191,3 +192,77 @@ def qk_norm_rope(q, k, qn, kn, nH, nKV, D, eps):
     qo = L.rmsnorm(np.ascontiguousarray(q.reshape(T * nH, D), F32), qn, eps).reshape(T, nH * D)
     ko = L.rmsnorm(np.ascontiguousarray(k.reshape(T * nKV, D), F32), kn, eps).reshape(T, nKV * D)
     return np.ascontiguousarray(qo), np.ascontiguousarray(ko)
+
+
+def full_block_extras(model, layer, lw, x, segs):
+    """fullBlockSegs (model.js:368-410) on a hybrid checkpoint: attn_gate,
+    q_norm / k_norm before RoPE, the output gate before o_proj."""
+    d, g = model.d, model.group
+    nH, nKV, D = d["n_heads"], d["n_kv_heads"], d["head_dim"]
+    h = L.rmsnorm(x, lw["ln1"], d["rms_eps"])
+    q = L.matmul_q8(h, *lw["q"], group=g)
+    k = L.matmul_q8(h, *lw["k"], group=g)
+    v = L.matmul_q8(h, *lw["v"], group=g)
+    gate = L.matmul_q8(h, *lw["attn_gate"], group=g)
+    qn, kn = qk_norm_rope(q, k, lw["q_norm"], lw["k_norm"], nH, nKV, D, d["rms_eps"])
+    merged = np.empty_like(q)
+    for s in segs:
+        a, b = s["row"], s["row"] + s["n"]
+        merged[a:b] = model.attend(layer, s["slot"], qn[a:b], kn[a:b], v[a:b], s["past"])
+    attn = L.matmul_q8(sigmoid_mul(gate, merged), *lw["o"], group=g)
+    L.add_inplace(x, attn)
+
+
+class HybridModel:
+    """The oracle pass over a hybrid model: model.js:619-624 blockSegs picks
+    fullBlockSegs or linearBlockSegs per block. Wraps oracle.model.Model (the
+    paged KV pool, attention, embedding and head) and keeps one LinearState
+    per (session slot, linear block), started from zero by a job at position
+    0 (a new session, model.js:46-58)."""
+
+    def __init__(self, d, n_slots, max_pages):
+        from . import model as Mo
+
+        self.d = d
+        self.base = Mo.Model(d, n_slots=n_slots, max_pages=max_pages)
+        self.base.block = self.block
+        self.lin = lin_dims(d) if d.get("lin_nk") else None
+        self.states = {}
+
+    @property
+    def w(self):
+        return self.base.w
+
+    @w.setter
+    def w(self, value):
+        self.base.w = value
+
+    def state(self, slot, layer, past):
+        key = (slot, layer)
+        if past == 0 or key not in self.states:
+            self.states[key] = LinearState(self.lin)
+        return self.states[key]
+
+    def _ffn(self, lw, x):
+        d, g = self.d, self.base.group
+        h = L.rmsnorm(x, lw["ln2"], d["rms_eps"])
+        act = L.silu_mul(L.matmul_q8(h, *lw["gate"], group=g), L.matmul_q8(h, *lw["up"], group=g))
+        L.add_inplace(x, L.matmul_q8(act, *lw["down"], group=g))
+        L.lib().orc_round_f16(L._p(x), x.size)
+
+    def block(self, layer, x, segs):
+        lw = self.w["layers"][layer]
+        if lw.get("kind") == "linear":
+            states = [self.state(s["slot"], layer, s["past"]) for s in segs]
+            g = self.base.group
+
+            def mm(h, name):
+                return L.matmul_q8(h, *lw[name], group=g)
+            linear_block(self.d, lw, x, segs, states, mm, self.d["rms_eps"])
+        else:
+            full_block_extras(self.base, layer, lw, x, segs)
+        self._ffn(lw, x)
+        return x
+
+    def pass_(self, jobs, **kw):
+        return self.base.pass_(jobs, **kw)

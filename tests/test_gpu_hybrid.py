@@ -1,0 +1,121 @@
+"""Hybrid (Qwen3.5-architecture) models through cc_step against the oracle's
+HybridModel on identical weights (tests/hybrid_weights.py): Gated DeltaNet
+blocks with each session's recurrent state and conv ring carried across
+passes (web/model/model.js:418-527), full-attention blocks with q_norm /
+k_norm, partial rotary and the output gate (:368-410), in packed ragged
+batches; a session restarted at position 0 starts from a zero state."""
+import numpy as np
+import pytest
+
+import hybrid_weights as HW
+from oracle import hybrid as Hy
+
+pytestmark = pytest.mark.gpu
+SEED = 11
+
+
+def _ids(rng, n, vocab):
+    return rng.integers(0, vocab, size=n).astype(np.int32)
+
+
+def _check(got_vals, got_ids, want, ctx):
+    """Whole logits rows within 2e-3 of the rows' largest magnitude; greedy
+    ids equal unless the oracle's top-2 margin is below that."""
+    logits = np.concatenate([w["logits"] for w in want])
+    full = ctx.read_logits(logits.shape[0])
+    tol = max(1e-2, 2e-3 * np.abs(logits).max())
+    err = np.abs(full - logits).max()
+    assert err <= tol, (err, tol)
+    for r in range(logits.shape[0]):
+        order = np.argsort(-logits[r], kind="stable")
+        if logits[r, order[0]] - logits[r, order[1]] > tol:
+            assert got_ids[r, 0] == order[0], (r, got_ids[r, 0], order[0])
+    return logits
+
+
+def _pair(d, slots=3, n_max=512, t_max=64):
+    from chattorrent_amd.ccdecode import Context
+    c = Context(d, n_max=n_max, t_max=t_max, slots=slots)
+    om = Hy.HybridModel(d, n_slots=slots, max_pages=-(-n_max // 64))
+    om.w = HW.make(d, SEED)
+    HW.upload(c, om.w, d)
+    return c, om
+
+
+@pytest.mark.parametrize("cfg", ["spike", "wide"])
+def test_hybrid_passes_match_oracle(gpu, cfg):
+    """Prefill of two sessions, decode steps fed back greedily, a 3-row verify
+    beside a decode, then a new session in a used slot (state reset)."""
+    d = HW.SPIKE if cfg == "spike" else HW.WIDE
+    c, om = _pair(d)
+    rng = np.random.default_rng(3)
+    V = d["vocab"]
+    try:
+        jobs = [dict(slot=0, past=0, n=12, ids=_ids(rng, 12, V), sampled=1, topk=4),
+                dict(slot=1, past=0, n=5, ids=_ids(rng, 5, V), sampled=1, topk=4)]
+        pasts = [12, 5]
+        vals, ids = c.step(jobs, topk=4)
+        _check(vals, ids, om.pass_(jobs), c)
+        nxt = [int(ids[0, 0]), int(ids[1, 0])]
+        for step in range(4):
+            jobs = [dict(slot=s, past=pasts[s], n=1, ids=np.array([nxt[s]], np.int32), sampled=1, topk=4)
+                    for s in (0, 1)]
+            vals, ids = c.step(jobs, topk=4)
+            logits = _check(vals, ids, om.pass_(jobs), c)
+            nxt = [int(np.argmax(logits[0])), int(np.argmax(logits[1]))]
+            pasts = [pasts[0] + 1, pasts[1] + 1]
+        # a verify of 3 rows on session 0 beside a decode row on session 1
+        jobs = [dict(slot=0, past=pasts[0], n=3, ids=_ids(rng, 3, V), sampled=3, topk=4),
+                dict(slot=1, past=pasts[1], n=1, ids=np.array([nxt[1]], np.int32), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        _check(vals, ids, om.pass_(jobs), c)
+        # slot 1 taken by a new session: its pages go back, it starts at 0
+        c.release(1)
+        om.base.pool.release(om.base.frames[1])
+        jobs = [dict(slot=1, past=0, n=7, ids=_ids(rng, 7, V), sampled=1, topk=4),
+                dict(slot=0, past=pasts[0] + 3, n=1, ids=np.array([nxt[0]], np.int32), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        _check(vals, ids, om.pass_(jobs), c)
+    finally:
+        c.close()
+
+
+def test_hybrid_state_carries_across_passes_bitwise(gpu):
+    """A prompt in one pass, in two and in three gives the last row's logits
+    bit for bit: the recurrent state and the conv ring are stored as f32
+    between passes and each token runs the same arithmetic."""
+    d = HW.SPIKE
+    rng = np.random.default_rng(9)
+    prompt = _ids(rng, 12, d["vocab"])
+    got = []
+    for cuts in ([12], [5, 7], [5, 1, 6], [1, 1, 1, 9]):
+        c, _ = _pair(d, slots=1)
+        try:
+            past = 0
+            for n in cuts:
+                job = dict(slot=0, past=past, n=n, ids=prompt[past:past + n], sampled=1, topk=2)
+                c.step([job], topk=2)
+                past += n
+            got.append(c.read_logits(1).copy())
+        finally:
+            c.close()
+    for g in got[1:]:
+        assert np.array_equal(g.view(np.uint32), got[0].view(np.uint32))
+
+
+def test_hybrid_batch_mates_do_not_change_bits(gpu):
+    """A session's logits do not depend on the other sessions packed with it."""
+    d = HW.WIDE
+    rng = np.random.default_rng(4)
+    p0, p1 = _ids(rng, 9, d["vocab"]), _ids(rng, 20, d["vocab"])
+    c, _ = _pair(d)
+    try:
+        c.step([dict(slot=0, past=0, n=9, ids=p0, sampled=1, topk=2)], topk=2)
+        alone = c.read_logits(1).copy()
+        c.release(0)
+        c.step([dict(slot=1, past=0, n=20, ids=p1, sampled=1, topk=2),
+                dict(slot=0, past=0, n=9, ids=p0, sampled=1, topk=2)], topk=2)
+        both = c.read_logits(2)
+        assert np.array_equal(both[1].view(np.uint32), alone[0].view(np.uint32))
+    finally:
+        c.close()
