@@ -47,7 +47,8 @@ class Opts(C.Structure):
 
 class Job(C.Structure):
     _fields_ = [("slot", C.c_int32), ("past", C.c_int32), ("n", C.c_int32), ("sampled", C.c_int32),
-                ("ids", C.POINTER(C.c_int32)), ("hidden", C.POINTER(C.c_uint16))]
+                ("ids", C.POINTER(C.c_int32)), ("hidden", C.POINTER(C.c_uint16)), ("snap", C.c_int32),
+                ("rollback", C.c_int32), ("keep", C.c_int32)]
 
 
 class Stats(C.Structure):
@@ -252,7 +253,7 @@ class Context:
     # --- the pass -----------------------------------------------------------------
     def step(self, jobs, at=0, to=None, topk=1):
         """jobs: dicts with slot, past, n, sampled and ids (or hidden f16 bits
-        [n, H]). Returns (vals [S, topk], ids [S, topk]) at the head, else the
+        [n, H]), optionally snap (a verify) and keep (a rollback). Returns (vals [S, topk], ids [S, topk]) at the head, else the
         f16 bits of every row [T, H]. Raises CCError; `.statuses` holds the
         per-job statuses."""
         positions = self.d["n_layer"] + 2
@@ -271,6 +272,11 @@ class Context:
                 a = np.ascontiguousarray(j["hidden"], np.uint16)
                 keep.append(a)
                 arr[i].hidden = a.ctypes.data_as(C.POINTER(C.c_uint16))
+            # speculation through linear_attention blocks: `snap` marks a
+            # verify, `keep` (not None) rolls back to before the last verify
+            arr[i].snap = 1 if j.get("snap") else 0
+            if j.get("keep") is not None:
+                arr[i].rollback, arr[i].keep = 1, int(j["keep"])
             T += j["n"]
             S += arr[i].sampled
         status = np.zeros(len(jobs), np.int32)

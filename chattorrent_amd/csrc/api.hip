@@ -62,6 +62,11 @@ struct cc_ctx {
     float* lcore = nullptr;        // [t_max][valueDim] recurrence output
     uint4* xp_v = nullptr;         // operand for K = valueDim
     float* gbuf = nullptr;         // [t_max][qdim] output-gate values
+    float* lrep = nullptr;         // [max_jobs][LIN_SPEC_ROWS][lg.lrep_w] rows a rollback re-runs
+    bool any_linear = false;
+    // per session: its last job here was a verify from spec_base of spec_n rows
+    std::vector<int> spec_base, spec_n;
+    std::vector<int> fed;          // per session: rows its recurrent blocks hold
     std::vector<Layer> layers;
     QTensor wte, lm_head;
     float* norm = nullptr;
@@ -397,7 +402,11 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
             lg.W = lg.convDim + lg.valueDim + 2 * lg.nV;
             lg.N = 2 * lg.keyDim + 2 * lg.valueDim + 2 * lg.nVp;
             lg.hist_off = (size_t)lg.nV * lg.Dk * lg.Dv;
-            lg.sstride = lg.hist_off + (size_t)(LIN_CONV_K - 1) * lg.convDim;
+            lg.blk = lg.hist_off + (size_t)(LIN_CONV_K - 1) * lg.convDim;
+            lg.rep_w = 2 * lg.convDim + 2 * lg.nV;
+            lg.lrep_w = lg.convDim + 2 * lg.nV;
+            lg.rep_off = 2 * lg.blk;
+            lg.sstride = lg.rep_off + (size_t)LIN_SPEC_ROWS * lg.rep_w;
         }
         const int positions = d.n_layer + 2;
         ctx->embed = o.lo == 0;
@@ -493,7 +502,12 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
             HIPCHK(dalloc(ctx, &ctx->xp_v, xp_bytes(lg.valueDim), &ctx->scratch_bytes));
             HIPCHK(dalloc(ctx, &ctx->lraw, (size_t)T * lg.W * 4, &ctx->scratch_bytes));
             HIPCHK(dalloc(ctx, &ctx->lcore, (size_t)T * lg.valueDim * 4, &ctx->scratch_bytes));
+            HIPCHK(dalloc(ctx, &ctx->lrep, (size_t)o.max_jobs * LIN_SPEC_ROWS * lg.lrep_w * 4, &ctx->scratch_bytes));
         }
+        ctx->any_linear = any_linear;
+        ctx->spec_base.assign(o.sessions, 0);
+        ctx->spec_n.assign(o.sessions, -1);
+        ctx->fed.assign(o.sessions, 0);
         if (ctx->hybrid) HIPCHK(dalloc(ctx, &ctx->gbuf, (size_t)T * nH * D * 4, &ctx->scratch_bytes));
         size_t pf = 16;
         for (const Layer& L : ctx->layers)
@@ -715,6 +729,8 @@ cc_status cc_release(cc_ctx* ctx, int32_t slot) {
     launch_release_pages(ctx->stream, slot, n, ctx->free_stack, ctx->top, ctx->page_table, ctx->max_pages);
     ctx->top += n;
     ctx->owned[slot] = 0;
+    ctx->spec_n[slot] = -1;
+    ctx->fed[slot] = 0;
     HIPCHK(hipStreamSynchronize(ctx->stream));
     return CC_OK;
 }
@@ -849,6 +865,8 @@ static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, 
         jd.n = jobs[j].n;
         jd.row0 = row;
         jd.mtq = ceil_div(jd.n * ctx->group, 16);
+        jd.snap = jobs[j].snap ? 1 : 0;
+        jd.keep = jobs[j].rollback ? jobs[j].keep : -1;
         jd.qp_off = (int32_t)qp;
         qp += (size_t)ctx->geom.nKV * jd.mtq * ng * 128;
         const int T_act = jd.past + jd.n;
@@ -928,8 +946,8 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
             // recurrence on each session's state, gated norm, out_proj
             const LinGeom& lg = ctx->lg;
             launch_gemm(st, L.lin, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-            launch_lin_conv(st, ctx->part, L.lin.P, T, njobs, djobs, rs, L.conv, lg, L.state, ctx->lraw);
-            launch_gdn(st, ctx->lraw, njobs, djobs, L.gp, lg, L.state, ctx->lcore);
+            launch_lin_conv(st, ctx->part, L.lin.P, T, njobs, djobs, rs, L.conv, lg, L.state, ctx->lraw, ctx->lrep);
+            launch_gdn(st, ctx->lraw, ctx->lrep, njobs, djobs, L.gp, lg, L.state, ctx->lcore);
             launch_lin_norm(st, ctx->lcore, ctx->lraw, L.gnorm, d.rms_eps, T, lg, L.out.KU, ctx->xp_v);
             launch_gemm(st, L.out, ctx->xp_v, ctx->mt_alloc, ctx->part, T, ctx->ncu);
             launch_resid_w(st, ctx->x, ctx->part, L.out.P, T, Mpad, H, 0, L.ln2, KUH, ctx->xp_h, ctx->ssp);
@@ -1064,6 +1082,24 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         }
         if (at_end && !(jb.sampled == 0 || jb.sampled == 1 || jb.sampled == jb.n))
             return bad(j, "sampled must be 0, 1 or n at the head");
+        if (ctx->any_linear) {
+            // A recurrent block cannot be rewound, only restarted (past 0) or
+            // rolled back to before its last verify (stage.js:1028-1090).
+            if (jb.snap && jb.n > LIN_SPEC_ROWS)
+                return bad(j, "a verify job has at most " + std::to_string(LIN_SPEC_ROWS) + " rows");
+            const int sb = ctx->spec_base[jb.slot], sn = ctx->spec_n[jb.slot];
+            if (jb.rollback && (sn < 0 || jb.keep < 0 || jb.keep > sn || jb.past != sb + jb.keep)) {
+                if (status) status[j] = CC_COLD;
+                return fail(ctx, CC_COLD, "session " + std::to_string(jb.slot) +
+                                              " has no replay data here to roll back to " + std::to_string(jb.past));
+            }
+            if (!jb.rollback && jb.past > 0 && jb.past != ctx->fed[jb.slot]) {
+                if (status) status[j] = CC_COLD;
+                return fail(ctx, CC_COLD, "session " + std::to_string(jb.slot) + " is no longer cached here (its " +
+                                              "recurrent blocks hold " + std::to_string(ctx->fed[jb.slot]) +
+                                              " rows, the job continues from " + std::to_string(jb.past) + ")");
+            }
+        }
         T += jb.n;
     }
     if (T > ctx->o.t_max) return bad(-1, "the pass has " + std::to_string(T) + " rows, above t_max");
@@ -1158,6 +1194,19 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
     prof_collect(ctx);
     ctx->passes++;
     ctx->rows += T;
+    if (b1 > b0) {
+        // what the recurrent blocks now hold, and the verify a rollback may return to
+        for (int j = 0; j < njobs; j++) {
+            const int sl = jobs[j].slot;
+            ctx->fed[sl] = jobs[j].past + jobs[j].n;
+            if (jobs[j].snap) {
+                ctx->spec_base[sl] = jobs[j].past;
+                ctx->spec_n[sl] = jobs[j].n;
+            } else {
+                ctx->spec_n[sl] = -1;
+            }
+        }
+    }
     if (head) {
         std::memcpy(top_vals, hout, (size_t)p.S * topk * 4);
         std::memcpy(top_ids, (uint8_t*)hout + (size_t)p.S * topk * 4, (size_t)p.S * topk * 4);

@@ -38,6 +38,8 @@ struct JobDev {
     int32_t qp_off;                // this job's Q operand base (uint4 units)
     int32_t mtq;                   // Q m-tiles (ceil(n*group/16))
     int32_t item0, nchunk;         // attention work items: item0 + kvh*nchunk + c
+    int32_t snap;                  // a verify: linear blocks snapshot their state
+    int32_t keep;                  // >= 0: roll back to the snapshot, re-run `keep` rows
 };
 
 struct AttnItem {
@@ -89,21 +91,29 @@ void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const 
 // the fused projection (planes of N = 2*keyDim + 2*valueDim + 2*nVp): q, k, v
 // (the conv channels, convDim = 2*keyDim + valueDim), z, b (nV, padded to
 // nVp), a (nV, padded). `lraw` rows [M][LinGeom::W] hold the conv outputs
-// (after SiLU), then z, b, a. A session's state block (stride `sstride`
-// floats, session `slot`): S [nV][Dk][Dv], then the conv ring [K-1][convDim].
+// (after SiLU), then z, b, a.
+// A session's state (stride `sstride` floats, session `slot`):
+//   block 0 (current) and block 1 (snapshot), `blk` floats each:
+//     S [nV][Dk][Dv], then the conv ring [K-1][convDim] at `hist_off`;
+//   at `rep_off`, a verify's rows [LIN_SPEC_ROWS][rep_w]: raw q|k|v
+//     (convDim), conv outputs (convDim), b (nV), a (nV).
+// `lrep` [jobs][LIN_SPEC_ROWS][lrep_w]: the rows a rollback re-runs, conv
+// outputs then b, a, copied out before a verify overwrites them.
+constexpr int LIN_SPEC_ROWS = 8;   // SPEC_COLS (web/split.js:273)
 struct LinGeom {
     int nK = 0, nV = 0, Dk = 0, Dv = 0, K4 = 4, group = 1;
     int keyDim = 0, valueDim = 0, convDim = 0, nVp = 0;
     int W = 0;          // convDim + valueDim + 2*nV
     int N = 0;          // fused projection rows
-    size_t sstride = 0; // floats per session
-    size_t hist_off = 0;
+    size_t blk = 0, hist_off = 0, rep_off = 0, sstride = 0;
+    int rep_w = 0, lrep_w = 0;
 };
 constexpr int LIN_CONV_K = 4;
 void launch_lin_conv(hipStream_t st, const float* part, int splits, int M, int njobs, const JobDev* jobs,
-                     const RowScale& rs, const float* conv, const LinGeom& lg, float* state, float* lraw);
-void launch_gdn(hipStream_t st, const float* lraw, int njobs, const JobDev* jobs, const float* gp,
-                const LinGeom& lg, float* state, float* core);
+                     const RowScale& rs, const float* conv, const LinGeom& lg, float* state, float* lraw,
+                     float* lrep);
+void launch_gdn(hipStream_t st, const float* lraw, const float* lrep, int njobs, const JobDev* jobs,
+                const float* gp, const LinGeom& lg, float* state, float* core);
 // RMSNormGated per (row, value head) with the gated_norm weight, times
 // silu(z), into the out_proj operand (K = valueDim).
 void launch_lin_norm(hipStream_t st, const float* core, const float* lraw, const float* gnorm, float eps,

@@ -1018,27 +1018,59 @@ __device__ static inline float plane_col(const float* part, int splits, int M, i
 // from the session's state first (zeros for a job at position 0, a new
 // session) and written back after the job's last row. Per row: acc = sum over
 // k of w[c][k] * x[t-(K-1)+k] in k order, out = acc * (1/(1+exp(-acc))).
+// Speculation (model.js:447-470): a rollback job starts from the snapshot's
+// ring, advances it through the kept rows' stored raw values and copies
+// their stored outputs (and b, a) to `lrep` for the recurrence; a verify
+// writes the ring it starts from to the snapshot and stores each row's raw
+// value and output. The thread that reads a stored row is the one that
+// overwrites it, so a rollback job that is also a verify is ordered.
 __global__ __launch_bounds__(256) void k_lin_conv(const float* __restrict__ part, int splits, int M,
                                                   const JobDev* __restrict__ jobs, RowScale rs,
                                                   const float* __restrict__ conv, LinGeom lg,
-                                                  float* __restrict__ state, float* __restrict__ lraw) {
+                                                  float* __restrict__ state, float* __restrict__ lraw,
+                                                  float* __restrict__ lrep) {
     constexpr int K = LIN_CONV_K;
     const int c = blockIdx.x * 256 + threadIdx.x;
     if (c >= lg.W) return;
-    const JobDev jb = jobs[blockIdx.y];
+    const int j = blockIdx.y;
+    const JobDev jb = jobs[j];
+    float* base = state + (size_t)jb.slot * lg.sstride;
+    float* rep = base + lg.rep_off;
+    float* lr = lrep + (size_t)j * LIN_SPEC_ROWS * lg.lrep_w;
+    const int keep = jb.keep > 0 ? jb.keep : 0;
     // plane column: q|k|v|z in place, b and a each padded to nVp rows
     const int col = c < lg.convDim + lg.valueDim + lg.nV ? c : c - lg.nV + lg.nVp;
     if (c >= lg.convDim) {
+        // z, b, a pass through; b and a also feed a rollback's and a verify's rows
+        const bool ba = c >= lg.convDim + lg.valueDim;
+        const int e = c - lg.convDim - lg.valueDim;   // b: [0, nV), a: [nV, 2nV)
+        if (ba)
+            for (int i = 0; i < keep; i++)
+                lr[(size_t)i * lg.lrep_w + lg.convDim + e] = rep[(size_t)i * lg.rep_w + 2 * lg.convDim + e];
         for (int i = 0; i < jb.n; i++) {
             const int m = jb.row0 + i;
-            lraw[(size_t)m * lg.W + c] = plane_col(part, splits, M, lg.N, m, col, row_scale(rs, m));
+            const float v = plane_col(part, splits, M, lg.N, m, col, row_scale(rs, m));
+            lraw[(size_t)m * lg.W + c] = v;
+            if (ba && jb.snap) rep[(size_t)i * lg.rep_w + 2 * lg.convDim + e] = v;
         }
         return;
     }
-    float* ring = state + (size_t)jb.slot * lg.sstride + lg.hist_off + c;   // [K-1][convDim]
+    float* cur = base + lg.hist_off + c;            // [K-1][convDim]
+    float* snap = base + lg.blk + lg.hist_off + c;
+    const float* src = jb.keep >= 0 ? snap : cur;
     float h[K - 1];
 #pragma unroll
-    for (int r = 0; r < K - 1; r++) h[r] = jb.past > 0 ? ring[(size_t)r * lg.convDim] : 0.0f;
+    for (int r = 0; r < K - 1; r++) h[r] = jb.past > 0 ? src[(size_t)r * lg.convDim] : 0.0f;
+    for (int i = 0; i < keep; i++) {
+        lr[(size_t)i * lg.lrep_w + c] = rep[(size_t)i * lg.rep_w + lg.convDim + c];
+#pragma unroll
+        for (int k = 0; k < K - 2; k++) h[k] = h[k + 1];
+        h[K - 2] = rep[(size_t)i * lg.rep_w + c];
+    }
+    if (jb.snap) {
+#pragma unroll
+        for (int r = 0; r < K - 1; r++) snap[(size_t)r * lg.convDim] = h[r];
+    }
     float w[K];
 #pragma unroll
     for (int k = 0; k < K; k++) w[k] = conv[(size_t)c * K + k];
@@ -1050,20 +1082,26 @@ __global__ __launch_bounds__(256) void k_lin_conv(const float* __restrict__ part
         for (int k = 0; k < K - 1; k++) acc = acc + w[k] * h[k];
         acc = acc + w[K - 1] * x;
         const float sg = 1.0f / (1.0f + expf(-acc));
-        lraw[(size_t)m * lg.W + c] = acc * sg;
+        const float out = acc * sg;
+        lraw[(size_t)m * lg.W + c] = out;
+        if (jb.snap) {
+            rep[(size_t)i * lg.rep_w + c] = x;
+            rep[(size_t)i * lg.rep_w + lg.convDim + c] = out;
+        }
 #pragma unroll
         for (int k = 0; k < K - 2; k++) h[k] = h[k + 1];
         h[K - 2] = x;
     }
 #pragma unroll
-    for (int r = 0; r < K - 1; r++) ring[(size_t)r * lg.convDim] = h[r];
+    for (int r = 0; r < K - 1; r++) cur[(size_t)r * lg.convDim] = h[r];
 }
 
 void launch_lin_conv(hipStream_t st, const float* part, int splits, int M, int njobs, const JobDev* jobs,
-                     const RowScale& rs, const float* conv, const LinGeom& lg, float* state, float* lraw) {
+                     const RowScale& rs, const float* conv, const LinGeom& lg, float* state, float* lraw,
+                     float* lrep) {
     if (njobs <= 0) return;
     hipLaunchKernelGGL(k_lin_conv, dim3((lg.W + 255) / 256, njobs), dim3(256), 0, st, part, splits, M, jobs, rs,
-                       conv, lg, state, lraw);
+                       conv, lg, state, lraw, lrep);
     CHECK_LAUNCH();
 }
 
@@ -1079,10 +1117,13 @@ void launch_lin_conv(hipStream_t st, const float* part, int splits, int M, int n
 // the sums of squares share the token's one reduction through LDS (double
 // buffered on token parity, one barrier a token), and the factors
 // 1/sqrt(sum x^2 + 1e-6) are applied after it; the state update uses the
-// normalised k. A job at position 0 starts from a zero state.
+// normalised k. A job at position 0 starts from a zero state. A rollback
+// job starts from the snapshot and first re-runs the kept rows (from `lrep`,
+// no output); a verify writes the state it starts from to the snapshot.
 constexpr int GDN_KS = 8, GDN_TV = 32;
 template <int DK>
-__global__ __launch_bounds__(GDN_KS * GDN_TV) void k_gdn(const float* __restrict__ lraw, const JobDev* __restrict__ jobs,
+__global__ __launch_bounds__(GDN_KS * GDN_TV) void k_gdn(const float* __restrict__ lraw, const float* __restrict__ lrep,
+                                                         const JobDev* __restrict__ jobs,
                                                          const float* __restrict__ gp, LinGeom lg,
                                                          float* __restrict__ state, float* __restrict__ core) {
     constexpr int ROWS = DK / GDN_KS;
@@ -1090,29 +1131,34 @@ __global__ __launch_bounds__(GDN_KS * GDN_TV) void k_gdn(const float* __restrict
     __shared__ float pqo[2][GDN_KS][GDN_TV];
     __shared__ float psc[2][GDN_KS][3];   // k.q, q.q, k.k per k-group
     const int h = blockIdx.y;
-    const JobDev jb = jobs[blockIdx.z];
+    const int j = blockIdx.z;
+    const JobDev jb = jobs[j];
     const int col = threadIdx.x % GDN_TV, kg = threadIdx.x / GDN_TV;
     const int vv = blockIdx.x * GDN_TV + col;
     const bool live = vv < lg.Dv;
     const int vvc = live ? vv : lg.Dv - 1;   // out-of-range columns read a real one and discard it
     const int k0 = kg * ROWS;
     const int kh = h / lg.group;
-    float* S = state + (size_t)jb.slot * lg.sstride + (size_t)h * DK * lg.Dv;
+    float* base = state + (size_t)jb.slot * lg.sstride + (size_t)h * DK * lg.Dv;
+    float* S = base;                // current
+    float* Ssnap = base + lg.blk;   // snapshot
+    const float* src = jb.keep >= 0 ? Ssnap : S;
     float s[ROWS];
 #pragma unroll
-    for (int i = 0; i < ROWS; i++) s[i] = (jb.past > 0 && live) ? S[(size_t)(k0 + i) * lg.Dv + vv] : 0.0f;
+    for (int i = 0; i < ROWS; i++) s[i] = (jb.past > 0 && live) ? src[(size_t)(k0 + i) * lg.Dv + vv] : 0.0f;
     const float A = expf(gp[h]), dtb = gp[lg.nV + h];
     const float q_scale = 1.0f / sqrtf((float)DK);
-    for (int i = 0; i < jb.n; i++) {
-        const int m = jb.row0 + i;
-        const float* row = lraw + (size_t)m * lg.W;
+    int t = 0;   // tokens so far: the LDS buffers alternate on its parity
+    // One token: q, k, v at their channel offsets in `row`, b and a at
+    // boff + h and boff + nV + h. Every thread reaches its one barrier.
+    auto token = [&](const float* row, int boff, float* out) {
         const float* qr = row + kh * DK;
         const float* kr = row + lg.keyDim + kh * DK;
-        const float a = row[lg.convDim + lg.valueDim + lg.nV + h] + dtb;
+        const float a = row[boff + lg.nV + h] + dtb;
         const float sp = a > 20.0f ? a + logf(1.0f + expf(-a)) : logf(1.0f + expf(a));
         const float g = expf(-A * sp);
-        const float beta = 1.0f / (1.0f + expf(-row[lg.convDim + lg.valueDim + h]));
-        const int buf = i & 1;
+        const float beta = 1.0f / (1.0f + expf(-row[boff + h]));
+        const int buf = t & 1;
         float kv = 0.0f, qo = 0.0f, kq = 0.0f, qq = 0.0f, kk = 0.0f;
         float kx[ROWS];
 #pragma unroll
@@ -1136,18 +1182,30 @@ __global__ __launch_bounds__(GDN_KS * GDN_TV) void k_gdn(const float* __restrict
         __syncthreads();
         float kvT = 0.0f, qoT = 0.0f, kqT = 0.0f, qqT = 0.0f, kkT = 0.0f;
 #pragma unroll
-        for (int j = 0; j < GDN_KS; j++) {
-            kvT = kvT + pkv[buf][j][col];
-            qoT = qoT + pqo[buf][j][col];
-            kqT = kqT + psc[buf][j][0];
-            qqT = qqT + psc[buf][j][1];
-            kkT = kkT + psc[buf][j][2];
+        for (int q = 0; q < GDN_KS; q++) {
+            kvT = kvT + pkv[buf][q][col];
+            qoT = qoT + pqo[buf][q][col];
+            kqT = kqT + psc[buf][q][0];
+            qqT = qqT + psc[buf][q][1];
+            kkT = kkT + psc[buf][q][2];
         }
         const float rq = 1.0f / sqrtf(qqT + 1e-6f), rk = 1.0f / sqrtf(kkT + 1e-6f);
         const float delta = (row[2 * lg.keyDim + h * lg.Dv + vvc] - kvT * rk) * beta;
 #pragma unroll
         for (int r = 0; r < ROWS; r++) s[r] = s[r] + (kx[r] * rk) * delta;
-        if (kg == 0 && live) core[(size_t)m * lg.valueDim + h * lg.Dv + vv] = (qoT * rq + delta * (kqT * rq * rk)) * q_scale;
+        if (out && kg == 0 && live) *out = (qoT * rq + delta * (kqT * rq * rk)) * q_scale;
+        t++;
+    };
+    // a rollback re-runs the kept rows of the session's last verify
+    const float* lr = lrep + (size_t)j * LIN_SPEC_ROWS * lg.lrep_w;
+    for (int i = 0; i < jb.keep; i++) token(lr + (size_t)i * lg.lrep_w, lg.convDim, nullptr);
+    if (jb.snap && live) {
+#pragma unroll
+        for (int i = 0; i < ROWS; i++) Ssnap[(size_t)(k0 + i) * lg.Dv + vv] = s[i];
+    }
+    for (int i = 0; i < jb.n; i++) {
+        const int m = jb.row0 + i;
+        token(lraw + (size_t)m * lg.W, lg.convDim + lg.valueDim, core + (size_t)m * lg.valueDim + h * lg.Dv + vv);
     }
     if (live) {
 #pragma unroll
@@ -1155,15 +1213,15 @@ __global__ __launch_bounds__(GDN_KS * GDN_TV) void k_gdn(const float* __restrict
     }
 }
 
-void launch_gdn(hipStream_t st, const float* lraw, int njobs, const JobDev* jobs, const float* gp, const LinGeom& lg,
-                float* state, float* core) {
+void launch_gdn(hipStream_t st, const float* lraw, const float* lrep, int njobs, const JobDev* jobs, const float* gp,
+                const LinGeom& lg, float* state, float* core) {
     if (njobs <= 0) return;
     const dim3 grid((lg.Dv + GDN_TV - 1) / GDN_TV, lg.nV, njobs), blk(GDN_KS * GDN_TV);
     switch (lg.Dk) {
-        case 16: hipLaunchKernelGGL(k_gdn<16>, grid, blk, 0, st, lraw, jobs, gp, lg, state, core); break;
-        case 32: hipLaunchKernelGGL(k_gdn<32>, grid, blk, 0, st, lraw, jobs, gp, lg, state, core); break;
-        case 64: hipLaunchKernelGGL(k_gdn<64>, grid, blk, 0, st, lraw, jobs, gp, lg, state, core); break;
-        default: hipLaunchKernelGGL(k_gdn<128>, grid, blk, 0, st, lraw, jobs, gp, lg, state, core); break;
+        case 16: hipLaunchKernelGGL(k_gdn<16>, grid, blk, 0, st, lraw, lrep, jobs, gp, lg, state, core); break;
+        case 32: hipLaunchKernelGGL(k_gdn<32>, grid, blk, 0, st, lraw, lrep, jobs, gp, lg, state, core); break;
+        case 64: hipLaunchKernelGGL(k_gdn<64>, grid, blk, 0, st, lraw, lrep, jobs, gp, lg, state, core); break;
+        default: hipLaunchKernelGGL(k_gdn<128>, grid, blk, 0, st, lraw, lrep, jobs, gp, lg, state, core); break;
     }
     CHECK_LAUNCH();
 }

@@ -138,6 +138,17 @@ typedef struct cc_job {
     int32_t sampled;
     const int32_t* ids;
     const uint16_t* hidden;
+    /* Speculative decoding through linear_attention blocks (stage.js:1248-1283,
+     * model.js:447-470 restoreSpec / snapSpec). snap != 0: a verify job
+     * (n <= 8 rows); its blocks keep the state it starts from and its rows'
+     * projections. rollback != 0: the session's last job here was a verify
+     * from `base`; this job continues at past = base + keep (0 <= keep <= that
+     * verify's n): the blocks go back to the verify's starting state and
+     * re-run its first `keep` rows before this job's own. Zero-initialised
+     * fields mean neither. */
+    int32_t snap;
+    int32_t rollback;
+    int32_t keep;
 } cc_job;
 
 /* Runner.#pass — web/model/stage.js:1314-1481. Runs positions [at, to) for

@@ -166,20 +166,25 @@ def linear_core(lin, lw, state, q, k, v, a, b):
     return out.reshape(T, lin["nV"] * lin["Dv"])
 
 
-def linear_block(d, lw, x, segs, states, matmul, rms_eps):
-    """model.js:472-526 linearBlockSegs (no speculation), its attention half:
-    x [T, H] gets out_proj's rows added in place (the SwiGLU MLP and the
-    f16 round follow as in every block). `matmul(h, name)` gives the
-    projection of rows h by weight `name`; `states[s]` is segment s's
-    LinearState."""
+def linear_block(d, lw, x, segs, states, matmul, rms_eps, spec=None):
+    """model.js:472-526 linearBlockSegs, its attention half: x [T, H] gets
+    out_proj's rows added in place (the SwiGLU MLP and the f16 round follow
+    as in every block). `matmul(h, name)` gives the projection of rows h by
+    weight `name`; `states[s]` is segment s's LinearState. `spec(s, st, rows)`
+    (optional) runs before segment s's recurrence with its projections
+    (q, k, v, a, b) and returns the state to use: restoreSpec / snapSpec
+    (model.js:447-470)."""
     lin = lin_dims(d)
     h = L.rmsnorm(x, lw["ln1"], rms_eps)
     q, k, v = matmul(h, "in_q"), matmul(h, "in_k"), matmul(h, "in_v")
     z, bb, aa = matmul(h, "in_z"), matmul(h, "in_b"), matmul(h, "in_a")
     core = np.zeros((x.shape[0], lin["valueDim"]), F32)
-    for s, st in zip(segs, states):
+    for i, (s, st) in enumerate(zip(segs, states)):
         r0, r1 = s["row"], s["row"] + s["n"]
-        core[r0:r1] = linear_core(lin, lw, st, q[r0:r1], k[r0:r1], v[r0:r1], aa[r0:r1], bb[r0:r1])
+        rows = (q[r0:r1], k[r0:r1], v[r0:r1], aa[r0:r1], bb[r0:r1])
+        if spec is not None:
+            st = spec(i, st, rows)
+        core[r0:r1] = linear_core(lin, lw, st, *rows)
     gated = gated_rmsnorm(core, lw["gated_norm"], z, rms_eps)
     L.add_inplace(x, matmul(gated, "out"))
     return x
@@ -228,6 +233,7 @@ class HybridModel:
         self.base.block = self.block
         self.lin = lin_dims(d) if d.get("lin_nk") else None
         self.states = {}
+        self.spec = {}   # (slot, layer) -> (state before the last verify, its projections)
 
     @property
     def w(self):
@@ -258,7 +264,24 @@ class HybridModel:
 
             def mm(h, name):
                 return L.matmul_q8(h, *lw[name], group=g)
-            linear_block(self.d, lw, x, segs, states, mm, self.d["rms_eps"])
+
+            def spec(i, st, rows):
+                # restoreSpec: the state from before the last verify, then its
+                # first `keep` rows again from their stored projections;
+                # snapSpec: a verify keeps the state it starts from and its rows
+                s = segs[i]
+                key = (s["slot"], layer)
+                if s.get("keep") is not None:
+                    snap, saved = self.spec[key]
+                    st = snap.copy()
+                    kk = s["keep"]
+                    if kk > 0:
+                        linear_core(self.lin, lw, st, *(r[:kk] for r in saved))
+                    self.states[key] = st
+                if s.get("snap"):
+                    self.spec[key] = (st.copy(), tuple(np.array(r) for r in rows))
+                return st
+            linear_block(self.d, lw, x, segs, states, mm, self.d["rms_eps"], spec)
         else:
             full_block_extras(self.base, layer, lw, x, segs)
         self._ffn(lw, x)

@@ -213,7 +213,8 @@ class Model:
             frame = self.frames[j["slot"]]
             if not self.pool.ensure(frame, j["past"] + j["n"]):
                 raise RuntimeError("the KV pool cannot fit the job")
-            segs.append({"slot": j["slot"], "past": j["past"], "n": j["n"], "row": row})
+            segs.append({"slot": j["slot"], "past": j["past"], "n": j["n"], "row": row,
+                         "snap": bool(j.get("snap")), "keep": j.get("keep")})
             row += j["n"]
         T = row
         if "ids" in jobs[0] and jobs[0]["ids"] is not None:

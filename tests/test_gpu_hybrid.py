@@ -119,3 +119,92 @@ def test_hybrid_batch_mates_do_not_change_bits(gpu):
         assert np.array_equal(both[1].view(np.uint32), alone[0].view(np.uint32))
     finally:
         c.close()
+
+
+def _run(c, jobs, topk=2):
+    c.step(jobs, topk=topk)
+    return c.read_logits(sum(j.get("sampled", 1) for j in jobs)).copy()
+
+
+@pytest.mark.parametrize("keep", [0, 2, 4])
+def test_hybrid_verify_rollback_matches_oracle(gpu, keep):
+    """A 4-row verify (snap) beside another session's decode, then the next
+    job rolls the linear blocks back to before the verify and re-runs its
+    first `keep` rows (stage.js:1248-1283, model.js:447-470); the following
+    decode continues from there. Every pass against the oracle."""
+    d = HW.SPIKE
+    c, om = _pair(d)
+    rng = np.random.default_rng(21)
+    V = d["vocab"]
+    try:
+        jobs = [dict(slot=0, past=0, n=12, ids=_ids(rng, 12, V), sampled=1, topk=4),
+                dict(slot=1, past=0, n=6, ids=_ids(rng, 6, V), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        _check(vals, ids, om.pass_(jobs), c)
+        jobs = [dict(slot=0, past=12, n=4, ids=_ids(rng, 4, V), sampled=4, topk=4, snap=True),
+                dict(slot=1, past=6, n=1, ids=_ids(rng, 1, V), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        _check(vals, ids, om.pass_(jobs), c)
+        jobs = [dict(slot=0, past=12 + keep, n=1, ids=_ids(rng, 1, V), sampled=1, topk=4, keep=keep),
+                dict(slot=1, past=7, n=1, ids=_ids(rng, 1, V), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        _check(vals, ids, om.pass_(jobs), c)
+        jobs = [dict(slot=0, past=13 + keep, n=1, ids=_ids(rng, 1, V), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        _check(vals, ids, om.pass_(jobs), c)
+    finally:
+        c.close()
+
+
+def test_hybrid_rollback_equals_plain_feed_bitwise(gpu):
+    """A verify of [t, d1, d2, d3] rolled back to keep 2, then token x, gives
+    the same logits bit for bit as feeding [t, d1] and then x plainly: the
+    recurrent state is replayed with the same arithmetic, and the rejected
+    rows' KV is overwritten or masked."""
+    d = HW.SPIKE
+    rng = np.random.default_rng(22)
+    V = d["vocab"]
+    prompt, ver, x = _ids(rng, 10, V), _ids(rng, 4, V), _ids(rng, 1, V)
+    c, _ = _pair(d, slots=1)
+    try:
+        _run(c, [dict(slot=0, past=0, n=10, ids=prompt, sampled=1)])
+        _run(c, [dict(slot=0, past=10, n=4, ids=ver, sampled=4, snap=True)])
+        spec = _run(c, [dict(slot=0, past=12, n=1, ids=x, sampled=1, keep=2)])
+    finally:
+        c.close()
+    c, _ = _pair(d, slots=1)
+    try:
+        _run(c, [dict(slot=0, past=0, n=10, ids=prompt, sampled=1)])
+        _run(c, [dict(slot=0, past=10, n=2, ids=ver[:2], sampled=1)])
+        plain = _run(c, [dict(slot=0, past=12, n=1, ids=x, sampled=1)])
+    finally:
+        c.close()
+    assert np.array_equal(spec.view(np.uint32), plain.view(np.uint32))
+
+
+def test_hybrid_refuses_what_it_cannot_replay(gpu):
+    """A rollback with no verify before it, one past the verify's rows, a
+    plain job that skips or rewinds rows, and a verify above 8 rows are
+    refused (cold / bad job) and change nothing."""
+    from chattorrent_amd.ccdecode import CC_COLD, CC_EARG, CCError
+    d = HW.SPIKE
+    rng = np.random.default_rng(23)
+    V = d["vocab"]
+    c, _ = _pair(d, slots=1, t_max=64)
+    try:
+        _run(c, [dict(slot=0, past=0, n=5, ids=_ids(rng, 5, V), sampled=1)])
+        for job, code in ((dict(slot=0, past=5, n=1, keep=0), CC_COLD),        # no verify to return to
+                          (dict(slot=0, past=7, n=1), CC_COLD),                # skips rows
+                          (dict(slot=0, past=3, n=1), CC_COLD),                # rewinds
+                          (dict(slot=0, past=5, n=9, snap=True), CC_EARG)):    # verify above 8 rows
+            job = dict(job, ids=_ids(rng, job["n"], V), sampled=1)
+            with pytest.raises(CCError) as e:
+                c.step([job], topk=2)
+            assert e.value.status == code, (job, e.value)
+        _run(c, [dict(slot=0, past=5, n=3, ids=_ids(rng, 3, V), sampled=3, snap=True)])
+        with pytest.raises(CCError) as e:   # keep beyond the verify's 3 rows
+            c.step([dict(slot=0, past=9, n=1, ids=_ids(rng, 1, V), sampled=1, keep=4)], topk=2)
+        assert e.value.status == CC_COLD
+        _run(c, [dict(slot=0, past=8, n=1, ids=_ids(rng, 1, V), sampled=1, keep=3)])
+    finally:
+        c.close()
