@@ -19,12 +19,15 @@ STATUS_NAMES = ["ok", "busy", "cold", "stale", "nospec", "bad-job", "pool-too-sm
 # a hybrid checkpoint's full_attention extras and linear_attention tensors
 (T_ATTN_GATE, T_Q_NORM, T_K_NORM, T_IN_Q, T_IN_K, T_IN_V, T_IN_Z, T_IN_B, T_IN_A, T_CONV_Q, T_CONV_K, T_CONV_V,
  T_GATE_PARAMS, T_GATED_NORM, T_OUT_PROJ) = range(12, 27)
+# the MTP draft head; its block's tensors are the block ids at LAYER_MTP
+(T_MTP_ENORM, T_MTP_HNORM, T_MTP_FC_E, T_MTP_FC_H, T_MTP_NORM, T_MTP_EMBED, T_MTP_HEAD) = range(27, 34)
+LAYER_MTP = -2
 FULL_ATTENTION, LINEAR_ATTENTION = 0, 1
 EXPORTS = [
     "cc_create", "cc_destroy", "cc_last_error", "cc_upload", "cc_fill_random", "cc_step", "cc_release",
     "cc_slot_pages", "cc_free_pages", "cc_fill_random_kv", "cc_read_kv", "cc_write_kv", "cc_read_pages",
     "cc_stats_get", "cc_op_matmul_q8", "cc_op_store_kv", "cc_op_round_f16", "cc_op_topk", "cc_op_rmsnorm",
-    "cc_op_attend", "cc_profile", "cc_profile_read", "cc_read_logits",
+    "cc_op_attend", "cc_profile", "cc_profile_read", "cc_read_logits", "cc_mtp_draft",
 ]
 
 
@@ -36,7 +39,7 @@ class Dims(C.Structure):
                 ("rs_high_freq", C.c_double), ("rs_orig_max_pos", C.c_double), ("tied", C.c_int32),
                 ("rot_dim", C.c_int32), ("hybrid", C.c_int32), ("layer_kinds", C.POINTER(C.c_uint8)),
                 ("lin_nk", C.c_int32), ("lin_nv", C.c_int32), ("lin_dk", C.c_int32), ("lin_dv", C.c_int32),
-                ("lin_conv", C.c_int32)]
+                ("lin_conv", C.c_int32), ("mtp_vocab", C.c_int32)]
 
 
 class Opts(C.Structure):
@@ -48,7 +51,7 @@ class Opts(C.Structure):
 class Job(C.Structure):
     _fields_ = [("slot", C.c_int32), ("past", C.c_int32), ("n", C.c_int32), ("sampled", C.c_int32),
                 ("ids", C.POINTER(C.c_int32)), ("hidden", C.POINTER(C.c_uint16)), ("snap", C.c_int32),
-                ("rollback", C.c_int32), ("keep", C.c_int32)]
+                ("rollback", C.c_int32), ("keep", C.c_int32), ("mtp", C.c_int32)]
 
 
 class Stats(C.Structure):
@@ -92,6 +95,7 @@ def load():
         "cc_op_rmsnorm": (i32, [P, P, P, i32, i32, P]),
         "cc_op_attend": (i32, [P, i32, i32, P, i32, i32, P]),
         "cc_read_logits": (i32, [P, i32, P]),
+        "cc_mtp_draft": (i32, [P, i32, i32, i32, i32, i32, P]),
         "cc_profile": (i32, [P, i32]),
         "cc_profile_read": (i32, [P, i32, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
     }
@@ -134,7 +138,8 @@ def make_dims(d):
                 rs_orig_max_pos=sc["original_max_position_embeddings"] if sc else 0.0,
                 tied=1 if d.get("tied", True) else 0, rot_dim=d.get("rot_dim", 0) or 0,
                 hybrid=1 if d.get("hybrid") else 0, lin_nk=d.get("lin_nk", 0), lin_nv=d.get("lin_nv", 0),
-                lin_dk=d.get("lin_dk", 0), lin_dv=d.get("lin_dv", 0), lin_conv=d.get("lin_conv", 0))
+                lin_dk=d.get("lin_dk", 0), lin_dv=d.get("lin_dv", 0), lin_conv=d.get("lin_conv", 0),
+                mtp_vocab=d.get("mtp_vocab", 0) or 0)
     kinds = layer_kinds(d)
     if kinds is not None:
         arr = (C.c_uint8 * len(kinds))(*kinds)
@@ -228,6 +233,13 @@ class Context:
     def free_pages(self):
         return self.lib.cc_free_pages(self.h)
 
+    def mtp_draft(self, slot, row, token, pos, k):
+        """cc_mtp_draft: keep row `row` of the last pass (-1: the kept one) and
+        chain `k` drafts after `token` at positions pos.. (uint32 [k])."""
+        out = np.zeros(max(k, 1), np.uint32)
+        self._chk(self.lib.cc_mtp_draft(self.h, slot, row, token, pos, k, _p(out)))
+        return out[:k]
+
     def release(self, slot):
         self._chk(self.lib.cc_release(self.h, slot))
 
@@ -275,6 +287,7 @@ class Context:
             # speculation through linear_attention blocks: `snap` marks a
             # verify, `keep` (not None) rolls back to before the last verify
             arr[i].snap = 1 if j.get("snap") else 0
+            arr[i].mtp = 1 if j.get("mtp") else 0
             if j.get("keep") is not None:
                 arr[i].rollback, arr[i].keep = 1, int(j["keep"])
             T += j["n"]

@@ -45,6 +45,8 @@ struct Layer {
 
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+constexpr int MTP_STEPS_MAX = 7;   // SPEC_COLS - 1 drafts (stage.js:303-304)
+
 }  // namespace
 
 struct cc_ctx {
@@ -67,6 +69,24 @@ struct cc_ctx {
     // per session: its last job here was a verify from spec_base of spec_n rows
     std::vector<int> spec_base, spec_n;
     std::vector<int> fed;          // per session: rows its recurrent blocks hold
+    // the MTP draft head (model.js:529-576), held with the LM head
+    bool mtp = false;
+    Layer mtpL;                    // its full-attention block, own KV pools
+    QTensor fc_e, fc_h, embed_draft, head_draft;
+    float* enorm = nullptr;
+    float* hnorm = nullptr;
+    float* mtp_norm = nullptr;
+    float* mtpH = nullptr;         // [sessions][H] the trunk row a session's next MTP row pairs with
+    float* mx = nullptr;           // [t_max][H] the MTP block's rows
+    float* mtp_in = nullptr;       // [t_max][H] the hidden rows paired with the tokens
+    float* mtp_e = nullptr;        // [t_max][H] draft embeddings
+    uint4* xp_e = nullptr;         // operands of enorm(e) and hnorm(h)
+    uint4* xp_hh = nullptr;
+    float* mtp_logits = nullptr;   // head_draft planes for one row
+    uint8_t* d_chain = nullptr;    // draft chain metadata (device) and its pinned staging
+    uint8_t* h_chain = nullptr;
+    size_t chain_step = 0;         // bytes per chain step
+    int last_T = 0;                // rows the last pass left in x
     std::vector<Layer> layers;
     QTensor wte, lm_head;
     float* norm = nullptr;
@@ -213,6 +233,7 @@ cc_status check_dims(cc_ctx* ctx, const cc_dims& d, const cc_opts& o) {
         }
     }
     if (any_linear && !hyb) return fail(ctx, CC_EARG, "linear_attention blocks need a hybrid checkpoint");
+    if (d.mtp_vocab < 0 || d.mtp_vocab > d.vocab) return fail(ctx, CC_EARG, "mtp_vocab must be 0..vocab");
     if (any_linear) {
         // loader.js:225-230, plus the Gated DeltaNet kernels' shapes
         if (d.lin_nk <= 0 || d.lin_nv <= 0 || d.lin_nv % d.lin_nk)
@@ -266,7 +287,7 @@ struct StepPlan {
 // Per-step metadata: jobs, items, row_job, plan, head_rows, combine
 // workgroups (job, kv head, m-tile), ids | hidden.
 struct MetaLayout {
-    size_t jobs, items, row_job, plan, head_rows, cwg, ids, hidden, total;
+    size_t jobs, items, row_job, plan, head_rows, cwg, ids, mtp_jobs, mtp_row_job, mtp_src, mtp_ids, hidden, total;
 };
 
 // (job, kv head, m-tile) triples a pass can hold.
@@ -286,6 +307,12 @@ MetaLayout meta_layout(const cc_ctx* ctx) {
     m.head_rows = take(4 * (size_t)t_max);
     m.cwg = take(12 * max_cwg_for(ctx));
     m.ids = take(4 * (size_t)t_max);
+    // the MTP fill's rows (the MTP jobs' rows, packed): jobs, row -> job,
+    // hidden-row source (x row, or -1 - slot for the session's kept row), ids
+    m.mtp_jobs = take(sizeof(JobDev) * max_jobs);
+    m.mtp_row_job = take(4 * (size_t)t_max);
+    m.mtp_src = take(4 * (size_t)t_max);
+    m.mtp_ids = take(4 * (size_t)t_max);
     m.hidden = take(2 * (size_t)t_max * H);
     m.total = at;
     return m;
@@ -341,6 +368,7 @@ void cc_destroy(cc_ctx* ctx) {
     for (void* p : ctx->allocs) hipFree(p);
     if (ctx->h_meta) hipHostFree(ctx->h_meta);
     if (ctx->h_out) hipHostFree(ctx->h_out);
+    if (ctx->h_chain) hipHostFree(ctx->h_chain);
     if (ctx->ev0) hipEventDestroy(ctx->ev0);
     if (ctx->ev1) hipEventDestroy(ctx->ev1);
     for (hipEvent_t e : ctx->pev) hipEventDestroy(e);
@@ -525,6 +553,51 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         // Attention partials: 16 rows of (D + 4) floats per item.
         ctx->apart_floats = ctx->items_cap * 16 * (size_t)(D + 4);
         HIPCHK(dalloc(ctx, &ctx->apart, ctx->apart_floats * 4, &ctx->scratch_bytes));
+        if (ctx->head && d.mtp_vocab > 0) {
+            // the MTP head (stage.js:273-289 attachMtp): its block's KV is laid
+            // out as a pool layer, addressed by each session's page table
+            ctx->mtp = true;
+            Layer& M = ctx->mtpL;
+            HIPCHK(alloc_q(ctx, M.qkv, (nH + 2 * nKV) * D + (ctx->hybrid ? nH * D : 0), H));
+            HIPCHK(alloc_q(ctx, M.o, H, nH * D));
+            HIPCHK(alloc_q(ctx, M.gu, 2 * F, H));
+            HIPCHK(alloc_q(ctx, M.down, H, F));
+            for (float** w : {&M.ln1, &M.ln2}) {
+                HIPCHK(dalloc(ctx, w, (size_t)H * 4, &ctx->weight_bytes));
+                launch_fill(ctx->stream, *w, H, 1.0f);
+            }
+            if (ctx->hybrid) {
+                for (float** w : {&M.qn, &M.kn}) {
+                    HIPCHK(dalloc(ctx, w, (size_t)D * 4, &ctx->weight_bytes));
+                    launch_fill(ctx->stream, *w, D, 1.0f);
+                }
+            }
+            HIPCHK(dalloc(ctx, &M.kpool, pool_bytes, &ctx->kv_bytes));
+            HIPCHK(dalloc(ctx, &M.vpool, pool_bytes, &ctx->kv_bytes));
+            HIPCHK(alloc_q(ctx, ctx->fc_e, H, H));
+            HIPCHK(alloc_q(ctx, ctx->fc_h, H, H));
+            HIPCHK(alloc_q(ctx, ctx->embed_draft, d.mtp_vocab, H));
+            HIPCHK(alloc_q(ctx, ctx->head_draft, d.mtp_vocab, H));
+            for (float** w : {&ctx->enorm, &ctx->hnorm, &ctx->mtp_norm}) {
+                HIPCHK(dalloc(ctx, w, (size_t)H * 4, &ctx->weight_bytes));
+                launch_fill(ctx->stream, *w, H, 1.0f);
+            }
+            HIPCHK(dalloc(ctx, &ctx->mtpH, (size_t)o.sessions * H * 4, &ctx->scratch_bytes));
+            for (float** b : {&ctx->mx, &ctx->mtp_in, &ctx->mtp_e})
+                HIPCHK(dalloc(ctx, b, (size_t)T * H * 4, &ctx->scratch_bytes));
+            HIPCHK(dalloc(ctx, &ctx->xp_e, xp_bytes(H), &ctx->scratch_bytes));
+            HIPCHK(dalloc(ctx, &ctx->xp_hh, xp_bytes(H), &ctx->scratch_bytes));
+            HIPCHK(dalloc(ctx, &ctx->mtp_logits, (size_t)ctx->head_draft.P * d.mtp_vocab * 4, &ctx->scratch_bytes));
+            // one region per draft step: a one-row job's plan
+            const size_t mtq1 = ceil_div(ctx->group, 16);
+            const size_t a256 = 255;
+            auto al = [&](size_t b) { return (b + a256) & ~a256; };
+            ctx->chain_step = al(sizeof(JobDev)) + al(sizeof(AttnItem) * nKV * mtq1 * ceil_div(ctx->max_pages, ctx->ppw)) +
+                              al(4) + al(12 * nKV * mtq1);
+            const size_t cb = 256 + MTP_STEPS_MAX * ctx->chain_step;
+            HIPCHK(dalloc(ctx, &ctx->d_chain, cb, &ctx->scratch_bytes));
+            HIPCHK(hipHostMalloc((void**)&ctx->h_chain, cb, hipHostMallocDefault));
+        }
         if (ctx->head) {
             ctx->head_planes = lx_planes(ceil_div(H, 64));
             HIPCHK(dalloc(ctx, &ctx->logits, (size_t)ctx->head_planes * T * d.vocab * 4, &ctx->scratch_bytes));
@@ -554,9 +627,28 @@ static QTensor* tensor_of(cc_ctx* ctx, int layer, int tensor, int* row_tile0, in
     const int H = d.hidden, F = d.ffn, D = d.head_dim, nH = d.n_heads, nKV = d.n_kv_heads;
     if (tensor == CC_T_WTE) { *row_tile0 = 0; *N = d.vocab; *K = H; return ctx->wte.codes ? &ctx->wte : nullptr; }
     if (tensor == CC_T_LM_HEAD) { *row_tile0 = 0; *N = d.vocab; *K = H; return ctx->lm_head.codes ? &ctx->lm_head : nullptr; }
-    const int li = layer - ctx->L0;
-    if (li < 0 || li >= (int)ctx->layers.size()) return nullptr;
-    Layer& L = ctx->layers[li];
+    if (tensor >= CC_T_MTP_FC_E && tensor <= CC_T_MTP_HEAD) {
+        if (!ctx->mtp) return nullptr;
+        *row_tile0 = 0;
+        *K = H;
+        *N = tensor == CC_T_MTP_FC_E || tensor == CC_T_MTP_FC_H ? H : d.mtp_vocab;
+        switch (tensor) {
+            case CC_T_MTP_FC_E: return &ctx->fc_e;
+            case CC_T_MTP_FC_H: return &ctx->fc_h;
+            case CC_T_MTP_EMBED: return &ctx->embed_draft;
+            case CC_T_MTP_HEAD: return &ctx->head_draft;
+        }
+        return nullptr;
+    }
+    Layer* Lp = nullptr;
+    if (layer == CC_LAYER_MTP) {
+        if (ctx->mtp) Lp = &ctx->mtpL;
+    } else {
+        const int li = layer - ctx->L0;
+        if (li >= 0 && li < (int)ctx->layers.size()) Lp = &ctx->layers[li];
+    }
+    if (!Lp) return nullptr;
+    Layer& L = *Lp;
     if (L.kind == CC_LINEAR_ATTENTION) {
         // fused in_proj rows: q | k | v | z | b (nVp) | a (nVp)
         const LinGeom& lg = ctx->lg;
@@ -596,15 +688,20 @@ cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data
     const cc_dims& d = ctx->d;
     const bool f32_tensor = tensor == CC_T_LN1 || tensor == CC_T_LN2 || tensor == CC_T_NORM ||
                             (tensor >= CC_T_Q_NORM && tensor <= CC_T_K_NORM) ||
-                            (tensor >= CC_T_CONV_Q && tensor <= CC_T_GATED_NORM);
+                            (tensor >= CC_T_CONV_Q && tensor <= CC_T_GATED_NORM) || tensor == CC_T_MTP_ENORM ||
+                            tensor == CC_T_MTP_HNORM || tensor == CC_T_MTP_NORM;
     if (f32_tensor) {
         float* dst = nullptr;
         size_t want = d.hidden;
         if (tensor == CC_T_NORM) dst = ctx->norm;
+        else if (tensor == CC_T_MTP_ENORM) dst = ctx->enorm;
+        else if (tensor == CC_T_MTP_HNORM) dst = ctx->hnorm;
+        else if (tensor == CC_T_MTP_NORM) dst = ctx->mtp_norm;
         else {
             const int li = layer - ctx->L0;
-            if (li < 0 || li >= (int)ctx->layers.size()) return fail(ctx, CC_EARG, "layer not held here");
-            Layer& L = ctx->layers[li];
+            const bool m = layer == CC_LAYER_MTP && ctx->mtp;
+            if (!m && (li < 0 || li >= (int)ctx->layers.size())) return fail(ctx, CC_EARG, "layer not held here");
+            Layer& L = m ? ctx->mtpL : ctx->layers[li];
             const LinGeom& lg = ctx->lg;
             switch (tensor) {
                 case CC_T_LN1: dst = L.ln1; break;
@@ -921,23 +1018,92 @@ static cc_status grow(cc_ctx* ctx, const StepPlan& p) {
 // residual (+ operand x*ln2 and the row's sum of squares), gate|up GEMM,
 // finish (row factor + SwiGLU), down GEMM, residual (+ round_f16 + the next
 // block's operand x*ln1 and sum of squares).
+// Device pointers of a pass's metadata, and its counts.
+struct PassMeta {
+    const JobDev* jobs = nullptr;
+    const AttnItem* items = nullptr;
+    const int32_t* row_job = nullptr;
+    const int32_t* cwg = nullptr;
+    int njobs = 0, nitems = 0, ncwg = 0;
+};
+
+static RowScale row_scale_of(const cc_ctx* ctx) {
+    RowScale rs;
+    rs.ssp = ctx->ssp;
+    rs.nsl = ceil_div(ctx->d.hidden / 4, RW_THREADS);
+    rs.H = ctx->d.hidden;
+    rs.eps = ctx->d.rms_eps;
+    return rs;
+}
+
+// fullBlockSegs's attention half (model.js:368-410) on rows x [T][H] whose
+// operand x*ln1 and sums of squares are in place: q|k|v (+ attn_gate) GEMM,
+// finish (row factor, q/k norm, RoPE, KV store, Q operand), attention,
+// combine (output gate, o_proj operand), o GEMM, residual with the operand
+// x*ln2 for the MLP.
+static void full_attn_half(cc_ctx* ctx, Layer& L, float* x, int T, int Mpad, const PassMeta& pm) {
+    const cc_dims& d = ctx->d;
+    hipStream_t st = ctx->stream;
+    const int H = d.hidden, nH = d.n_heads;
+    const RowScale rs = row_scale_of(ctx);
+    QkExtras ex;
+    if (ctx->hybrid) {
+        ex.qn = L.qn;
+        ex.kn = L.kn;
+        ex.eps = d.rms_eps;
+        ex.gate = ctx->gbuf;
+    }
+    launch_gemm(st, L.qkv, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
+    launch_fin_qkv(st, ctx->part, L.qkv.P, T, pm.row_job, pm.jobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
+                   L.kpool, L.vpool, ctx->page_table, ctx->qp, rs, 1, 1, ex);
+    launch_attn(st, pm.items, pm.nitems, pm.jobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
+                ctx->ppw, ctx->apart);
+    launch_attn_combine(st, pm.jobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU, ctx->xp_o, nullptr, pm.cwg,
+                        pm.ncwg, ctx->hybrid ? ctx->gbuf : nullptr);
+    launch_gemm(st, L.o, ctx->xp_o, ctx->mt_alloc, ctx->part, T, ctx->ncu);
+    launch_resid_w(st, x, ctx->part, L.o.P, T, Mpad, H, 0, L.ln2, ceil_div(H, 64), ctx->xp_h, ctx->ssp);
+}
+
+// The SwiGLU MLP (model.js:307-315) from the operand x*ln2: gate|up GEMM,
+// finish (row factor, silu*up), down GEMM, residual (+ round_f16 for a
+// trunk block) and the next block's operand x*next_ln1 (or none).
+static void ffn_half(cc_ctx* ctx, Layer& L, float* x, int T, int Mpad, int round, const float* next_ln1) {
+    const cc_dims& d = ctx->d;
+    hipStream_t st = ctx->stream;
+    const int H = d.hidden;
+    const RowScale rs = row_scale_of(ctx);
+    launch_gemm(st, L.gu, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
+    launch_fin_swiglu(st, ctx->part, L.gu.P, T, Mpad, d.ffn, L.down.KU, ctx->xp_f, rs);
+    launch_gemm(st, L.down, ctx->xp_f, ctx->mt_alloc, ctx->part, T, ctx->ncu);
+    launch_resid_w(st, x, ctx->part, L.down.P, T, Mpad, H, round, next_ln1, next_ln1 ? ceil_div(H, 64) : 0,
+                   next_ln1 ? ctx->xp_h : nullptr, ctx->ssp);
+}
+
+static int mpad_of(int T) { return 16 * ceil_div(T, 16) + (ceil_div(T, 16) > 1 && (ceil_div(T, 16) & 1) ? 16 : 0); }
+
+// The blocks [p0, p1) (model indices) over the packed rows: blockSegs
+// (web/model/model.js:619-624) per layer, with the reference's dispatches
+// fused into: operand prep, q|k|v GEMM, finish (rmsnorm's row factor + RoPE +
+// KV store + Q operand), attention, combine (o_proj operand), o GEMM,
+// residual (+ operand x*ln2 and the row's sum of squares), gate|up GEMM,
+// finish (row factor + SwiGLU), down GEMM, residual (+ round_f16 + the next
+// block's operand x*ln1 and sum of squares). A linear_attention block
+// replaces the attention half with linearBlockSegs (model.js:472-527).
 static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int b0, int b1) {
     const cc_dims& d = ctx->d;
     hipStream_t st = ctx->stream;
-    const int T = p.T, H = d.hidden, nH = d.n_heads, D = d.head_dim;
-    const int Mpad = 16 * ceil_div(T, 16) + (ceil_div(T, 16) > 1 && (ceil_div(T, 16) & 1) ? 16 : 0);
-    const JobDev* djobs = (const JobDev*)(ctx->d_meta + ml.jobs);
-    const AttnItem* ditems = (const AttnItem*)(ctx->d_meta + ml.items);
-    const int32_t* drow_job = (const int32_t*)(ctx->d_meta + ml.row_job);
-    const int32_t* dcwg = (const int32_t*)(ctx->d_meta + ml.cwg);
-    // rmsnorm's row factor, applied by the finish after each normed matmul
-    RowScale rs;
-    rs.ssp = ctx->ssp;
-    rs.nsl = ceil_div(H / 4, RW_THREADS);
-    rs.H = H;
-    rs.eps = d.rms_eps;
+    const int T = p.T, H = d.hidden;
+    const int Mpad = mpad_of(T);
+    PassMeta pm;
+    pm.jobs = (const JobDev*)(ctx->d_meta + ml.jobs);
+    pm.items = (const AttnItem*)(ctx->d_meta + ml.items);
+    pm.row_job = (const int32_t*)(ctx->d_meta + ml.row_job);
+    pm.cwg = (const int32_t*)(ctx->d_meta + ml.cwg);
+    pm.njobs = (int)p.jobs.size();
+    pm.nitems = p.nitems;
+    pm.ncwg = p.ncwg;
+    const RowScale rs = row_scale_of(ctx);
     const int KUH = ceil_div(H, 64);   // every block's first matmul reads K = hidden
-    const int njobs = (int)p.jobs.size();
     for (int b = b0; b < b1; b++) {
         Layer& L = ctx->layers[b - ctx->L0];
         if (b == b0) launch_resid_w(st, ctx->x, nullptr, 0, T, Mpad, H, 0, L.ln1, KUH, ctx->xp_h, ctx->ssp);
@@ -946,41 +1112,61 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
             // recurrence on each session's state, gated norm, out_proj
             const LinGeom& lg = ctx->lg;
             launch_gemm(st, L.lin, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-            launch_lin_conv(st, ctx->part, L.lin.P, T, njobs, djobs, rs, L.conv, lg, L.state, ctx->lraw, ctx->lrep);
-            launch_gdn(st, ctx->lraw, ctx->lrep, njobs, djobs, L.gp, lg, L.state, ctx->lcore);
+            launch_lin_conv(st, ctx->part, L.lin.P, T, pm.njobs, pm.jobs, rs, L.conv, lg, L.state, ctx->lraw,
+                            ctx->lrep);
+            launch_gdn(st, ctx->lraw, ctx->lrep, pm.njobs, pm.jobs, L.gp, lg, L.state, ctx->lcore);
             launch_lin_norm(st, ctx->lcore, ctx->lraw, L.gnorm, d.rms_eps, T, lg, L.out.KU, ctx->xp_v);
             launch_gemm(st, L.out, ctx->xp_v, ctx->mt_alloc, ctx->part, T, ctx->ncu);
             launch_resid_w(st, ctx->x, ctx->part, L.out.P, T, Mpad, H, 0, L.ln2, KUH, ctx->xp_h, ctx->ssp);
         } else {
-            QkExtras ex;
-            if (ctx->hybrid) {
-                ex.qn = L.qn;
-                ex.kn = L.kn;
-                ex.eps = d.rms_eps;
-                ex.gate = ctx->gbuf;
-            }
-            const int sq = L.qkv.P;
-            launch_gemm(st, L.qkv, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-            launch_fin_qkv(st, ctx->part, sq, T, drow_job, djobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
-                           L.kpool, L.vpool, ctx->page_table, ctx->qp, rs, 1, 1, ex);
-            launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom,
-                         ctx->group, ctx->ppw, ctx->apart);
-            launch_attn_combine(st, djobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU, ctx->xp_o, nullptr, dcwg,
-                                 p.ncwg, ctx->hybrid ? ctx->gbuf : nullptr);
-            const int so = L.o.P;
-            launch_gemm(st, L.o, ctx->xp_o, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-            launch_resid_w(st, ctx->x, ctx->part, so, T, Mpad, H, 0, L.ln2, KUH, ctx->xp_h, ctx->ssp);
+            full_attn_half(ctx, L, ctx->x, T, Mpad, pm);
         }
-        const int sg = L.gu.P;
-        launch_gemm(st, L.gu, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-        launch_fin_swiglu(st, ctx->part, sg, T, Mpad, d.ffn, L.down.KU, ctx->xp_f, rs);
-        const int sd = L.down.P;
-        launch_gemm(st, L.down, ctx->xp_f, ctx->mt_alloc, ctx->part, T, ctx->ncu);
         const bool next = b + 1 < b1;
-        launch_resid_w(st, ctx->x, ctx->part, sd, T, Mpad, H, 1, next ? ctx->layers[b + 1 - ctx->L0].ln1 : nullptr,
-                       next ? KUH : 0, next ? ctx->xp_h : nullptr, ctx->ssp);
+        ffn_half(ctx, L, ctx->x, T, Mpad, 1, next ? ctx->layers[b + 1 - ctx->L0].ln1 : nullptr);
     }
-    (void)D;
+}
+
+// mtpBlock's input (model.js:543-553): x = fc_e . enorm(embed_draft[ids]) +
+// fc_h . hnorm(h), into ctx->mx, followed by the block's operand x*ln1 and
+// its sums of squares. `ids` device int32 [T], `hin` rows [T][H]. The draft
+// embedding is not rounded (gatherEmbedNoPos).
+static void mtp_input(cc_ctx* ctx, const int32_t* ids, float* hin, int T) {
+    const cc_dims& d = ctx->d;
+    hipStream_t st = ctx->stream;
+    const int H = d.hidden, KUH = ceil_div(H, 64), Mpad = mpad_of(T);
+    launch_embed(st, ids, nullptr, T, ctx->embed_draft, ctx->mtp_e, 0);
+    launch_resid_norm(st, ctx->mtp_e, nullptr, nullptr, 0, T, Mpad, H, 0, ctx->enorm, d.rms_eps, KUH, ctx->xp_e,
+                      nullptr);
+    launch_resid_norm(st, hin, nullptr, nullptr, 0, T, Mpad, H, 0, ctx->hnorm, d.rms_eps, KUH, ctx->xp_hh, nullptr);
+    launch_gemm(st, ctx->fc_e, ctx->xp_e, ctx->mt_alloc, ctx->part, T, ctx->ncu);
+    launch_sum_splits(st, ctx->part, ctx->fc_e.P, T, H, ctx->mx);
+    launch_gemm(st, ctx->fc_h, ctx->xp_hh, ctx->mt_alloc, ctx->part, T, ctx->ncu);
+    launch_resid_w(st, ctx->mx, ctx->part, ctx->fc_h.P, T, Mpad, H, 0, ctx->mtpL.ln1, KUH, ctx->xp_h, ctx->ssp);
+}
+
+// The MTP layer's KV rows for a pass's MTP jobs (stage.js:1404-1421): each
+// row's token with the trunk's hidden row one position earlier (the
+// session's kept row for row 0). Only K and V are wanted, so the block runs
+// as far as the KV store: its output is not used (mtpBlock's is discarded).
+static void mtp_fill(cc_ctx* ctx, const MetaLayout& ml, int Tm, int njobs) {
+    hipStream_t st = ctx->stream;
+    const cc_dims& d = ctx->d;
+    const JobDev* mj = (const JobDev*)(ctx->d_meta + ml.mtp_jobs);
+    const int32_t* mrow = (const int32_t*)(ctx->d_meta + ml.mtp_row_job);
+    launch_gather_rows(st, ctx->x, ctx->mtpH, (const int32_t*)(ctx->d_meta + ml.mtp_src), Tm, d.hidden, ctx->mtp_in);
+    mtp_input(ctx, (const int32_t*)(ctx->d_meta + ml.mtp_ids), ctx->mtp_in, Tm);
+    Layer& M = ctx->mtpL;
+    launch_gemm(st, M.qkv, ctx->xp_h, ctx->mt_alloc, ctx->part, Tm, ctx->ncu);
+    QkExtras ex;
+    if (ctx->hybrid) {   // k_norm applies; the gate's columns are in the planes but not read
+        ex.qn = M.qn;
+        ex.kn = M.kn;
+        ex.eps = d.rms_eps;
+        ex.gate = ctx->gbuf;
+    }
+    launch_fin_qkv(st, ctx->part, M.qkv.P, Tm, mrow, mj, d.n_heads, ctx->group, ctx->geom, ctx->tbl, ctx->rot, M.kpool,
+                   M.vpool, ctx->page_table, ctx->qp, row_scale_of(ctx), 0, 1, ex);
+    (void)njobs;
 }
 
 // Profile replay (cc_profile): after the step's own work, each class's
@@ -1082,6 +1268,12 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         }
         if (at_end && !(jb.sampled == 0 || jb.sampled == 1 || jb.sampled == jb.n))
             return bad(j, "sampled must be 0, 1 or n at the head");
+        if (jb.mtp && ctx->mtp && at_end) {
+            // the MTP fill pairs each row's token with the row before (stage.js:1293)
+            if (!jb.ids) return bad(j, "an MTP job needs its " + std::to_string(jb.n) + " token ids");
+            for (int i = 0; i < jb.n; i++)
+                if (jb.ids[i] < 0 || jb.ids[i] >= d.vocab) return bad(j, "a token id is outside the vocabulary");
+        }
         if (ctx->any_linear) {
             // A recurrent block cannot be rewound, only restarted (past 0) or
             // rolled back to before its last verify (stage.js:1028-1090).
@@ -1134,6 +1326,31 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         }
     }
     size_t copy_bytes = ml.hidden;
+    // The MTP jobs' rows, packed (stage.js:1404-1421): row 0 of a job pairs
+    // its first token with the session's kept row, row i with the job's row
+    // i - 1.
+    int Tm = 0, nmj = 0;
+    if (ctx->mtp && at_end) {
+        JobDev* mj = (JobDev*)(hm + ml.mtp_jobs);
+        int32_t* mrow = (int32_t*)(hm + ml.mtp_row_job);
+        int32_t* msrc = (int32_t*)(hm + ml.mtp_src);
+        int32_t* mids = (int32_t*)(hm + ml.mtp_ids);
+        for (int j = 0; j < njobs; j++) {
+            if (!jobs[j].mtp) continue;
+            JobDev jd = p.jobs[j];
+            jd.row0 = Tm;
+            jd.qp_off = 0;
+            jd.snap = 0;
+            jd.keep = -1;
+            for (int i = 0; i < jobs[j].n; i++) {
+                mrow[Tm + i] = nmj;
+                msrc[Tm + i] = i == 0 ? -1 - jobs[j].slot : p.jobs[j].row0 + i - 1;
+                mids[Tm + i] = jobs[j].ids[i];
+            }
+            mj[nmj++] = jd;
+            Tm += jobs[j].n;
+        }
+    }
     if (gather) {
         int32_t* ids = (int32_t*)(hm + ml.ids);
         int r = 0;
@@ -1184,6 +1401,16 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         launch_to_half_bits(st, ctx->x, (int64_t)T * d.hidden, ctx->d_hbits);
         HIPCHK(hipMemcpyAsync(hout, ctx->d_hbits, (size_t)T * d.hidden * 2, hipMemcpyDeviceToHost, st));
     }
+    if (Tm > 0) {
+        mtp_fill(ctx, ml, Tm, nmj);
+        // a job that samples nothing (a prefill chunk) keeps its last row for
+        // the next job's row 0; a sampled job's row is kept by cc_mtp_draft
+        for (int j = 0; j < njobs; j++)
+            if (jobs[j].mtp && jobs[j].sampled == 0)
+                HIPCHK(hipMemcpyAsync(ctx->mtpH + (size_t)jobs[j].slot * d.hidden,
+                                      ctx->x + (size_t)(p.jobs[j].row0 + jobs[j].n - 1) * d.hidden,
+                                      (size_t)d.hidden * 4, hipMemcpyDeviceToDevice, st));
+    }
     HIPCHK(hipEventRecord(ctx->ev1, st));
     if (ctx->prof) prof_replay(ctx, p, ml, b0, b1, head);
     HIPCHK(hipStreamSynchronize(st));
@@ -1194,6 +1421,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
     prof_collect(ctx);
     ctx->passes++;
     ctx->rows += T;
+    ctx->last_T = T;
     if (b1 > b0) {
         // what the recurrent blocks now hold, and the verify a rollback may return to
         for (int j = 0; j < njobs; j++) {
@@ -1213,6 +1441,97 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
     } else if (!at_end) {
         std::memcpy(hidden_out, hout, (size_t)T * d.hidden * 2);
     }
+    return CC_OK;
+}
+
+cc_status cc_mtp_draft(cc_ctx* ctx, int32_t slot, int32_t row, int32_t token, int32_t pos, int32_t k_drafts,
+                       uint32_t* drafts) {
+    if (!ctx) return CC_EARG;
+    if (!ctx->mtp) return fail(ctx, CC_EARG, "no MTP head here");
+    const cc_dims& d = ctx->d;
+    const int H = d.hidden, K = k_drafts;
+    if (slot < 0 || slot >= (int)ctx->owned.size()) return fail(ctx, CC_EARG, "bad slot");
+    if (row < -1 || row >= ctx->last_T) return fail(ctx, CC_EARG, "row is not a row of the last pass");
+    if (K < 0 || K > MTP_STEPS_MAX) return fail(ctx, CC_EARG, "0..7 drafts");
+    if (K > 0 && (token < 0 || token >= d.mtp_vocab)) return fail(ctx, CC_EARG, "the token is outside the draft rows");
+    if (K > 0 && (pos < 0 || pos + K > ctx->o.n_max)) return fail(ctx, CC_EARG, "the drafts pass the context window");
+    if (K > 0 && !drafts) return fail(ctx, CC_EARG, "null drafts");
+    hipStream_t st = ctx->stream;
+    float* kept = ctx->mtpH + (size_t)slot * H;
+    if (row >= 0) HIPCHK(hipMemcpyAsync(kept, ctx->x + (size_t)row * H, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
+    if (K == 0) {
+        HIPCHK(hipStreamSynchronize(st));
+        return CC_OK;
+    }
+    // pages for the draft rows (stage.js:1291: the head takes them with the job)
+    {
+        int32_t* h_plan = (int32_t*)ctx->h_meta;
+        int32_t* d_plan = (int32_t*)ctx->d_meta;
+        HIPCHK(hipStreamSynchronize(st));
+        const int need = ceil_div(pos + K, ctx->geom.page);
+        h_plan[0] = slot;
+        h_plan[1] = ctx->owned[slot];
+        h_plan[2] = std::max(0, need - ctx->owned[slot]);
+        h_plan[3] = 0;
+        HIPCHK(hipMemcpyAsync(d_plan, h_plan, 16, hipMemcpyHostToDevice, st));
+        std::vector<std::pair<int, int>> want{{slot, pos + K}};
+        cc_status ps = take_pages(ctx, want, d_plan, h_plan, nullptr);
+        if (ps != CC_OK) return ps;
+    }
+    // every step's one-row plan, in one upload; ids[0] the token, ids[k+1]
+    // step k's draft (written on the device, read by step k+1)
+    std::vector<StepPlan> plans(K);
+    uint8_t* hc = ctx->h_chain;
+    ((int32_t*)hc)[0] = token;
+    const size_t mtq1 = ceil_div(ctx->group, 16);
+    const size_t a256 = 255;
+    auto al = [&](size_t b) { return (b + a256) & ~a256; };
+    const size_t o_items = al(sizeof(JobDev)), o_row = o_items + al(sizeof(AttnItem) * ctx->geom.nKV * mtq1 *
+                                                                     ceil_div(ctx->max_pages, ctx->ppw));
+    const size_t o_cwg = o_row + al(4);
+    for (int k = 0; k < K; k++) {
+        cc_job j{};
+        j.slot = slot;
+        j.past = pos + k;
+        j.n = 1;
+        build_plan(ctx, &j, 1, plans[k], false);
+        uint8_t* b = hc + 256 + (size_t)k * ctx->chain_step;
+        if (o_items + plans[k].items.size() * sizeof(AttnItem) > o_row || plans[k].cwg.size() * 4 > 12 * ctx->geom.nKV * mtq1)
+            return fail(ctx, CC_EARG, "draft step plan too large");
+        std::memcpy(b, plans[k].jobs.data(), sizeof(JobDev));
+        std::memcpy(b + o_items, plans[k].items.data(), plans[k].items.size() * sizeof(AttnItem));
+        std::memcpy(b + o_row, plans[k].row_job.data(), 4);
+        std::memcpy(b + o_cwg, plans[k].cwg.data(), plans[k].cwg.size() * 4);
+    }
+    HIPCHK(hipMemcpyAsync(ctx->d_chain, hc, 256 + (size_t)K * ctx->chain_step, hipMemcpyHostToDevice, st));
+    int32_t* ids = (int32_t*)ctx->d_chain;
+    HIPCHK(hipMemcpyAsync(ctx->mtp_in, kept, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
+    const int KUH = ceil_div(H, 64);
+    for (int k = 0; k < K; k++) {
+        // mtpChain step k (model.js:567-576): mtpBlock then mtpDraft
+        const uint8_t* b = ctx->d_chain + 256 + (size_t)k * ctx->chain_step;
+        PassMeta pm;
+        pm.jobs = (const JobDev*)b;
+        pm.items = (const AttnItem*)(b + o_items);
+        pm.row_job = (const int32_t*)(b + o_row);
+        pm.cwg = (const int32_t*)(b + o_cwg);
+        pm.njobs = 1;
+        pm.nitems = plans[k].nitems;
+        pm.ncwg = plans[k].ncwg;
+        mtp_input(ctx, ids + k, ctx->mtp_in, 1);
+        full_attn_half(ctx, ctx->mtpL, ctx->mx, 1, mpad_of(1), pm);
+        ffn_half(ctx, ctx->mtpL, ctx->mx, 1, mpad_of(1), 0, nullptr);
+        launch_resid_norm(st, ctx->mx, nullptr, nullptr, 0, 1, 32, H, 0, ctx->mtp_norm, d.rms_eps, KUH, ctx->xp_h,
+                          nullptr);
+        launch_gemm(st, ctx->head_draft, ctx->xp_h, ctx->mt_alloc, ctx->mtp_logits, 1, ctx->ncu);
+        launch_topk(st, ctx->mtp_logits, ctx->head_draft.P, 1, d.mtp_vocab, 1, ctx->tk_a, ctx->tk_b, ctx->d_vals,
+                    (uint32_t*)(ids + k + 1));
+        if (k + 1 < K)
+            HIPCHK(hipMemcpyAsync(ctx->mtp_in, ctx->mx, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
+    }
+    HIPCHK(hipMemcpyAsync(drafts, ids + 1, (size_t)K * 4, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipStreamSynchronize(st));
+    HIPCHK(take_launch_error());
     return CC_OK;
 }
 

@@ -118,8 +118,12 @@ void launch_gdn(hipStream_t st, const float* lraw, const float* lrep, int njobs,
 // silu(z), into the out_proj operand (K = valueDim).
 void launch_lin_norm(hipStream_t st, const float* core, const float* lraw, const float* gnorm, float eps,
                      int M, const LinGeom& lg, int KU, uint4* Xp);
+// round: the trunk's rows are rounded to f16 (stage.js:1365-1370); the MTP
+// head's draft embedding is not (model.js:545). An id past wte.N reads zero.
 void launch_embed(hipStream_t st, const int32_t* ids, const uint16_t* hidden, int T, const QTensor& wte,
-                  float* x);
+                  float* x, int round = 1);
+void launch_gather_rows(hipStream_t st, const float* x, const float* alt, const int32_t* src, int T, int H,
+                        float* rows);
 void launch_topk(hipStream_t st, const float* logits, int planes, int rows, int V, int M, uint64_t* a,
                  uint64_t* b, float* vals, uint32_t* ids);
 void launch_round_f16(hipStream_t st, float* a, int64_t n);

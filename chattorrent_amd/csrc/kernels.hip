@@ -1623,7 +1623,8 @@ void launch_attn_combine(hipStream_t st, const JobDev* jobs, const float* part, 
 // embedding rows are rounded like a block's output, stage.js:1365-1370);
 // or, for a pass entering past position 0, the f16 rows handed in.
 __global__ void k_embed(const int32_t* __restrict__ ids, const uint16_t* __restrict__ hidden, int T, int H,
-                        const uint8_t* __restrict__ rec, int Nt, int KU, int P, float* __restrict__ x) {
+                        const uint8_t* __restrict__ rec, int Nt, int KU, int P, float* __restrict__ x, int round,
+                        int nrows) {
     const int t = blockIdx.y;
     const int h = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= T || h >= H) return;
@@ -1632,18 +1633,42 @@ __global__ void k_embed(const int32_t* __restrict__ ids, const uint16_t* __restr
         return;
     }
     const int v = ids[t];
+    if (v < 0 || v >= nrows) {   // a token outside a shorter table (the MTP's draft rows) reads zero
+        x[(size_t)t * H + h] = 0.0f;
+        return;
+    }
     const int tile = v >> 4, u = h >> 6, lane = (v & 15) + 16 * ((h & 31) >> 3);
     const int byte = 8 * ((h & 63) >> 5) + (h & 7);
     const uint8_t* r = rec + lx_record(tile, u, KU, P, Nt);
     const int8_t q = (int8_t)(r[(tile & 1) * 1024 + lane * 16 + byte] ^ 0x80);
     const uint16_t sb = *(const uint16_t*)(r + 2048 + (v & 15) * 8 + (tile & 1) * 4 + ((h >> 5) & 1) * 2);
-    x[(size_t)t * H + h] = round_f16_value((float)q * half_value(sb));
+    const float e = (float)q * half_value(sb);
+    x[(size_t)t * H + h] = round ? round_f16_value(e) : e;
 }
 
 void launch_embed(hipStream_t st, const int32_t* ids, const uint16_t* hidden, int T, const QTensor& wte,
-                  float* x) {
+                  float* x, int round) {
     dim3 grid((wte.K + 255) / 256, T);
-    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, st, ids, hidden, T, wte.K, wte.codes, wte.Nt, wte.KU, wte.P, x);
+    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, st, ids, hidden, T, wte.K, wte.codes, wte.Nt, wte.KU, wte.P, x,
+                       round, ids ? wte.N : 0);
+    CHECK_LAUNCH();
+}
+
+// rows[r] = src[r] >= 0 ? x row src[r] : alt row (-1 - src[r]), H floats each:
+// the MTP's hidden rows, the session's kept row first (stage.js:1408-1417).
+__global__ void k_gather_rows(const float* __restrict__ x, const float* __restrict__ alt,
+                              const int32_t* __restrict__ src, int T, int H, float* __restrict__ rows) {
+    const int r = blockIdx.y;
+    const int h = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= T || h >= H) return;
+    const int s = src[r];
+    rows[(size_t)r * H + h] = s >= 0 ? x[(size_t)s * H + h] : alt[(size_t)(-1 - s) * H + h];
+}
+
+void launch_gather_rows(hipStream_t st, const float* x, const float* alt, const int32_t* src, int T, int H,
+                        float* rows) {
+    if (T <= 0) return;
+    hipLaunchKernelGGL(k_gather_rows, dim3((H + 255) / 256, T), dim3(256), 0, st, x, alt, src, T, H, rows);
     CHECK_LAUNCH();
 }
 

@@ -67,6 +67,10 @@ typedef struct cc_dims {
     int32_t hybrid;
     const uint8_t* layer_kinds;
     int32_t lin_nk, lin_nv, lin_dk, lin_dv, lin_conv;
+    /* The MTP draft head (model.js:529-576, loader.js:628-638): the
+     * vocabulary rows it drafts over (manifest mtp.draft_vocab); 0: none. A
+     * context holding the head holds it. */
+    int32_t mtp_vocab;
 } cc_dims;
 enum { CC_FULL_ATTENTION = 0, CC_LINEAR_ATTENTION = 1 };
 
@@ -102,8 +106,15 @@ enum {
      * dt_bias), gated_norm f32 [Dv], out_proj q8 [hidden, valueDim] */
     CC_T_IN_Q = 15, CC_T_IN_K = 16, CC_T_IN_V = 17, CC_T_IN_Z = 18, CC_T_IN_B = 19, CC_T_IN_A = 20,
     CC_T_CONV_Q = 21, CC_T_CONV_K = 22, CC_T_CONV_V = 23, CC_T_GATE_PARAMS = 24, CC_T_GATED_NORM = 25,
-    CC_T_OUT_PROJ = 26
+    CC_T_OUT_PROJ = 26,
+    /* the MTP head (loader.js:633-634): enorm, hnorm, mtp_norm f32 [hidden];
+     * fc_e, fc_h q8 [hidden, hidden]; embed_draft, head_draft q8
+     * [mtp_vocab, hidden]. Its full-attention block's tensors are the block
+     * ids above at layer CC_LAYER_MTP. */
+    CC_T_MTP_ENORM = 27, CC_T_MTP_HNORM = 28, CC_T_MTP_FC_E = 29, CC_T_MTP_FC_H = 30, CC_T_MTP_NORM = 31,
+    CC_T_MTP_EMBED = 32, CC_T_MTP_HEAD = 33
 };
+enum { CC_LAYER_MTP = -2 };
 enum { CC_SCALES_F16 = 0, CC_SCALES_F32 = 1 };
 
 /* new Runner(device, d, w, {...}) — web/model/stage.js:107-238. */
@@ -149,6 +160,12 @@ typedef struct cc_job {
     int32_t snap;
     int32_t rollback;
     int32_t keep;
+    /* The job's session drafts with the MTP head (stage.js:1287-1293): at a
+     * context holding it, the MTP layer's KV rows past..past+n-1 are filled
+     * from the job's `ids` (given whatever the entry position) paired with
+     * the trunk's hidden rows one position earlier; a job that samples
+     * nothing keeps its last row for the next job (stage.js:1408-1421). */
+    int32_t mtp;
 } cc_job;
 
 /* Runner.#pass — web/model/stage.js:1314-1481. Runs positions [at, to) for
@@ -161,6 +178,17 @@ typedef struct cc_job {
 cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, int32_t to,
                   int32_t topk, float* top_vals, uint32_t* top_ids, uint16_t* hidden_out,
                   int32_t* status);
+
+/* After sampling `token` from row `row` of the last pass (Runner.#mtpAfter,
+ * web/model/stage.js:296-320): the session keeps that row's hidden state
+ * (row -1: keep the one it has) and, for k_drafts > 0 (at most 7), the MTP
+ * head chains that many drafts after `token` at positions pos..
+ * (model.js:567-576 mtpChain: each step's argmax over the draft vocabulary,
+ * lowest id on a tie, is the next step's token). The MTP layer's KV rows
+ * written there are speculative; the next job's fill rewrites them. Pages
+ * are taken for pos + k_drafts tokens. `drafts` receives k_drafts ids. */
+cc_status cc_mtp_draft(cc_ctx* ctx, int32_t slot, int32_t row, int32_t token, int32_t pos, int32_t k_drafts,
+                       uint32_t* drafts);
 
 /* Runner.#release / freePages — web/model/stage.js:842-874,
  * web/model/model.js:204-211: the slot's pages return to the pool. */

@@ -289,3 +289,78 @@ class HybridModel:
 
     def pass_(self, jobs, **kw):
         return self.base.pass_(jobs, **kw)
+
+
+class MtpHead:
+    """The MTP draft head (model.js:529-576 mtpBlock / mtpDraft / mtpChain,
+    stage.js:296-320 #mtpAfter and :1404-1421 the fill). Its one
+    full-attention block keeps its own int8 KV in a pool layer addressed by
+    the trunk's page tables; each session keeps the trunk row its next MTP
+    row pairs with (`kept`, zero until set). `trunk` is the oracle model
+    (HybridModel or model.Model) whose frames and pool it shares."""
+
+    def __init__(self, trunk, w, draft_vocab):
+        from . import model as Mo
+
+        base = trunk.base if isinstance(trunk, HybridModel) else trunk
+        self.d = base.d
+        d1 = dict(self.d, n_layer=1, layer_types=["full_attention"])
+        self.m = Mo.Model(d1, n_slots=len(base.frames), max_pages=base.max_pages, n_pages=base.pool.n_pages)
+        self.m.frames, self.m.pool = base.frames, base.pool
+        self.w, self.V = w, draft_vocab
+        self.kept = {}
+        self.hybrid = bool(self.d.get("hybrid"))
+
+    def _mm(self, h, t):
+        return L.matmul_q8(np.ascontiguousarray(h, F32), *t, group=self.m.group)
+
+    def block(self, hin, ids, slot, past):
+        """mtpBlock: x = fc_e·enorm(embed_draft[ids]) + fc_h·hnorm(h), then the
+        layer (no f16 round: it is not a trunk block)."""
+        d, w = self.d, self.w
+        codes, sc = w["embed_draft"]
+        e = L.gather_embed_q8(np.asarray(ids, np.int32), codes, sc, self.m.group)
+        x = self._mm(L.rmsnorm(e, w["enorm"], d["rms_eps"]), w["fc_e"])
+        L.add_inplace(x, self._mm(L.rmsnorm(np.asarray(hin, F32), w["hnorm"], d["rms_eps"]), w["fc_h"]))
+        lw = w["block"]
+        segs = [{"slot": slot, "past": past, "n": len(ids), "row": 0}]
+        if self.hybrid:
+            full_block_extras(self.m, 0, lw, x, segs)
+        else:
+            h = L.rmsnorm(x, lw["ln1"], d["rms_eps"])
+            qkv = [self._mm(h, lw[n]) for n in ("q", "k", "v")]
+            L.add_inplace(x, self._mm(self.m.attend(0, slot, *qkv, past), lw["o"]))
+        h = L.rmsnorm(x, lw["ln2"], d["rms_eps"])
+        act = L.silu_mul(self._mm(h, lw["gate"]), self._mm(h, lw["up"]))
+        L.add_inplace(x, self._mm(act, lw["down"]))
+        return x
+
+    def kept_row(self, slot):
+        return self.kept.get(slot, np.zeros(self.d["hidden"], F32))
+
+    def fill(self, job, hidden):
+        """The MTP layer's KV for a job's rows: token past + r with the trunk
+        row of past + r - 1 (the kept row for r = 0). `hidden`: the job's rows
+        after the last block. A job that samples nothing keeps its last row."""
+        n = job["n"]
+        hin = np.concatenate([self.kept_row(job["slot"])[None, :], hidden[:n - 1]], axis=0)
+        self.block(hin, job["ids"], job["slot"], job["past"])
+        if job.get("sampled", 1) == 0:
+            self.kept[job["slot"]] = np.array(hidden[n - 1], F32)
+
+    def draft(self, slot, row, token, pos, k):
+        """#mtpAfter + mtpChain: keep `row` (None: the kept one), then k drafts,
+        each the argmax of head_draft·mtp_norm(x) over the draft rows, lowest
+        id on a tie (argmax_rows, kernels.js:1405-1440)."""
+        if row is not None:
+            self.kept[slot] = np.array(row, F32)
+        if k > 0 and not self.m.pool.ensure(self.m.frames[slot], pos + k):
+            raise RuntimeError("the KV pool cannot fit the drafts")
+        h, t, out = self.kept_row(slot)[None, :], token, []
+        for i in range(k):
+            x = self.block(h, [t], slot, pos + i)
+            logits = self._mm(L.rmsnorm(x, self.w["mtp_norm"], self.d["rms_eps"]), self.w["head_draft"])[0]
+            t = int(np.argmax(logits))   # the first maximum: the lowest id on a tie
+            out.append((t, logits))
+            h = x
+        return out

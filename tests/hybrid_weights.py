@@ -92,3 +92,39 @@ def upload(ctx, w, d, lo=0, hi=None):
                 ctx.upload_q8(i, t, *lw[name])
             ctx.upload_norm(i, cc.T_Q_NORM, lw["q_norm"])
             ctx.upload_norm(i, cc.T_K_NORM, lw["k_norm"])
+
+
+def make_mtp(d, seed, draft_vocab):
+    """The MTP head's weights (loader.js:633-634): the norms, fc_e / fc_h,
+    the draft embedding and head over the first `draft_vocab` rows, and one
+    full-attention block (with the hybrid extras on a hybrid model)."""
+    rng = np.random.default_rng(seed + 1000)
+    H, F, D = d["hidden"], d["ffn"], d["head_dim"]
+    qd, kvd = d["n_heads"] * D, d["n_kv_heads"] * D
+    norm = lambda n: (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)   # noqa: E731
+    blk = {"kind": "full", "ln1": norm(H), "ln2": norm(H), "gate": q8(rng, F, H), "up": q8(rng, F, H),
+           "down": q8(rng, H, F), "q": q8(rng, qd, H), "k": q8(rng, kvd, H), "v": q8(rng, kvd, H), "o": q8(rng, H, qd)}
+    if d.get("hybrid"):
+        blk.update(attn_gate=q8(rng, qd, H), q_norm=norm(D), k_norm=norm(D))
+    return {"enorm": norm(H), "hnorm": norm(H), "mtp_norm": norm(H), "fc_e": q8(rng, H, H), "fc_h": q8(rng, H, H),
+            "embed_draft": q8(rng, draft_vocab, H, out_std=np.sqrt(H)), "head_draft": q8(rng, draft_vocab, H),
+            "block": blk}
+
+
+def upload_mtp(ctx, wm, d):
+    from chattorrent_amd import ccdecode as cc
+    for t, name in ((cc.T_MTP_ENORM, "enorm"), (cc.T_MTP_HNORM, "hnorm"), (cc.T_MTP_NORM, "mtp_norm")):
+        ctx.upload_norm(-1, t, wm[name])
+    for t, name in ((cc.T_MTP_FC_E, "fc_e"), (cc.T_MTP_FC_H, "fc_h"), (cc.T_MTP_EMBED, "embed_draft"),
+                    (cc.T_MTP_HEAD, "head_draft")):
+        ctx.upload_q8(-1, t, *wm[name])
+    b, L = wm["block"], cc.LAYER_MTP
+    ctx.upload_norm(L, cc.T_LN1, b["ln1"])
+    ctx.upload_norm(L, cc.T_LN2, b["ln2"])
+    for t, name in ((cc.T_Q, "q"), (cc.T_K, "k"), (cc.T_V, "v"), (cc.T_O, "o"), (cc.T_GATE, "gate"),
+                    (cc.T_UP, "up"), (cc.T_DOWN, "down")):
+        ctx.upload_q8(L, t, *b[name])
+    if d.get("hybrid"):
+        ctx.upload_q8(L, cc.T_ATTN_GATE, *b["attn_gate"])
+        ctx.upload_norm(L, cc.T_Q_NORM, b["q_norm"])
+        ctx.upload_norm(L, cc.T_K_NORM, b["k_norm"])
