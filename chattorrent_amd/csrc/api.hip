@@ -246,8 +246,8 @@ cc_status check_dims(cc_ctx* ctx, const cc_dims& d, const cc_opts& o) {
         if (d.lin_conv != LIN_CONV_K) return fail(ctx, CC_EARG, "linear_conv_kernel_dim must be 4");
     }
     if (d.n_heads % d.n_kv_heads != 0) return fail(ctx, CC_EARG, "n_heads not divisible by n_kv_heads");
-    if (d.head_dim != 64 && d.head_dim != 128)
-        return fail(ctx, CC_EARG, "head_dim must be 64 or 128 (the int8 KV blocks are 32 wide)");
+    if (d.head_dim != 64 && d.head_dim != 128 && d.head_dim != 256)
+        return fail(ctx, CC_EARG, "head_dim must be 64, 128 or 256 (the int8 KV blocks are 32 wide)");
     if (d.q8_group != 32) return fail(ctx, CC_EARG, "q8 weights must use one scale per 32 values");
     // Fused q|k|v and gate|up start each part on a tile pair (32 rows).
     if (d.hidden % 64 || d.ffn % 32) return fail(ctx, CC_EARG, "hidden must be a multiple of 64, ffn of 32");

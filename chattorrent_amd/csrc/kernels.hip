@@ -986,7 +986,10 @@ void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const 
                     int do_q, int do_kv, const QkExtras& ex) {
     const int nall = nH + 2 * g.nKV + (ex.gate ? nH : 0);
     dim3 grid((nall + 3) / 4, M);
-    if (g.D == 128)
+    if (g.D == 256)
+        hipLaunchKernelGGL(k_fin_qkv<256>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
+                           rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv, ex);
+    else if (g.D == 128)
         hipLaunchKernelGGL(k_fin_qkv<128>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
                            rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv, ex);
     else
@@ -1302,7 +1305,7 @@ void launch_lin_norm(hipStream_t st, const float* core, const float* lraw, const
 // branch on row state: MFMA reads all lanes' operands whatever the execution
 // mask, and a still fully masked row (max -inf) just takes alpha = 0, p = 0.
 template <int NG>
-__global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ items, int nitems,
+__global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __restrict__ items, int nitems,
                                                  const JobDev* __restrict__ jobs, const uint4* __restrict__ Qp,
                                                  const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
                                                  const uint32_t* __restrict__ page_table, KVGeom g, int group, int ppw,
@@ -1310,8 +1313,9 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
     constexpr int D = 32 * NG;
     constexpr int DT = D / 16;
     // per wave, the current page's K and V scale blocks (64 tokens x NG groups, f32)
-    __shared__ __attribute__((aligned(16))) float ksl[4][256];
-    __shared__ __attribute__((aligned(16))) float vsl[4][256];
+    constexpr int SCL = NG > 4 ? NG / 4 : 1;   // 1 KiB loads per scale block (16 B a lane)
+    __shared__ __attribute__((aligned(16))) float ksl[4][256 * SCL];
+    __shared__ __attribute__((aligned(16))) float vsl[4][256 * SCL];
     const int lane = threadIdx.x & 63, j4 = lane >> 4, l16 = lane & 15;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wid = blockIdx.x * 4 + wv;
@@ -1359,11 +1363,14 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
     for (int dt = 0; dt < DT; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     u32x4 kc[4][NG / 2], vc[DT];
-    u32x4 kst, vst;   // the next page's scale blocks, 16 B a lane, on their way to LDS
+    u32x4 kst[SCL], vst[SCL];   // the next page's scale blocks, 16 B a lane per KiB, on their way to LDS
     // the next page's scale blocks, then its K codes
     auto load_k = [&](__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv) {
-        kst = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16, 64 * D, 0);
-        vst = __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 64 * D, 0);
+#pragma unroll
+        for (int q = 0; q < SCL; q++) {
+            kst[q] = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16, 64 * D + 1024 * q, 0);
+            vst[q] = __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 64 * D + 1024 * q, 0);
+        }
 #pragma unroll
         for (int tt = 0; tt < 4; tt++)
 #pragma unroll
@@ -1380,8 +1387,11 @@ __global__ __launch_bounds__(256, 2) void k_attn(const AttnItem* __restrict__ it
     auto page = [&](int p) {
         // the last page reloads itself instead of branching (an L2 hit)
         const int pn = p + 1 < p1 ? p + 1 : p;
-        *(u32x4*)&ksl[wv][lane * 4] = kst;
-        *(u32x4*)&vsl[wv][lane * 4] = vst;
+#pragma unroll
+        for (int q = 0; q < SCL; q++) {
+            *(u32x4*)&ksl[wv][256 * q + lane * 4] = kst[q];
+            *(u32x4*)&vsl[wv][256 * q + lane * 4] = vst[q];
+        }
         {
             float pr[4][4];
             uint32_t keep[4][4];   // all ones for a visible token, zero for a masked one
@@ -1498,7 +1508,10 @@ void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev
                  int ppw, float* part) {
     if (nitems <= 0) return;
     const int blocks = (nitems + 3) / 4;
-    if (g.ng == 4)
+    if (g.ng == 8)
+        hipLaunchKernelGGL(k_attn<8>, dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool, page_table, g,
+                     group, ppw, part);
+    else if (g.ng == 4)
         hipLaunchKernelGGL(k_attn<4>, dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool, page_table, g,
                      group, ppw, part);
     else
@@ -1551,63 +1564,71 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
         if (lane == 0) Ls[rl] = L;
     }
     __syncthreads();
+    // 16 rows x D columns, 8 a thread, in chunks of at most 128 columns (one
+    // chunk up to D = 128, two at D = 256); every thread reaches every barrier
     const int sub = threadIdx.x >> 8, t = threadIdx.x & 255;
-    const int rl = t / (D / 8), d0 = (t % (D / 8)) * 8;
+    const int CW = D < 128 ? D : 128;
+    const int rl = t / (CW / 8);
     const bool live = rl < 16 && mt * 16 + rl < R;
-    float O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (live) {
-        const float* src = base + (size_t)rl * W + 4 + d0;
-        auto add = [&](const float4& a, const float4& b, float w) {
-            O[0] += a.x * w; O[1] += a.y * w; O[2] += a.z * w; O[3] += a.w * w;
-            O[4] += b.x * w; O[5] += b.y * w; O[6] += b.z * w; O[7] += b.w * w;
-        };
-        const int c1 = ((sub + 1) * nc) / COMBINE_SPLIT;
-        int c = (sub * nc) / COMBINE_SPLIT;
-        for (; c + 8 <= c1; c += 8) {
-            float4 a[8], b[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                a[u] = *(const float4*)(src + (c + u) * pstride);
-                b[u] = *(const float4*)(src + (c + u) * pstride + 4);
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) add(a[u], b[u], wgt[rl][c + u]);
-        }
-        for (; c < c1; c++) add(*(const float4*)(src + c * pstride), *(const float4*)(src + c * pstride + 4), wgt[rl][c]);
-        if (sub > 0) {
-            red[sub - 1][t][0] = make_float4(O[0], O[1], O[2], O[3]);
-            red[sub - 1][t][1] = make_float4(O[4], O[5], O[6], O[7]);
-        }
-    }
-    __syncthreads();
     const int rho = mt * 16 + rl;
-    if (sub > 0 || !live) return;   // no barrier below
+    for (int c0 = 0; c0 < D; c0 += CW) {
+        const int d0 = c0 + (t % (CW / 8)) * 8;
+        float O[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (live) {
+            const float* src = base + (size_t)rl * W + 4 + d0;
+            auto add = [&](const float4& a, const float4& b, float w) {
+                O[0] += a.x * w; O[1] += a.y * w; O[2] += a.z * w; O[3] += a.w * w;
+                O[4] += b.x * w; O[5] += b.y * w; O[6] += b.z * w; O[7] += b.w * w;
+            };
+            const int c1 = ((sub + 1) * nc) / COMBINE_SPLIT;
+            int c = (sub * nc) / COMBINE_SPLIT;
+            for (; c + 8 <= c1; c += 8) {
+                float4 a[8], b[8];
 #pragma unroll
-    for (int q = 0; q < COMBINE_SPLIT - 1; q++) {
-        const float4 a = red[q][t][0], b = red[q][t][1];
-        O[0] += a.x; O[1] += a.y; O[2] += a.z; O[3] += a.w;
-        O[4] += b.x; O[5] += b.y; O[6] += b.z; O[7] += b.w;
-    }
-    float v[8];
-    const float L = Ls[rl];
+                for (int u = 0; u < 8; u++) {
+                    a[u] = *(const float4*)(src + (c + u) * pstride);
+                    b[u] = *(const float4*)(src + (c + u) * pstride + 4);
+                }
 #pragma unroll
-    for (int j = 0; j < 8; j++) v[j] = O[j] / L;
-    const int i = rho / group, gi = rho % group;
-    const int r = jb.row0 + i;
-    const int k = (kvh * group + gi) * D + d0;
-    if (gate) {
-        // sigmoid_mul (kernels.js:1822-1839): s = 1/(1+exp(-gate)), s*a
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float sg = 1.0f / (1.0f + expf(-gate[(size_t)r * nH * D + k + j]));
-            v[j] = sg * v[j];
+                for (int u = 0; u < 8; u++) add(a[u], b[u], wgt[rl][c + u]);
+            }
+            for (; c < c1; c++) add(*(const float4*)(src + c * pstride), *(const float4*)(src + c * pstride + 4), wgt[rl][c]);
+            if (sub > 0) {
+                red[sub - 1][t][0] = make_float4(O[0], O[1], O[2], O[3]);
+                red[sub - 1][t][1] = make_float4(O[4], O[5], O[6], O[7]);
+            }
         }
-    }
-    if (ctx_out) {
+        __syncthreads();
+        if (sub == 0 && live) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) ctx_out[(size_t)r * nH * D + k + j] = v[j];
+            for (int q = 0; q < COMBINE_SPLIT - 1; q++) {
+                const float4 a = red[q][t][0], b = red[q][t][1];
+                O[0] += a.x; O[1] += a.y; O[2] += a.z; O[3] += a.w;
+                O[4] += b.x; O[5] += b.y; O[6] += b.z; O[7] += b.w;
+            }
+            float v[8];
+            const float L = Ls[rl];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = O[j] / L;
+            const int i = rho / group, gi = rho % group;
+            const int r = jb.row0 + i;
+            const int k = (kvh * group + gi) * D + d0;
+            if (gate) {
+                // sigmoid_mul (kernels.js:1822-1839): s = 1/(1+exp(-gate)), s*a
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float sg = 1.0f / (1.0f + expf(-gate[(size_t)r * nH * D + k + j]));
+                    v[j] = sg * v[j];
+                }
+            }
+            if (ctx_out) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) ctx_out[(size_t)r * nH * D + k + j] = v[j];
+            }
+            write_hilo(Xp, r, k / 8, KU, v);
+        }
+        __syncthreads();   // `red` is reused by the next chunk
     }
-    write_hilo(Xp, r, k / 8, KU, v);
 }
 
 void launch_attn_combine(hipStream_t st, const JobDev* jobs, const float* part, const KVGeom& g, int nH, int group,

@@ -19,6 +19,13 @@ WIDE = dict(hidden=1024, n_layer=4, n_heads=8, n_kv_heads=2, head_dim=128, ffn=1
             layer_types=["linear_attention", "full_attention", "linear_attention", "linear_attention"],
             lin_nk=2, lin_nv=6, lin_dk=128, lin_dv=128, lin_conv=4)
 
+# Qwen3.8-27B's full-attention heads (head_dim 256, a quarter of it rotary,
+# four query heads per kv head) and its Gated DeltaNet widths, small hidden
+D256 = dict(hidden=512, n_layer=4, n_heads=4, n_kv_heads=1, head_dim=256, ffn=1024, vocab=384, rms_eps=1e-6,
+            rope_theta=1e7, rot_dim=64, tied=False, hybrid=True,
+            layer_types=["linear_attention"] * 3 + ["full_attention"],
+            lin_nk=2, lin_nv=4, lin_dk=128, lin_dv=128, lin_conv=4)
+
 
 def q8(rng, N, K, out_std=1.0):
     """int8 codes in ±127 and per-32 scales (exact in f16) sized so that a

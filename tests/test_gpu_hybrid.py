@@ -42,11 +42,11 @@ def _pair(d, slots=3, n_max=512, t_max=64):
     return c, om
 
 
-@pytest.mark.parametrize("cfg", ["spike", "wide"])
+@pytest.mark.parametrize("cfg", ["spike", "wide", "d256"])
 def test_hybrid_passes_match_oracle(gpu, cfg):
     """Prefill of two sessions, decode steps fed back greedily, a 3-row verify
     beside a decode, then a new session in a used slot (state reset)."""
-    d = HW.SPIKE if cfg == "spike" else HW.WIDE
+    d = {"spike": HW.SPIKE, "wide": HW.WIDE, "d256": HW.D256}[cfg]
     c, om = _pair(d)
     rng = np.random.default_rng(3)
     V = d["vocab"]

@@ -138,7 +138,12 @@ def _oracle_cache(d, n_pages, page=64):
     return np.zeros(n_pages * d["n_kv_heads"] * page * rw, np.uint32)
 
 
-@pytest.mark.parametrize("dims", ["smol", "27b"])
+# head_dim 256 (Qwen3.8-27B's full-attention heads) on a plain model shape
+D256 = dict(hidden=1024, n_layer=1, n_heads=4, n_kv_heads=1, head_dim=256, ffn=1024, vocab=512, rms_eps=1e-6,
+            rope_theta=1e7, tied=True)
+
+
+@pytest.mark.parametrize("dims", ["smol", "27b", "d256"])
 def test_store_kv_bit_exact(gpu, dims):
     """store_kv (web/model/kernels.js:1024-1073): RoPE'd K and plain V quantised
     per 32 values — codes and scales bit-exact with the oracle given the same
@@ -146,7 +151,7 @@ def test_store_kv_bit_exact(gpu, dims):
     page boundary; rows outside the job are untouched."""
     from oracle import lib as L
     from oracle import model as Mo
-    d = configs.with_layers(configs.SMOLLM2 if dims == "smol" else configs.M27B, 1)
+    d = D256 if dims == "d256" else configs.with_layers(configs.SMOLLM2 if dims == "smol" else configs.M27B, 1)
     c = _ctx(gpu, d, n_max=512, t_max=16, slots=2)
     try:
         D, nKV = d["head_dim"], d["n_kv_heads"]
@@ -181,7 +186,7 @@ def test_attend_vs_oracle(gpu):
     from oracle import lib as L
     from oracle import model as Mo
     for base, tokens, n in [(configs.SMOLLM2, 130, 1), (configs.M27B, 700, 1), (configs.M27B, 300, 8),
-                            (configs.SMOLLM2, 64, 37)]:
+                            (configs.SMOLLM2, 64, 37), (D256, 200, 1), (D256, 520, 6)]:
         d = configs.with_layers(base, 1)
         c = _ctx(gpu, d, n_max=1024, t_max=64, slots=2)
         try:
