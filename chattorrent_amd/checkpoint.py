@@ -11,10 +11,13 @@ reference's converter writes and its loader reads:
   [N, K] followed by f32 scales [N, ceil(K/group)] at scales_offset
   (tools/convert_hf.py:594-649 pack_file; loader.js:455-525 uploadTensors,
   with its shape, alignment and size checks and its error messages);
-* block tensor names and shapes of loader.js:543-565 fullAttnBlockShapes.
+* block tensor names and shapes of loader.js:543-590 (fullAttnBlockShapes,
+  with a hybrid checkpoint's attn_gate / q_norm / k_norm, and
+  linearAttnBlockShapes for its Gated DeltaNet blocks), and the MTP head's
+  file (loader.js:628-638 loadMtp).
 
-Only q8 checkpoints of full-attention blocks load here (this build's matmuls
-read q8 weights). The reference's converter writes group 64 with f32 scales
+Only q8 checkpoints load here (this build's matmuls read q8 weights); norms,
+conv weights and gate parameters are f32 as the converter writes them. The reference's converter writes group 64 with f32 scales
 (convert_hf.py:493); cc_upload repeats each scale over its 32-wide groups,
 which is exact, and rounds the scale to f16, the device's scale format.
 """
@@ -26,7 +29,12 @@ import numpy as np
 
 # cc_upload tensor ids (include/ccdecode.h), by the checkpoint's names.
 TENSOR = {"q_proj": 0, "k_proj": 1, "v_proj": 2, "o_proj": 3, "gate_proj": 4, "up_proj": 5, "down_proj": 6,
-          "input_layernorm": 7, "post_attention_layernorm": 8, "wte": 9, "norm": 10, "lm_head": 11}
+          "input_layernorm": 7, "post_attention_layernorm": 8, "wte": 9, "norm": 10, "lm_head": 11,
+          "attn_gate": 12, "q_norm": 13, "k_norm": 14, "in_proj_q": 15, "in_proj_k": 16, "in_proj_v": 17,
+          "in_proj_z": 18, "in_proj_b": 19, "in_proj_a": 20, "conv1d_q": 21, "conv1d_k": 22, "conv1d_v": 23,
+          "gate_params": 24, "gated_norm": 25, "out_proj": 26, "enorm": 27, "hnorm": 28, "fc_e": 29, "fc_h": 30,
+          "mtp_norm": 31, "embed_draft": 32, "head_draft": 33}
+LAYER_MTP = -2
 
 
 def load_manifest(path):
@@ -46,7 +54,17 @@ def dims_from_manifest(m):
              head_dim=m["head_dim"], ffn=m["ffn"], vocab=m["vocab"],
              rms_eps=m.get("rms_eps", 1e-5), rope_theta=m.get("rope_theta", 10000.0),
              tied=m.get("tied_lm_head") is not False, group_q8=32, dtype=m.get("dtype", "f32"),
-             hybrid=bool(layer_types) and len(set(layer_types)) > 1)
+             hybrid=bool(layer_types) and len(set(layer_types)) > 1, rot_dim=m.get("rot_dim", m["head_dim"]))
+    if layer_types:
+        d["layer_types"] = list(layer_types)
+    if d["hybrid"]:
+        # Gated DeltaNet's own head config (loader.js:185-195 d.linear)
+        d.update(lin_nk=m.get("linear_num_key_heads"), lin_nv=m.get("linear_num_value_heads"),
+                 lin_dk=m.get("linear_key_head_dim"), lin_dv=m.get("linear_value_head_dim"),
+                 lin_conv=m.get("linear_conv_kernel_dim"))
+    if m.get("mtp"):
+        d["mtp_vocab"] = m["mtp"]["draft_vocab"]
+        d["mtp_file"] = m["mtp"]["file"]
     if m.get("rope_scaling"):
         d["rope_scaling"] = dict(m["rope_scaling"])
     return d
@@ -66,8 +84,9 @@ def check_manifest(m, d=None):
         problems.append(f"act {m['act']}, but only silu/SwiGLU is implemented")
     if d["dtype"] != "q8":
         problems.append(f"dtype {d['dtype']}, but this build's matmuls read q8 weights")
-    if d["hybrid"]:
-        problems.append("linear_attention (Gated DeltaNet) blocks are not built here")
+    if d["hybrid"] and (not d.get("lin_nk") or not d.get("lin_nv") or d["lin_nv"] % d["lin_nk"]):
+        problems.append(f"linear_num_value_heads ({d.get('lin_nv')}) not divisible by linear_num_key_heads "
+                        f"({d.get('lin_nk')}): l2NormalizeHeads' integer group factor needs this")
     if not d["hybrid"] and d["n_heads"] * d["head_dim"] != d["hidden"]:
         problems.append(f"n_head*head_dim ({d['n_heads'] * d['head_dim']}) != hidden ({d['hidden']})")
     if d["n_heads"] % d["n_kv_heads"] != 0:
@@ -83,12 +102,29 @@ def check_manifest(m, d=None):
     return problems
 
 
-def block_shapes(d):
-    """loader.js:543-565 fullAttnBlockShapes (non-hybrid)."""
-    H, kv, q = d["hidden"], d["n_kv_heads"] * d["head_dim"], d["n_heads"] * d["head_dim"]
-    return {"input_layernorm": [H], "q_proj": [q, H], "k_proj": [kv, H], "v_proj": [kv, H], "o_proj": [H, q],
-            "post_attention_layernorm": [H], "gate_proj": [d["ffn"], H], "up_proj": [d["ffn"], H],
-            "down_proj": [H, d["ffn"]]}
+def block_shapes(d, kind="full_attention"):
+    """loader.js:543-590 fullAttnBlockShapes (with a hybrid checkpoint's
+    attn_gate, q_norm, k_norm) / linearAttnBlockShapes."""
+    H, F = d["hidden"], d["ffn"]
+    if kind == "linear_attention":
+        kd, vd, nV = d["lin_nk"] * d["lin_dk"], d["lin_nv"] * d["lin_dv"], d["lin_nv"]
+        K4 = d["lin_conv"]
+        return {"input_layernorm": [H], "post_attention_layernorm": [H], "in_proj_q": [kd, H], "in_proj_k": [kd, H],
+                "in_proj_v": [vd, H], "in_proj_z": [vd, H], "in_proj_b": [nV, H], "in_proj_a": [nV, H],
+                "conv1d_q": [kd, K4], "conv1d_k": [kd, K4], "conv1d_v": [vd, K4], "gate_params": [2 * nV],
+                "gated_norm": [d["lin_dv"]], "out_proj": [H, vd], "gate_proj": [F, H], "up_proj": [F, H],
+                "down_proj": [H, F]}
+    kv, q = d["n_kv_heads"] * d["head_dim"], d["n_heads"] * d["head_dim"]
+    out = {"input_layernorm": [H], "q_proj": [q, H], "k_proj": [kv, H], "v_proj": [kv, H], "o_proj": [H, q],
+           "post_attention_layernorm": [H], "gate_proj": [F, H], "up_proj": [F, H], "down_proj": [H, F]}
+    if d.get("hybrid"):
+        out.update(attn_gate=[q, H], q_norm=[d["head_dim"]], k_norm=[d["head_dim"]])
+    return out
+
+
+def kind_of(d, index):
+    lt = d.get("layer_types")
+    return lt[index] if lt else "full_attention"
 
 
 def read_tensors(path, filename, entries, expected, strict=True):
@@ -140,7 +176,16 @@ def block_file(index):
 def load_block(path, m, d, index):
     """loader.js:610-626 loadBlock: block `index` (model numbering)."""
     fn = block_file(index)
-    return read_tensors(path, fn, m["files"][fn], block_shapes(d))
+    return read_tensors(path, fn, m["files"][fn], block_shapes(d, kind_of(d, index)))
+
+
+def load_mtp(path, m, d):
+    """loader.js:628-638 loadMtp: the MTP head's full-attention block and its
+    enorm, hnorm, fc_e, fc_h, mtp_norm, embed_draft, head_draft."""
+    fn, H, V = d["mtp_file"], d["hidden"], d["mtp_vocab"]
+    shapes = dict(block_shapes(d), enorm=[H], hnorm=[H], fc_e=[H, H], fc_h=[H, H], mtp_norm=[H],
+                  embed_draft=[V, H], head_draft=[V, H])
+    return read_tensors(path, fn, m["files"][fn], shapes)
 
 
 def load_client(path, m, d):
@@ -185,3 +230,8 @@ def upload(ctx, path, m=None, d=None):
     for pos in range(max(lo, 1), min(hi, last)):
         for name, t in load_block(path, m, d, pos - 1).items():
             put(pos - 1, name, t)
+    if hi - 1 == last and d.get("mtp_vocab"):
+        # the MTP head, held with the LM head (stage.js:273-289)
+        head = {"enorm", "hnorm", "fc_e", "fc_h", "mtp_norm", "embed_draft", "head_draft"}
+        for name, t in load_mtp(path, m, d).items():
+            put(-1 if name in head else LAYER_MTP, name, t)

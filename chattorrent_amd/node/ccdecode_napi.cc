@@ -9,6 +9,7 @@
 #define NAPI_VERSION 8
 #include <node_api.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <string>
@@ -62,6 +63,22 @@ double num(napi_env env, napi_value obj, const char* name, double dflt) {
     double d = dflt;
     napi_get_value_double(env, v, &d);
     return d;
+}
+
+// A flag given as a boolean or a number.
+bool flag(napi_env env, napi_value obj, const char* name) {
+    napi_value v;
+    if (!get_prop(env, obj, name, &v)) return false;
+    napi_valuetype t;
+    napi_typeof(env, v, &t);
+    if (t == napi_boolean) {
+        bool b = false;
+        napi_get_value_bool(env, v, &b);
+        return b;
+    }
+    double d = 0;
+    napi_get_value_double(env, v, &d);
+    return d != 0;
 }
 
 Ctx* unwrap(napi_env env, napi_value v) {
@@ -118,6 +135,43 @@ napi_value Create(napi_env env, napi_callback_info info) {
     d.rms_eps = (float)num(env, argv[0], "rms_eps", 1e-5);
     d.rope_theta = num(env, argv[0], "rope_theta", 10000.0);
     d.tied = num(env, argv[0], "tied", 1) != 0;
+    {
+        napi_value tv;   // a boolean `tied` too
+        napi_valuetype t = napi_undefined;
+        if (get_prop(env, argv[0], "tied", &tv)) napi_typeof(env, tv, &t);
+        if (t == napi_boolean) d.tied = flag(env, argv[0], "tied");
+    }
+    // hybrid checkpoints (loader.js dimsFromManifest): rot_dim, hybrid,
+    // layer_types (strings), linear {nK, nV, Dk, Dv, K4}, mtp {draftVocab}
+    d.rot_dim = (int32_t)num(env, argv[0], "rot_dim", 0);
+    d.hybrid = flag(env, argv[0], "hybrid");
+    std::vector<uint8_t> kinds;
+    napi_value lt;
+    if (get_prop(env, argv[0], "layer_types", &lt)) {
+        bool arr = false;
+        napi_is_array(env, lt, &arr);
+        uint32_t n = 0;
+        if (arr) napi_get_array_length(env, lt, &n);
+        for (uint32_t i = 0; i < n; i++) {
+            napi_value e;
+            napi_get_element(env, lt, i, &e);
+            char buf[32] = {0};
+            size_t len = 0;
+            napi_get_value_string_utf8(env, e, buf, sizeof buf, &len);
+            kinds.push_back(std::string(buf) == "linear_attention" ? CC_LINEAR_ATTENTION : CC_FULL_ATTENTION);
+        }
+        if ((int)kinds.size() == d.n_layer) d.layer_kinds = kinds.data();
+    }
+    napi_value lin;
+    if (get_prop(env, argv[0], "linear", &lin)) {
+        d.lin_nk = (int32_t)num(env, lin, "nK", 0);
+        d.lin_nv = (int32_t)num(env, lin, "nV", 0);
+        d.lin_dk = (int32_t)num(env, lin, "Dk", 0);
+        d.lin_dv = (int32_t)num(env, lin, "Dv", 0);
+        d.lin_conv = (int32_t)num(env, lin, "K4", 0);
+    }
+    napi_value mtp;
+    if (get_prop(env, argv[0], "mtp", &mtp)) d.mtp_vocab = (int32_t)num(env, mtp, "draftVocab", 0);
     napi_value rs;
     if (get_prop(env, argv[0], "rope_scaling", &rs)) {
         d.rope_scaling = 1;
@@ -337,6 +391,14 @@ napi_value Step(napi_env env, napi_callback_info info) {
         jb.past = (int32_t)num(env, o, "past", 0);
         jb.n = (int32_t)num(env, o, "n", 0);
         jb.sampled = (int32_t)num(env, o, "sampled", 0);
+        // speculation through linear_attention blocks, and the MTP fill
+        jb.snap = flag(env, o, "snap");
+        napi_value kv;
+        if (get_prop(env, o, "keep", &kv)) {
+            jb.rollback = 1;
+            jb.keep = (int32_t)num(env, o, "keep", 0);
+        }
+        jb.mtp = flag(env, o, "mtp");
         napi_value v;
         void* data;
         size_t len;
@@ -423,6 +485,30 @@ napi_value ReadLogits(napi_env env, napi_callback_info info) {
     return copy_out(env, out, napi_float32_array);
 }
 
+// mtpDraft(ctx, slot, row, token, pos, k) -> Uint32Array [k]: cc_mtp_draft
+// (Runner.#mtpAfter, stage.js:296-320).
+napi_value MtpDraft(napi_env env, napi_callback_info info) {
+    size_t argc = 6;
+    napi_value argv[6];
+    NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
+    if (argc < 6) {
+        napi_throw_type_error(env, nullptr, "mtpDraft(ctx, slot, row, token, pos, k)");
+        return nullptr;
+    }
+    Ctx* c = unwrap(env, argv[0]);
+    if (!c) return nullptr;
+    int32_t a[5] = {0, 0, 0, 0, 0};
+    for (int i = 0; i < 5; i++) napi_get_value_int32(env, argv[1 + i], &a[i]);
+    std::vector<uint32_t> out((size_t)std::max(a[4], 1));
+    const cc_status st = cc_mtp_draft(c->ctx, a[0], a[1], a[2], a[3], a[4], out.data());
+    if (st != CC_OK) {
+        throw_status(env, st, cc_last_error(c->ctx));
+        return nullptr;
+    }
+    out.resize((size_t)std::max(a[4], 0));
+    return copy_out(env, out, napi_uint32_array);
+}
+
 napi_value Stats(napi_env env, napi_callback_info info) {
     size_t argc = 1;
     napi_value argv[1];
@@ -462,7 +548,8 @@ napi_value Init(napi_env env, napi_value exports) {
         {"create", Create},         {"destroy", Destroy},     {"fillRandom", FillRandom},
         {"fillRandomKV", FillRandomKV}, {"upload", Upload},   {"step", Step},
         {"release", Release},       {"slotPages", SlotPages}, {"freePages", FreePages},
-        {"readLogits", ReadLogits}, {"stats", Stats},         {"lastError", LastError}};
+        {"readLogits", ReadLogits}, {"stats", Stats},         {"lastError", LastError},
+        {"mtpDraft", MtpDraft}};
     for (const auto& f : fns) {
         napi_value fn;
         napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.fn, nullptr, &fn);

@@ -5,10 +5,10 @@
 //
 // A checkpoint is `manifest.json` plus concatenated-tensor files:
 // block_NN.bin per block, client.bin (wte, norm) and, when the head is
-// untied, lm_head.bin. A q8 entry is an int8 block [N, K] followed by f32
-// scales [N, ceil(K/group)] (tools/convert_hf.py:594-649 pack_file); norms are
-// f32. Only q8 checkpoints of full-attention blocks load (this build's
-// matmuls read q8). cc_upload repeats a group-64 scale over both 32-wide
+// untied, lm_head.bin; a hybrid checkpoint's MTP head in its own file. A q8
+// entry is an int8 block [N, K] followed by f32 scales [N, ceil(K/group)]
+// (tools/convert_hf.py:594-649 pack_file); norms, conv weights and gate
+// parameters are f32. Only q8 checkpoints load (this build's matmuls read q8). cc_upload repeats a group-64 scale over both 32-wide
 // groups, which is exact, and keeps scales as f16.
 //
 // Node 12 syntax: no ?? / ?. / #private.
@@ -47,6 +47,19 @@ function dimsFromManifest(m) {
         layer_types: layerTypes,
         hybrid: !!layerTypes && new Set(layerTypes).size > 1,
         rot_dim: def(m.rot_dim, m.head_dim),
+        // the MTP draft head's file and draft rows (loader.js:181-184)
+        mtp: m.mtp ? { file: m.mtp.file, draftVocab: m.mtp.draft_vocab } : undefined,
+        // Gated DeltaNet's head config (loader.js:185-195)
+        linear: layerTypes && new Set(layerTypes).size > 1 ? {
+            nK: m.linear_num_key_heads,
+            nV: m.linear_num_value_heads,
+            Dk: m.linear_key_head_dim,
+            Dv: m.linear_value_head_dim,
+            K4: m.linear_conv_kernel_dim,
+            keyDim: m.linear_num_key_heads * m.linear_key_head_dim,
+            valueDim: m.linear_num_value_heads * m.linear_value_head_dim,
+            group: m.linear_num_value_heads / m.linear_num_key_heads,
+        } : undefined,
     };
 }
 
@@ -60,7 +73,9 @@ function checkManifest(m, d) {
     if (m.norm && m.norm !== 'rmsnorm') problems.push(`norm ${m.norm}, but only rmsnorm is implemented`);
     if (m.act && m.act !== 'silu') problems.push(`act ${m.act}, but only silu/SwiGLU is implemented`);
     if (d.dtype !== 'q8') problems.push(`dtype ${d.dtype}, but this build's matmuls read q8 weights`);
-    if (d.hybrid) problems.push('linear_attention (Gated DeltaNet) blocks are not built here');
+    if (d.hybrid && d.linear.nV % d.linear.nK !== 0)
+        problems.push(`linear_num_value_heads (${d.linear.nV}) not divisible by ` +
+            `linear_num_key_heads (${d.linear.nK}): l2NormalizeHeads' integer group factor needs this`);
     if (!d.hybrid && d.n_heads * d.head_dim !== d.hidden)
         problems.push(`n_head*head_dim (${d.n_heads * d.head_dim}) != hidden (${d.hidden})`);
     if (d.n_heads % d.n_kv_heads !== 0)
@@ -75,10 +90,22 @@ function checkManifest(m, d) {
     return problems;
 }
 
-// loader.js:543-565 fullAttnBlockShapes (non-hybrid).
-function blockShapes(d) {
+// loader.js:543-590: fullAttnBlockShapes (a hybrid checkpoint's full blocks
+// also carry attn_gate, q_norm, k_norm) and linearAttnBlockShapes.
+function blockShapes(d, kind) {
     const H = d.hidden, kvDim = d.n_kv_heads * d.head_dim, qDim = d.n_heads * d.head_dim;
-    return {
+    if (kind === 'linear_attention') {
+        const { keyDim, valueDim, nV, Dv, K4 } = d.linear;
+        return {
+            input_layernorm: [H], post_attention_layernorm: [H],
+            in_proj_q: [keyDim, H], in_proj_k: [keyDim, H], in_proj_v: [valueDim, H], in_proj_z: [valueDim, H],
+            in_proj_b: [nV, H], in_proj_a: [nV, H],
+            conv1d_q: [keyDim, K4], conv1d_k: [keyDim, K4], conv1d_v: [valueDim, K4],
+            gate_params: [2 * nV], gated_norm: [Dv], out_proj: [H, valueDim],
+            gate_proj: [d.ffn, H], up_proj: [d.ffn, H], down_proj: [H, d.ffn],
+        };
+    }
+    const shapes = {
         input_layernorm: [H],
         q_proj: [qDim, H],
         k_proj: [kvDim, H],
@@ -89,7 +116,15 @@ function blockShapes(d) {
         up_proj: [d.ffn, H],
         down_proj: [H, d.ffn],
     };
+    if (d.hybrid) {
+        shapes.attn_gate = [qDim, H];
+        shapes.q_norm = [d.head_dim];
+        shapes.k_norm = [d.head_dim];
+    }
+    return shapes;
 }
+
+const kindOf = (d, index) => (d.layer_types && d.layer_types[index]) || 'full_attention';
 
 // uploadTensors (loader.js:455-525) without the device: the expected tensors
 // of one file as host views, with its shape, alignment and size checks and
@@ -151,7 +186,17 @@ const blockFile = (index) => `block_${String(index).padStart(2, '0')}.bin`;
 // loader.js:610-626 loadBlock: block `index` (model numbering).
 function loadBlock(dir, m, d, index) {
     const fn = blockFile(index);
-    return readTensors(readFile(dir, fn), m.files[fn], fn, blockShapes(d));
+    return readTensors(readFile(dir, fn), m.files[fn], fn, blockShapes(d, kindOf(d, index)));
+}
+
+// loader.js:628-638 loadMtp: the MTP head's block and its own tensors, for
+// Runner.attachMtp.
+function loadMtp(dir, m, d) {
+    if (!d.mtp) throw new Error('the checkpoint has no MTP head');
+    const fn = d.mtp.file, H = d.hidden, V = d.mtp.draftVocab;
+    const shapes = Object.assign({}, blockShapes(d), { enorm: [H], hnorm: [H], fc_e: [H, H], fc_h: [H, H],
+                                                       mtp_norm: [H], embed_draft: [V, H], head_draft: [V, H] });
+    return readTensors(readFile(dir, fn), m.files[fn], fn, shapes);
 }
 
 // loader.js:644-671 loadClient: wte and norm, and lm_head when untied.
@@ -174,4 +219,4 @@ function weightsFor(dir, m, d, p, client) {
 }
 
 module.exports = { loadManifest, dimsFromManifest, checkManifest, blockShapes, readTensors, loadBlock, loadClient,
-                   weightsFor, blockFile };
+                   loadMtp, weightsFor, blockFile };

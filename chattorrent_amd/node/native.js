@@ -37,6 +37,8 @@ class NativeBackend {
     slotPages(slot) { return load().slotPages(this.ctx, slot); }
     freePages() { return load().freePages(this.ctx); }
     readLogits(rows) { return load().readLogits(this.ctx, rows); }
+    // cc_mtp_draft: keep `row` of the last pass, chain k drafts after `token`
+    mtpDraft(slot, row, token, pos, k) { return load().mtpDraft(this.ctx, slot, row, token, pos, k); }
     fillRandom(seed) { load().fillRandom(this.ctx, seed); }
     fillRandomKV(slot, tokens, seed, key) { load().fillRandomKV(this.ctx, slot, tokens, seed, key); }
     upload(layer, tensor, data, scales, group) {

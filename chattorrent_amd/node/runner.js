@@ -28,9 +28,21 @@ const WARMUP = '\0warmup';       // stage.js:31
 
 // cc_upload tensor ids (include/ccdecode.h) by HF tensor name.
 const TENSOR = { q_proj: 0, k_proj: 1, v_proj: 2, o_proj: 3, gate_proj: 4, up_proj: 5, down_proj: 6,
-                 input_layernorm: 7, post_attention_layernorm: 8, wte: 9, norm: 10, lm_head: 11 };
+                 input_layernorm: 7, post_attention_layernorm: 8, wte: 9, norm: 10, lm_head: 11,
+                 attn_gate: 12, q_norm: 13, k_norm: 14, in_proj_q: 15, in_proj_k: 16, in_proj_v: 17,
+                 in_proj_z: 18, in_proj_b: 19, in_proj_a: 20, conv1d_q: 21, conv1d_k: 22, conv1d_v: 23,
+                 gate_params: 24, gated_norm: 25, out_proj: 26, enorm: 27, hnorm: 28, fc_e: 29, fc_h: 30,
+                 mtp_norm: 31, embed_draft: 32, head_draft: 33 };
+const LAYER_MTP = -2;
 const BLOCK_TENSORS = ['q_proj', 'k_proj', 'v_proj', 'o_proj', 'gate_proj', 'up_proj', 'down_proj',
                        'input_layernorm', 'post_attention_layernorm'];
+// a hybrid checkpoint's full-attention extras, and its linear_attention
+// blocks' tensors (loader.js:543-590)
+const HYBRID_FULL = ['attn_gate', 'q_norm', 'k_norm'];
+const LINEAR_TENSORS = ['in_proj_q', 'in_proj_k', 'in_proj_v', 'in_proj_z', 'in_proj_b', 'in_proj_a', 'conv1d_q',
+                        'conv1d_k', 'conv1d_v', 'gate_params', 'gated_norm', 'out_proj', 'gate_proj', 'up_proj',
+                        'down_proj', 'input_layernorm', 'post_attention_layernorm'];
+const MTP_TENSORS = ['enorm', 'hnorm', 'fc_e', 'fc_h', 'mtp_norm', 'embed_draft', 'head_draft'];
 
 // Thrown by _cacheFor for a job that must wait for a frame; never escapes.
 const WAIT = new Error('waiting for a session frame');
@@ -100,7 +112,18 @@ class Runner {
         this.decoded = false;
         this.warmups = 0;
         this.counts = { admitted: 0, evicted: 0, released: 0, refused: 0, cold: 0, waited: 0,
-                        batched: 0, batchedJobs: 0 };
+                        batched: 0, batchedJobs: 0, nospec: 0 };
+        // speculative decoding's replay slots (stage.js:222-228): the device
+        // keeps every session's replay data, so a slot here is the lease that
+        // bounds how many sessions speculate through linear_attention blocks
+        this.specSlots = o.specSlots === undefined ? this.slots : o.specSlots;
+        this.specLive = new Set();
+        this.mtp = null;
+    }
+
+    _kind(b) {
+        const lt = this.d.layer_types;
+        return lt && lt[b] ? lt[b] : 'full_attention';
     }
 
     holds(pos) { return pos >= this.lo && pos < this.have; }
@@ -127,14 +150,64 @@ class Runner {
             if (w.lm_head) up(-1, TENSOR.lm_head, w.lm_head);
             else if (w.wte) up(-1, TENSOR.wte, w.wte);
         } else {
-            if (!w.q_proj) throw new Error(`position ${p} is a block and needs its tensors`);
-            for (const name of BLOCK_TENSORS) {
+            const linear = this._kind(p - 1) === 'linear_attention';
+            const names = linear ? LINEAR_TENSORS : this.d.hybrid ? BLOCK_TENSORS.concat(HYBRID_FULL) : BLOCK_TENSORS;
+            if (!w[linear ? 'in_proj_q' : 'q_proj']) throw new Error(`position ${p} is a block and needs its tensors`);
+            for (const name of names) {
                 if (!w[name]) throw new Error(`position ${p} is a block and needs ${name}`);
                 up(p - 1, TENSOR[name], w[name]);
             }
         }
         this.have = p + 1;
         return this.have;
+    }
+
+    // attachMtp(m) — stage.js:273-289: the MTP head (loader.js loadMtp's
+    // tensors: its full-attention block's, enorm, hnorm, fc_e, fc_h,
+    // mtp_norm, embed_draft, head_draft), held with the LM head. The
+    // backend was created with d.mtp set, which sizes its KV and scratch.
+    attachMtp(m) {
+        if (this.hi !== positions(this.d.n_layer)) throw new Error('the MTP head is held with the LM head');
+        if (!this.d.mtp) throw new Error('the model dims carry no mtp head');
+        const up = (layer, id, t) => this.backend.upload(layer, id, t.codes || t, t.codes ? t.scales : null,
+                                                         t.codes ? t.group : undefined);
+        const names = this.d.hybrid ? BLOCK_TENSORS.concat(HYBRID_FULL) : BLOCK_TENSORS;
+        for (const name of names) {
+            if (!m[name]) throw new Error(`the MTP head needs ${name}`);
+            up(LAYER_MTP, TENSOR[name], m[name]);
+        }
+        for (const name of MTP_TENSORS) {
+            if (!m[name]) throw new Error(`the MTP head needs ${name}`);
+            up(-1, TENSOR[name], m[name]);
+        }
+        this.mtp = { draftVocab: this.d.mtp.draftVocab };
+    }
+
+    // #specSlot — stage.js:336-372: the session's lease, taken on its first
+    // verify through a linear_attention block here and held until its frame
+    // goes. With every lease taken, an idle session's is taken from it (it
+    // loses its rollback, #specSteal :374-386) or the job is refused nospec.
+    _specSlot(session) {
+        if (this.specLive.has(session)) return;
+        if (this.specLive.size >= this.specSlots) {
+            let stolen = false;
+            const t = now();
+            for (const [id, frame] of this.live) {
+                if (!this.specLive.has(id) || this.pending.has(id) || t - (frame.lastUse || 0) < this.idleMs) continue;
+                this.specLive.delete(id);
+                if (frame.specAt) frame.specAt.clear();
+                frame.specLost = true;
+                stolen = true;
+                break;
+            }
+            if (!stolen) {
+                this.counts.nospec++;
+                const err = new Error(`no speculative replay slot here (${this.specSlots} in use)`);
+                err.nospec = true;
+                throw err;
+            }
+        }
+        this.specLive.add(session);
     }
 
     get vramBytes() { return this.backend.stats().vramBytes; }
@@ -304,6 +377,7 @@ class Runner {
             this.free.push(frame);
             this.counts.released++;
         }
+        this.specLive.delete(session);
         this.cuts.delete(session);
         this.logs.delete(session);
         this.refused.delete(session);
@@ -382,6 +456,7 @@ class Runner {
         this.backend.release(victim.slot);
         this.cuts.delete(id);
         this.logs.delete(id);
+        this.specLive.delete(id);
         this.counts.evicted++;
         return victim;
     }
@@ -406,30 +481,52 @@ class Runner {
             frame = this._evict(oldest);
         }
         frame.fed = new Map();
+        frame.specAt = new Map();
+        frame.specLost = false;
         frame.lastUse = now();
         this.live.set(session, frame);
         this.counts.admitted++;
         return frame;
     }
 
-    // #checkFed — stage.js:1049-1091, for full-attention blocks: a job may
-    // start at or below the rows a block holds (a rewind), never above; a
-    // closed-loop job (`auto`) must continue exactly, and one behind is stale.
-    _checkFed(session, frame, at, last, past, exact) {
+    // #checkFed — stage.js:1028-1091. A job continues where the block's last
+    // one ended: a full-attention block may be rewound (past <= fed), a
+    // recurrent (linear_attention) one only restarted (past 0). After a
+    // verify of n rows from `base`, the next job may start inside it, at
+    // (base, base + n] (or at base for a re-sent refused verify, `rb`): it
+    // keeps past - base of those rows. A closed-loop job (`auto`) must
+    // continue exactly; one behind is a duplicate (stale). Returns keep (null:
+    // nothing rolled back).
+    _checkFed(session, frame, at, last, past, exact, rb) {
+        let keep = null;
         for (let p = Math.max(at, 1); p < last; p++) {
             const b = p - 1;
             const fed = frame.fed.get(b) || 0;
-            if (past === 0 && !exact) continue;
-            if (exact ? past === fed : past <= fed) continue;
-            if (exact && past < fed) {
+            const rc = this._kind(b) === 'linear_attention';
+            const sp = frame.specAt ? frame.specAt.get(b) : undefined;
+            let k = null;
+            if (sp && fed === sp.base + sp.n && past < fed && (past > sp.base || (rb && past === sp.base))) {
+                k = past - sp.base;
+            } else if (past === 0 && !exact) {
+                continue;
+            } else if (rc || exact ? past === fed : past <= fed) {
+                continue;
+            } else if (exact && past < fed && !frame.specLost) {
                 const err = new Error(`a duplicate of session ${session}'s job at ${past} ` +
                     `(block ${b} is already at ${fed})`);
                 err.stale = true;
                 throw err;
+            } else {
+                throw this._cold(session, `session ${session} is no longer cached here ` +
+                    `(block ${b} holds ${fed} rows, the job continues from ${past})`);
             }
-            throw this._cold(session, `session ${session} is no longer cached here ` +
-                `(block ${b} holds ${fed} rows, the job continues from ${past})`);
+            if (keep !== null && keep !== k) {
+                throw this._cold(session, `session ${session}'s blocks disagree on a rollback ` +
+                    `(${keep} and ${k} rows)`);
+            }
+            keep = k;
         }
+        return keep;
     }
 
     // #pagesFor — stage.js:1096-1120: pages for `tokens` positions, evicting
@@ -562,8 +659,24 @@ class Runner {
         }
         const frame = this._cacheFor(h.s, h.past);
         const first = Math.max(at, 1), last = Math.min(to, d.n_layer + 1);
-        if (h.s !== WARMUP) this._checkFed(h.s, frame, at, last, h.past, !!h.auto);
-        this._pagesFor(h.s, frame, h.past + T);
+        const keep = h.s !== WARMUP ? this._checkFed(h.s, frame, at, last, h.past, !!h.auto, !!h.rb) : null;
+        // the replay lease, when a linear_attention block here snapshots (a
+        // verify) or rolls back (the job after one), taken before anything
+        // changes so a nospec refusal leaves the session as it was
+        let linear = false;
+        for (let q = first; q < last; q++) {
+            if (this._kind(q - 1) === 'linear_attention') { linear = true; break; }
+        }
+        if (linear && keep !== null && !this.specLive.has(h.s)) {
+            this.counts.cold++;
+            throw new Error(`session ${h.s} has no replay data here to roll back`);
+        }
+        if (linear && verify) this._specSlot(h.s);
+        // the MTP head (stage.js:1287-1293): its KV is filled from a job
+        // that carries its ids; the head takes pages for the drafts too
+        const mtp = (head || filling) && !!this.mtp && !!h.mtp && h.s !== WARMUP;
+        const fill = mtp && Array.isArray(h.ids) && h.ids.length === T;
+        this._pagesFor(h.s, frame, mtp && head ? Math.min(this.nMax, h.past + T + SPEC_COLS) : h.past + T);
         const sampled = head && !spent ? (verify ? T : 1) : 0;
         const optsOf = (i) => (i === 0 ? h.opts : ((h.rowOpts && h.rowOpts[i - 1]) || h.opts));
         let M = sampled ? 0 : null;
@@ -572,7 +685,7 @@ class Runner {
             M = m === null ? null : Math.max(M, m);
         }
         return { h, bits, T, at, to, first, last, head, filling, spent, gather, verify, drafts,
-                 frame, sampled, optsOf, M };
+                 frame, sampled, optsOf, M, keep, linear, mtp, fill };
     }
 
     // #pass — stage.js:1314-1481: one packed pass on the backend.
@@ -594,8 +707,11 @@ class Runner {
         }
         const jobs = plans.map((p) => ({
             slot: p.frame.slot, past: p.h.past, n: p.T, sampled: p.sampled,
-            ids: p.gather ? Int32Array.from(p.h.ids) : undefined,
+            ids: p.gather || p.fill ? Int32Array.from(p.h.ids) : undefined,
             hidden: p.gather ? undefined : p.bits,
+            snap: p.linear && p.verify ? 1 : 0,
+            keep: p.linear && p.keep !== null ? p.keep : undefined,
+            mtp: p.fill ? 1 : 0,
         }));
         const t1 = now();
         const res = await this.backend.step(jobs, p0.at, p0.to, sampled ? (M || 1) : 1);
@@ -611,7 +727,11 @@ class Runner {
                 for (let q = p.first; q < p.last; q++) this.warm.fed.set(q - 1, p.h.past + p.T);
                 continue;
             }
-            for (let q = p.first; q < p.last; q++) p.frame.fed.set(q - 1, p.h.past + p.T);
+            for (let q = p.first; q < p.last; q++) {
+                p.frame.fed.set(q - 1, p.h.past + p.T);
+                if (p.verify) p.frame.specAt.set(q - 1, { base: p.h.past, n: p.T });
+                else p.frame.specAt.delete(q - 1);
+            }
         }
         if (p0.spent) return plans.map(() => ({ value: { at: p0.to } }));
         // A sampler that needs whole rows reads the logits back (the
@@ -647,6 +767,17 @@ class Runner {
             for (let m = 0; m < M; m++) { v.push(pass.res.vals[r * M + m]); c.push(pass.res.ids[r * M + m]); }
             return sampleFromCandidates(c, v, optsOf(i), d.vocab);
         };
+        // #mtpAfter (stage.js:296-320): after sampling t from row a, keep that
+        // row for the session and, for a loop job with speculation on, chain
+        // up to SPEC_COLS - 1 drafts after t
+        const mtpAfter = (a, t) => {
+            if (!p.mtp) return null;
+            const pos = h.past + a + 1;
+            const K = h.loop && h.loop.spec && t < this.mtp.draftVocab
+                ? Math.max(0, Math.min(SPEC_COLS - 1, this.nMax - pos - 1)) : 0;
+            const ids = this.backend.mtpDraft(p.frame.slot, p.rowOff + a, t, pos, K);
+            return K > 0 ? Array.from(ids) : null;
+        };
         if (head && verify) {
             const tokens = [];
             for (let i = 0; i < T; i++) {
@@ -655,14 +786,23 @@ class Runner {
                 if (i === T - 1 || t !== drafts[i]) break;
             }
             phases.sample = ms(tf, now());
+            const token = tokens[tokens.length - 1];
+            const next = mtpAfter(tokens.length - 1, token);
+            if (p.mtp) phases.mtp = ms(tf, now()) - phases.sample;
             timed();
-            return { at: to, token: tokens[tokens.length - 1], tokens, phases };
+            const out = { at: to, token, tokens, phases };
+            if (next) out.mtp = next;
+            return out;
         }
         if (head) {
             const token = sampleRow(0);
             phases.sample = ms(tf, now());
+            const next = mtpAfter(T - 1, token);
+            if (p.mtp) phases.mtp = ms(tf, now()) - phases.sample;
             timed();
-            return { at: to, token, phases };
+            const out = { at: to, token, phases };
+            if (next) out.mtp = next;
+            return out;
         }
         const bits = pass.res.hidden.subarray(p.rowOff * H, (p.rowOff + T) * H).slice();
         this._log(h.s, to, h.past, bits);
@@ -685,4 +825,4 @@ class Runner {
     }
 }
 
-module.exports = { Runner, WARMUP, MAX_QUEUE, MAX_SESSION_QUEUE, SPEC_COLS, PAGE_TOKENS, positions };
+module.exports = { Runner, WARMUP, MAX_QUEUE, MAX_SESSION_QUEUE, SPEC_COLS, PAGE_TOKENS, positions, TENSOR, LAYER_MTP };

@@ -82,3 +82,57 @@ def make(path, d, seed=11, group=64):
     with open(os.path.join(path, "manifest.json"), "w") as f:
         json.dump(manifest, f, indent=2)
     return written
+
+
+# tests/hybrid_weights.py names -> the checkpoint's (loader.js:543-590, 628-638)
+HYBRID_NAMES = {"ln1": "input_layernorm", "ln2": "post_attention_layernorm", "q": "q_proj", "k": "k_proj",
+                "v": "v_proj", "o": "o_proj", "gate": "gate_proj", "up": "up_proj", "down": "down_proj",
+                "attn_gate": "attn_gate", "q_norm": "q_norm", "k_norm": "k_norm", "in_q": "in_proj_q",
+                "in_k": "in_proj_k", "in_v": "in_proj_v", "in_z": "in_proj_z", "in_b": "in_proj_b", "in_a": "in_proj_a",
+                "out": "out_proj", "gate_params": "gate_params", "gated_norm": "gated_norm"}
+
+
+def _block_tensors(lw, kd):
+    out = []
+    for k, t in lw.items():
+        if k == "kind":
+            continue
+        if k == "conv":   # the converter splits conv1d into the q, k, v channel ranges
+            out += [("conv1d_q", t[:kd]), ("conv1d_k", t[kd:2 * kd]), ("conv1d_v", t[2 * kd:])]
+            continue
+        out.append((HYBRID_NAMES[k], (t[0], t[1], 32) if isinstance(t, tuple) else t))
+    return out
+
+
+def make_hybrid(path, d, w, wm=None):
+    """A hybrid (Qwen3.5-layout) q8 checkpoint of tests/hybrid_weights.py's
+    weights `w` (and MTP head `wm`) at group 32: layer_types, the
+    linear_num_* keys, rot_dim, and the MTP file in the manifest."""
+    os.makedirs(path, exist_ok=True)
+    kd = d["lin_nk"] * d["lin_dk"]
+    manifest = {"model": "synthetic-hybrid", "arch": "qwen3_5", "hidden": d["hidden"], "n_layer": d["n_layer"],
+                "n_head": d["n_heads"], "n_kv_head": d["n_kv_heads"], "head_dim": d["head_dim"],
+                "group": d["n_heads"] // d["n_kv_heads"], "ffn": d["ffn"], "vocab": d["vocab"], "n_pos": 2048,
+                "rms_eps": d["rms_eps"], "rope_theta": d["rope_theta"], "rot_dim": d["rot_dim"],
+                "layer_types": d["layer_types"], "linear_num_key_heads": d["lin_nk"],
+                "linear_num_value_heads": d["lin_nv"], "linear_key_head_dim": d["lin_dk"],
+                "linear_value_head_dim": d["lin_dv"], "linear_conv_kernel_dim": d["lin_conv"],
+                "norm": "rmsnorm", "act": "silu", "dtype": "q8", "weight_layout": "out_in",
+                "tied_lm_head": d.get("tied", True), "files": {}}
+    for i, lw in enumerate(w["layers"]):
+        fn = f"block_{i:02d}.bin"
+        manifest["files"][fn] = pack_file(path, fn, _block_tensors(lw, kd))
+    manifest["files"]["client.bin"] = pack_file(path, "client.bin",
+                                                [("wte", (*w["wte"], 32)), ("norm", w["norm"])])
+    if not d.get("tied", True):
+        manifest["files"]["lm_head.bin"] = pack_file(path, "lm_head.bin", [("lm_head", (*w["lm_head"], 32))])
+    if wm is not None:
+        ts = _block_tensors(wm["block"], kd)
+        for k in ("enorm", "hnorm", "mtp_norm"):
+            ts.append((k, wm[k]))
+        for k in ("fc_e", "fc_h", "embed_draft", "head_draft"):
+            ts.append((k, (*wm[k], 32)))
+        manifest["files"]["mtp.bin"] = pack_file(path, "mtp.bin", ts)
+        manifest["mtp"] = {"file": "mtp.bin", "draft_vocab": int(wm["embed_draft"][0].shape[0])}
+    with open(os.path.join(path, "manifest.json"), "w") as f:
+        json.dump(manifest, f, indent=2)

@@ -281,6 +281,68 @@ test('f16 hand-off: every half round-trips, ties go to even, ±65504 clamps', as
     assert.strictEqual(toF16([-1e9])[0], 0xfbff);
 });
 
+// A hybrid model: block 0 linear_attention, block 1 full_attention, with an
+// MTP head (stage.js:1028-1090 rollback, :296-320 drafting).
+const DH = Object.assign({}, D, { hybrid: true, layer_types: ['linear_attention', 'full_attention'],
+                                  mtp: { draftVocab: 64 } });
+function makeHybrid(o) {
+    const opts = Object.assign({ lo: 0, hi: END, nMax: 512, tMax: 16, slots: 3, sessions: 3, idleMs: 50,
+                                 waitMs: 0, batchRows: 16 }, o || {});
+    const be = new StubBackend(DH, { nMax: opts.nMax, slots: opts.slots, frames: opts.sessions + 1, tMax: opts.tMax });
+    const r = new Runner(be, DH, opts);
+    r.mtp = { draftVocab: 64 };   // as attachMtp leaves it (its uploads are not part of this test)
+    return { r, be };
+}
+
+test('hybrid: a verify snapshots; the next job inside it rolls back and keeps past - base rows', async () => {
+    const { r, be } = makeHybrid();
+    await r.run(job('a', { n: 4, ids: [1, 2, 3, 4] }));
+    assert.strictEqual(be.spec[0].snap, 0);
+    await r.run(job('a', { past: 4, n: 3, ids: [9, 9, 9], drafts: [9, 9] }));   // a verify of 3 rows from 4
+    assert.strictEqual(be.spec[0].snap, 1);
+    await r.run(job('a', { past: 6, n: 1, ids: [7] }));                         // keeps 2 of the 3
+    assert.strictEqual(be.spec[0].keep, 2);
+    assert.strictEqual(be.spec[0].snap, 0);
+    await r.run(job('a', { past: 7, n: 1, ids: [7] }));                         // a plain continuation
+    assert.strictEqual(be.spec[0].keep, undefined);
+});
+
+test('hybrid: a recurrent block cannot be rewound (cold), a restart at 0 is fine', async () => {
+    const { r } = makeHybrid();
+    await r.run(job('a', { n: 5, ids: [1, 2, 3, 4, 5] }));
+    await rejects(r.run(job('a', { past: 3, n: 1, ids: [1] })), /no longer cached here/);
+    await r.run(job('a', { past: 0, n: 2, ids: [1, 2] }));
+});
+
+test('hybrid: replay leases beyond specSlots are refused nospec; an idle session\'s is taken', async () => {
+    const { r } = makeHybrid({ specSlots: 1, idleMs: 30 });
+    await r.run(job('a', { n: 2, ids: [1, 2] }));
+    await r.run(job('b', { n: 2, ids: [1, 2] }));
+    await r.run(job('a', { past: 2, n: 2, ids: [3, 4], drafts: [4] }));
+    const e = await rejects(r.run(job('b', { past: 2, n: 2, ids: [3, 4], drafts: [4] })), /no speculative replay slot/);
+    assert.strictEqual(e.nospec, true);
+    assert.strictEqual(r.counts.nospec, 1);
+    await sleep(40);                                      // a is idle now: b takes its lease
+    await r.run(job('b', { past: 2, n: 2, ids: [3, 4], drafts: [4] }));
+    await rejects(r.run(job('a', { past: 3, n: 1, ids: [4] })), /no longer cached here/);   // a lost its rollback
+});
+
+test('MTP: an mtp job fills with its ids and, looping with spec on, drafts after the sample', async () => {
+    const { r, be } = makeHybrid();
+    const out = await r.run(job('a', { n: 3, ids: [1, 2, 3], mtp: true, loop: { spec: true } }));
+    assert.strictEqual(be.spec[0].mtp, 1);
+    const last = be.drafts[be.drafts.length - 1];
+    assert.strictEqual(last.row, 2);
+    assert.strictEqual(last.pos, 3);
+    assert.strictEqual(last.token, out.token);
+    assert.strictEqual(last.k, 7);
+    assert.deepStrictEqual(out.mtp, [1, 2, 3, 4, 5, 6, 7].map((i) => (out.token + i) % 64));
+    // without spec: the row is kept, no drafts
+    const out2 = await r.run(job('a', { past: 3, n: 1, ids: [out.token % 64], mtp: true }));
+    assert.strictEqual(be.drafts[be.drafts.length - 1].k, 0);
+    assert.strictEqual(out2.mtp, undefined);
+});
+
 (async () => {
     let failed = 0;
     for (const c of cases) {

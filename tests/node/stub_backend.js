@@ -33,10 +33,20 @@ class StubBackend {
         return out;
     }
 
+    // cc_mtp_draft: drafts t+1, t+2, ... (mod the draft rows), recorded
+    mtpDraft(slot, row, token, pos, k) {
+        this.drafts = (this.drafts || []).concat([{ slot, row, token, pos, k }]);
+        const out = new Uint32Array(k);
+        for (let i = 0; i < k; i++) out[i] = (token + 1 + i) % this.d.mtp.draftVocab;
+        return out;
+    }
+
     step(jobs, at, to, topk) {
         if (this.busy) return Promise.reject(new Error('a step is already running on this context'));
         this.busy = true;
         this.calls.push({ jobs: jobs.map((j) => ({ slot: j.slot, past: j.past, n: j.n, sampled: j.sampled })), at, to, topk });
+        // the speculation and MTP fields of each job, when set
+        this.spec = jobs.map((j) => ({ snap: j.snap || 0, keep: j.keep, mtp: j.mtp || 0 }));
         const end = to === this.d.n_layer + 2;
         const status = new Int32Array(jobs.length);
         let need = 0;

@@ -97,3 +97,30 @@ def test_manifest_is_json_the_reference_reads(ckpt):
         assert {"name", "shape", "offset", "size", "dtype"} <= set(e)
         if e["dtype"] == "q8":
             assert {"group", "scales_offset", "scales_size"} <= set(e)
+
+
+def test_hybrid_checkpoint_reads_back(tmp_path):
+    """A hybrid checkpoint (Gated DeltaNet and full blocks with the Qwen3.5
+    extras, an MTP file): dims, per-kind shapes and every tensor read back."""
+    import hybrid_weights as HW
+    d = dict(HW.SPIKE)
+    w = HW.make(d, 5)
+    wm = HW.make_mtp(d, 5, 64)
+    W.make_hybrid(str(tmp_path), d, w, wm)
+    m = C.load_manifest(str(tmp_path))
+    dd = C.dims_from_manifest(m)
+    assert C.check_manifest(m, dd) == []
+    for k in ("hybrid", "rot_dim", "lin_nk", "lin_nv", "lin_dk", "lin_dv", "lin_conv", "layer_types"):
+        assert dd[k] == d[k], k
+    assert dd["mtp_vocab"] == 64
+    blk = C.load_block(str(tmp_path), m, dd, 0)
+    assert set(blk) == set(C.block_shapes(dd, "linear_attention"))
+    kd = d["lin_nk"] * d["lin_dk"]
+    assert np.array_equal(blk["conv1d_k"], w["layers"][0]["conv"][kd:2 * kd])
+    assert np.array_equal(blk["in_proj_b"][0], w["layers"][0]["in_b"][0])
+    full = C.load_block(str(tmp_path), m, dd, 3)
+    assert {"attn_gate", "q_norm", "k_norm"} <= set(full)
+    mt = C.load_mtp(str(tmp_path), m, dd)
+    assert np.array_equal(mt["head_draft"][1], wm["head_draft"][1]) and mt["head_draft"][2] == 32
+    bad = dict(m, linear_num_value_heads=7)
+    assert any("not divisible" in p for p in C.check_manifest(bad))

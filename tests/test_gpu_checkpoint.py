@@ -104,3 +104,36 @@ def test_checkpoint_split_over_two_contexts(gpu, tmp_path):
     finally:
         for c in (whole, a, b):
             c.close()
+
+
+def test_hybrid_checkpoint_equals_direct_upload(gpu, tmp_path):
+    """A hybrid checkpoint with an MTP head (Gated DeltaNet blocks, full blocks
+    with attn_gate / q_norm / k_norm, mtp.bin) read by checkpoint.py gives the
+    same logits and drafts, bit for bit, as the same weights uploaded
+    directly (tests/hybrid_weights.py), which the oracle tests pin."""
+    import hybrid_weights as HW
+    from chattorrent_amd.ccdecode import Context
+    d = dict(HW.D256, mtp_vocab=64)
+    w = HW.make(d, 3)
+    wm = HW.make_mtp(d, 3, 64)
+    W.make_hybrid(str(tmp_path), d, w, wm)
+    m = C.load_manifest(str(tmp_path))
+    dd = C.dims_from_manifest(m)
+    rng = np.random.default_rng(8)
+    prompt = rng.integers(0, 64, 11).astype(np.int32)
+    got = []
+    for how in ("direct", "checkpoint"):
+        c = Context(d if how == "direct" else dd, n_max=512, t_max=16, slots=1)
+        try:
+            if how == "direct":
+                HW.upload(c, w, d)
+                HW.upload_mtp(c, wm, d)
+            else:
+                C.upload(c, str(tmp_path))
+            vals, ids = c.step([dict(slot=0, past=0, n=11, ids=prompt, sampled=1, mtp=True)], topk=2)
+            drafts = c.mtp_draft(0, 10, int(ids[0, 0]) % 64, 11, 4)
+            got.append((c.read_logits(1).copy(), drafts))
+        finally:
+            c.close()
+    assert np.array_equal(got[0][0].view(np.uint32), got[1][0].view(np.uint32))
+    assert np.array_equal(got[0][1], got[1][1])

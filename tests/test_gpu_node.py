@@ -83,3 +83,32 @@ def test_node_runner_loads_checkpoint(gpu, tmp_path):
         c.close()
     assert out["whole"] == hist
     assert out["split"] == hist
+
+
+@pytest.mark.gpu
+def test_node_speculative_decoding_equals_greedy(gpu, tmp_path):
+    """The JS Runner on a hybrid checkpoint with an MTP head: greedy decoding
+    with the head's drafts verified in one pass (rejected drafts rolled back
+    through the Gated DeltaNet blocks) emits exactly the tokens of plain
+    greedy decoding, for three chats at once."""
+    import ckpt_writer as W
+    import hybrid_weights as HW
+    d = dict(HW.D256)
+    w = HW.make(d, 4)
+    wm = HW.make_mtp(d, 4, d["vocab"])
+    W.make_hybrid(str(tmp_path), d, w, wm)
+    rng = np.random.default_rng(9)
+    prompts = [rng.integers(0, d["vocab"], n).tolist() for n in (5, 9, 3)]
+    cfg = {"checkpoint": str(tmp_path), "nMax": 256, "tMax": 32, "prompts": prompts, "steps": 24}
+    print("[node] running tests/node/spec_pass.js", flush=True)
+    r = subprocess.run([NODE, os.path.join(ROOT, "tests", "node", "spec_pass.js"), json.dumps(cfg)], cwd=ROOT,
+                       stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    print("[node] verifies", out["verifies"], "accepted drafts", out["accepted"], "| known drafts: verifies",
+          out["verifies2"], "accepted", out["accepted2"], flush=True)
+    assert out["spec"] == out["plain"]
+    assert out["verifies"] > 0 and out["nospec"] == 0
+    # drafts from the plain run itself (some wrong): partly and wholly accepted verifies
+    assert out["known"] == out["plain"]
+    assert out["accepted2"] > out["verifies2"]

@@ -28,7 +28,7 @@ def test_addon_exports_every_binding():
     assert r.returncode == 0, r.stdout
     assert r.stdout.strip().split(",") == sorted(
         ["create", "destroy", "fillRandom", "fillRandomKV", "upload", "step", "release", "slotPages", "freePages",
-         "readLogits", "stats", "lastError"])
+         "readLogits", "stats", "lastError", "mtpDraft"])
 
 
 def test_loader_reads_reference_checkpoint(tmp_path):
