@@ -136,6 +136,64 @@ def stream_copy_gbs(gib=2, iters=5):
     return 2.0 * n / (ms / 1000.0) / 1e9
 
 
+def hybrid_main(args):
+    """Decode over the Qwen3.8-27B hybrid shape (48 Gated DeltaNet + 16
+    full-attention blocks, untied 248320-row head): the same ragged 32-chat
+    step as the headline, on synthetic weights (the linear blocks' f32
+    parameters fixed), then the MTP head's 7-draft chain for one session."""
+    from chattorrent_amd import configs
+    from chattorrent_amd.ccdecode import Context
+    d = dict(configs.QWEN38)
+    chats = args.chats
+    pasts = contexts(chats, 128, 16384, args.seed)
+    total = args.warmup + args.steps
+    n_max = int(64 * math.ceil((pasts.max() + total + 16) / 64))
+    print(f"[bench] hybrid: creating context, {chats} chats, n_max {n_max}", file=sys.stderr, flush=True)
+    ctx = Context(d, n_max=n_max, t_max=chats, slots=chats, sessions=chats, max_jobs=chats)
+    ctx.fill_random(args.seed)
+    for s, T in enumerate(pasts):
+        ctx.fill_random_kv(s, int(T), args.seed, s + 1)
+    ids = np.random.default_rng(args.seed + 1).integers(0, 65536, chats)
+
+    def step(p, toks):
+        jobs = [dict(slot=s, past=int(p[s]), n=1, ids=[int(toks[s]) % 65536], sampled=1) for s in range(chats)]
+        _, out = ctx.step(jobs, topk=1)
+        return out[:, 0].astype(np.int64)
+
+    for _ in range(args.warmup):
+        ids = step(pasts, ids)
+        pasts = pasts + 1
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ids = step(pasts, ids)
+        pasts = pasts + 1
+    ms = (time.perf_counter() - t0) * 1000.0 / args.steps
+    ctx.profile(True)
+    ids = step(pasts, ids)
+    pasts = pasts + 1
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    # the MTP chain after the last row of session 0 (cc_mtp_draft, 7 drafts)
+    t0 = time.perf_counter()
+    reps = 10
+    for r in range(reps):
+        ctx.mtp_draft(0, 0, int(ids[0]) % 65536, int(pasts[0]), 7)
+    mtp_ms = (time.perf_counter() - t0) * 1000.0 / reps
+    st = ctx.stats()
+    line = {"metric": "hybrid decode tok/s @32 ragged chats, Qwen3.8-27B shape (48 Gated DeltaNet + 16 "
+                      "full-attention blocks), q8", "value": round(chats / (ms / 1000.0), 2), "unit": "tok/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+            "higher_is_better": True, "dtype": "int8xf32",
+            "data": "synthetic: random-init q8 weights, fixed Gated DeltaNet parameters, random int8 KV",
+            "mtp_chain_7_drafts_ms": round(mtp_ms, 3),
+            "per_kind_ms_per_step": {k: round(v[0], 4) for k, v in prof.items()},
+            "vram_gb": round(st["vram_bytes"] / 1e9, 2),
+            "config": {"workload": "Qwen3.8-27B shape, 32 chats, contexts log-uniform [128,16384]",
+                       "mean_context": float(pasts.mean())}}
+    print(json.dumps(line), flush=True)
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -150,6 +208,8 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (for scaling the HBM byte counters) and exit")
     ap.add_argument("--stream-copy", action="store_true", help="only print the device copy bandwidth and exit")
+    ap.add_argument("--hybrid", action="store_true",
+                    help="the Qwen3.8-27B hybrid shape instead (its own line; not the headline metric)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: every box here has one GPU and this build has no multi-GPU path "
@@ -160,6 +220,9 @@ def main():
         return
     if args.stream_copy:
         print(f"STREAM_COPY_GBPS {stream_copy_gbs():.3f}", flush=True)
+        return
+    if args.hybrid:
+        hybrid_main(args)
         return
     # before this process touches the GPU: the copy ceiling, from a child process
     import subprocess

@@ -41,3 +41,13 @@ def kv_token_bytes(d):
     """K and V bytes of one token in one layer: web/split.js:132 kvRowBytes x 2."""
     D = d["head_dim"]
     return 2 * d["n_kv_heads"] * (D + 4 * D // min(32, D))
+
+# Qwen3.8-27B (the reference's shipped hybrid, web/model/model.js:411-576):
+# 48 Gated DeltaNet blocks and 16 full-attention blocks (three to one), the
+# full ones with 24 query / 4 kv heads of 256 (a quarter rotary), the linear
+# ones with 16 key / 48 value heads of 128, and the MTP head over the first
+# 65536 vocabulary rows (tools/convert_hf.py:225 MTP_DRAFT_VOCAB).
+QWEN38 = dict(hidden=5120, n_layer=64, n_heads=24, n_kv_heads=4, head_dim=256, ffn=17408, vocab=248320,
+              rms_eps=1e-6, rope_theta=1e7, rot_dim=64, tied=False, hybrid=True,
+              layer_types=["linear_attention", "linear_attention", "linear_attention", "full_attention"] * 16,
+              lin_nk=16, lin_nv=48, lin_dk=128, lin_dv=128, lin_conv=4, mtp_vocab=65536)

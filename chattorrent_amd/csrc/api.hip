@@ -763,13 +763,49 @@ cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data
 cc_status cc_fill_random(cc_ctx* ctx, uint64_t seed) {
     if (!ctx) return CC_EARG;
     const cc_dims& d = ctx->d;
-    if (ctx->hybrid) return fail(ctx, CC_EARG, "a hybrid model's weights are uploaded, not generated");
+    hipStream_t st = ctx->stream;
     for (int li = 0; li < (int)ctx->layers.size(); li++) {
         const int layer = ctx->L0 + li;
+        Layer& L = ctx->layers[li];
+        if (L.kind == CC_LINEAR_ATTENTION) {
+            // synthetic Gated DeltaNet weights (timing only; the parity tests
+            // upload theirs): the fused in_proj and out_proj from the
+            // generator, fixed conv taps and gates
+            const LinGeom& lg = ctx->lg;
+            launch_gen_q8(st, L.lin, 0, lg.N, d.hidden, seed, (uint64_t)(layer + 1) * 16 + 7);
+            launch_gen_q8(st, L.out, 0, d.hidden, lg.valueDim, seed, (uint64_t)(layer + 1) * 16 + 8);
+            launch_fill(st, L.conv, (int64_t)lg.convDim * LIN_CONV_K, 0.25f);
+            launch_fill(st, L.gp, lg.nV, -1.0f);          // A_log
+            launch_fill(st, L.gp + lg.nV, lg.nV, 0.0f);   // dt_bias
+            for (int t = CC_T_GATE; t <= CC_T_DOWN; t++) {
+                int row_tile0, N, K;
+                QTensor* q = tensor_of(ctx, layer, t, &row_tile0, &N, &K);
+                launch_gen_q8(st, *q, row_tile0, N, K, seed, (uint64_t)(layer + 1) * 16 + t);
+            }
+            continue;
+        }
         for (int t = CC_T_Q; t <= CC_T_DOWN; t++) {
             int row_tile0, N, K;
             QTensor* q = tensor_of(ctx, layer, t, &row_tile0, &N, &K);
-            launch_gen_q8(ctx->stream, *q, row_tile0, N, K, seed, (uint64_t)(layer + 1) * 16 + t);
+            launch_gen_q8(st, *q, row_tile0, N, K, seed, (uint64_t)(layer + 1) * 16 + t);
+        }
+        if (ctx->hybrid) {
+            int row_tile0, N, K;
+            QTensor* q = tensor_of(ctx, layer, CC_T_ATTN_GATE, &row_tile0, &N, &K);
+            launch_gen_q8(st, *q, row_tile0, N, K, seed, (uint64_t)(layer + 1) * 16 + 12);
+        }
+    }
+    if (ctx->mtp) {
+        // the MTP head's matmuls and block (timing only)
+        const int H = d.hidden;
+        launch_gen_q8(st, ctx->fc_e, 0, H, H, seed, 3);
+        launch_gen_q8(st, ctx->fc_h, 0, H, H, seed, 4);
+        launch_gen_q8(st, ctx->embed_draft, 0, d.mtp_vocab, H, seed, 5);
+        launch_gen_q8(st, ctx->head_draft, 0, d.mtp_vocab, H, seed, 6);
+        for (int t = CC_T_Q; t <= CC_T_DOWN; t++) {
+            int row_tile0, N, K;
+            QTensor* q = tensor_of(ctx, CC_LAYER_MTP, t, &row_tile0, &N, &K);
+            launch_gen_q8(st, *q, row_tile0, N, K, seed, 0x4D545000ull + t);
         }
     }
     if (ctx->wte.codes) launch_gen_q8(ctx->stream, ctx->wte, 0, d.vocab, d.hidden, seed, 1);
@@ -851,6 +887,10 @@ cc_status cc_fill_random_kv(cc_ctx* ctx, int32_t slot, int32_t tokens, uint64_t 
             launch_fill_kv(ctx->stream, which ? ctx->layers[li].vpool : ctx->layers[li].kpool, ctx->page_table,
                            slot, tokens, ctx->geom, seed, 0x4B560000ull + (uint64_t)layer * 2 + which, key, which);
     }
+    // a synthetic history: the recurrent blocks hold these rows (their state
+    // is whatever the session's state block holds)
+    ctx->fed[slot] = tokens;
+    ctx->spec_n[slot] = -1;
     HIPCHK(hipStreamSynchronize(ctx->stream));
     return CC_OK;
 }

@@ -135,7 +135,10 @@ cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data
 
 /* Synthetic weights on the device from the counter-based generator shared
  * with the test oracle (no reference counterpart: the reference's random
- * models are randomWeights, web/model/model.js:697-717). */
+ * models are randomWeights, web/model/model.js:697-717). On a hybrid model
+ * (and for the MTP head) this is for timing only: the Gated DeltaNet's f32
+ * parameters take fixed values (conv taps 0.25, A_log -1, dt_bias 0) that
+ * the oracle does not mirror; parity tests upload their weights. */
 cc_status cc_fill_random(cc_ctx* ctx, uint64_t seed);
 
 /* One prepared job of a pass (the fields #prepare hands #pass,
