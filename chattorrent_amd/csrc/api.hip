@@ -65,6 +65,7 @@ struct cc_ctx {
     uint4* xp_v = nullptr;         // operand for K = valueDim
     float* gbuf = nullptr;         // [t_max][qdim] output-gate values
     float* lrep = nullptr;         // [max_jobs][LIN_SPEC_ROWS][lg.lrep_w] rows a rollback re-runs
+    float* lring = nullptr;        // [max_jobs][K-1][convDim] the ring each job starts from (long jobs)
     bool any_linear = false;
     // per session: its last job here was a verify from spec_base of spec_n rows
     std::vector<int> spec_base, spec_n;
@@ -531,6 +532,7 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
             HIPCHK(dalloc(ctx, &ctx->lraw, (size_t)T * lg.W * 4, &ctx->scratch_bytes));
             HIPCHK(dalloc(ctx, &ctx->lcore, (size_t)T * lg.valueDim * 4, &ctx->scratch_bytes));
             HIPCHK(dalloc(ctx, &ctx->lrep, (size_t)o.max_jobs * LIN_SPEC_ROWS * lg.lrep_w * 4, &ctx->scratch_bytes));
+            HIPCHK(dalloc(ctx, &ctx->lring, (size_t)o.max_jobs * (LIN_CONV_K - 1) * lg.convDim * 4, &ctx->scratch_bytes));
         }
         ctx->any_linear = any_linear;
         ctx->spec_base.assign(o.sessions, 0);
@@ -1144,6 +1146,8 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
     pm.ncwg = p.ncwg;
     const RowScale rs = row_scale_of(ctx);
     const int KUH = ceil_div(H, 64);   // every block's first matmul reads K = hidden
+    int longest = 0;                   // a long job takes the row-parallel conv
+    for (const JobDev& jd : p.jobs) longest = std::max(longest, (int)jd.n);
     for (int b = b0; b < b1; b++) {
         Layer& L = ctx->layers[b - ctx->L0];
         if (b == b0) launch_resid_w(st, ctx->x, nullptr, 0, T, Mpad, H, 0, L.ln1, KUH, ctx->xp_h, ctx->ssp);
@@ -1152,8 +1156,12 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
             // recurrence on each session's state, gated norm, out_proj
             const LinGeom& lg = ctx->lg;
             launch_gemm(st, L.lin, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-            launch_lin_conv(st, ctx->part, L.lin.P, T, pm.njobs, pm.jobs, rs, L.conv, lg, L.state, ctx->lraw,
-                            ctx->lrep);
+            if (longest > LIN_SEQ_ROWS)
+                launch_lin_conv_rows(st, ctx->part, L.lin.P, T, pm.njobs, pm.row_job, pm.jobs, rs, L.conv, lg, L.state,
+                                     ctx->lraw, ctx->lrep, ctx->lring);
+            else
+                launch_lin_conv(st, ctx->part, L.lin.P, T, pm.njobs, pm.jobs, rs, L.conv, lg, L.state, ctx->lraw,
+                                ctx->lrep);
             launch_gdn(st, ctx->lraw, ctx->lrep, pm.njobs, pm.jobs, L.gp, lg, L.state, ctx->lcore);
             launch_lin_norm(st, ctx->lcore, ctx->lraw, L.gnorm, d.rms_eps, T, lg, L.out.KU, ctx->xp_v);
             launch_gemm(st, L.out, ctx->xp_v, ctx->mt_alloc, ctx->part, T, ctx->ncu);

@@ -112,6 +112,12 @@ constexpr int LIN_CONV_K = 4;
 void launch_lin_conv(hipStream_t st, const float* part, int splits, int M, int njobs, const JobDev* jobs,
                      const RowScale& rs, const float* conv, const LinGeom& lg, float* state, float* lraw,
                      float* lrep);
+// The conv parallel over rows, for a pass with a long job; `lring`
+// [jobs][K-1][convDim] scratch.
+constexpr int LIN_SEQ_ROWS = 16;   // longest job the one-thread-per-channel conv walks
+void launch_lin_conv_rows(hipStream_t st, const float* part, int splits, int M, int njobs, const int32_t* row_job,
+                          const JobDev* jobs, const RowScale& rs, const float* conv, const LinGeom& lg, float* state,
+                          float* lraw, float* lrep, float* lring);
 void launch_gdn(hipStream_t st, const float* lraw, const float* lrep, int njobs, const JobDev* jobs,
                 const float* gp, const LinGeom& lg, float* state, float* core);
 // RMSNormGated per (row, value head) with the gated_norm weight, times

@@ -1108,6 +1108,128 @@ void launch_lin_conv(hipStream_t st, const float* part, int splits, int M, int n
     CHECK_LAUNCH();
 }
 
+// The same conv for a pass with a long job (a prefill chunk), parallel over
+// rows, in three steps (the arithmetic per row is the one above, so the bits
+// do not depend on the path):
+//   k_lin_ring_pre   the ring each job starts from (the session's, or the
+//                    snapshot's advanced through the kept rows) into `lring`
+//                    [job][K-1][convDim]; the rollback rows to `lrep`; a
+//                    verify's snapshot ring;
+//   k_lin_conv_rows  one thread per (row, channel): the window from the
+//                    job's own rows (planes summed again) and `lring`;
+//   k_lin_ring_post  the ring after the job's last row, into the session.
+__global__ __launch_bounds__(256) void k_lin_ring_pre(const JobDev* __restrict__ jobs, LinGeom lg,
+                                                      float* __restrict__ state, float* __restrict__ lrep,
+                                                      float* __restrict__ lring) {
+    constexpr int K = LIN_CONV_K;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= lg.W) return;
+    const int j = blockIdx.y;
+    const JobDev jb = jobs[j];
+    float* base = state + (size_t)jb.slot * lg.sstride;
+    const float* rep = base + lg.rep_off;
+    float* lr = lrep + (size_t)j * LIN_SPEC_ROWS * lg.lrep_w;
+    const int keep = jb.keep > 0 ? jb.keep : 0;
+    if (c >= lg.convDim) {
+        if (c >= lg.convDim + lg.valueDim) {
+            const int e = c - lg.convDim - lg.valueDim;
+            for (int i = 0; i < keep; i++)
+                lr[(size_t)i * lg.lrep_w + lg.convDim + e] = rep[(size_t)i * lg.rep_w + 2 * lg.convDim + e];
+        }
+        return;
+    }
+    float* cur = base + lg.hist_off + c;
+    float* snap = base + lg.blk + lg.hist_off + c;
+    const float* src = jb.keep >= 0 ? snap : cur;
+    float h[K - 1];
+#pragma unroll
+    for (int r = 0; r < K - 1; r++) h[r] = jb.past > 0 ? src[(size_t)r * lg.convDim] : 0.0f;
+    for (int i = 0; i < keep; i++) {
+        lr[(size_t)i * lg.lrep_w + c] = rep[(size_t)i * lg.rep_w + lg.convDim + c];
+#pragma unroll
+        for (int k = 0; k < K - 2; k++) h[k] = h[k + 1];
+        h[K - 2] = rep[(size_t)i * lg.rep_w + c];
+    }
+    float* e = lring + (size_t)j * (K - 1) * lg.convDim + c;
+#pragma unroll
+    for (int r = 0; r < K - 1; r++) {
+        e[(size_t)r * lg.convDim] = h[r];
+        if (jb.snap) snap[(size_t)r * lg.convDim] = h[r];
+    }
+}
+
+__global__ __launch_bounds__(256) void k_lin_conv_rows(const float* __restrict__ part, int splits, int M,
+                                                       const int32_t* __restrict__ row_job,
+                                                       const JobDev* __restrict__ jobs, RowScale rs,
+                                                       const float* __restrict__ conv, LinGeom lg,
+                                                       float* __restrict__ state, const float* __restrict__ lring,
+                                                       float* __restrict__ lraw) {
+    constexpr int K = LIN_CONV_K;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    const int m = blockIdx.y;
+    if (c >= lg.W || m >= M) return;
+    const int j = row_job[m];
+    const JobDev jb = jobs[j];
+    const int i = m - jb.row0;
+    float* rep = state + (size_t)jb.slot * lg.sstride + lg.rep_off;
+    const int col = c < lg.convDim + lg.valueDim + lg.nV ? c : c - lg.nV + lg.nVp;
+    if (c >= lg.convDim) {
+        const float v = plane_col(part, splits, M, lg.N, m, col, row_scale(rs, m));
+        lraw[(size_t)m * lg.W + c] = v;
+        if (jb.snap && c >= lg.convDim + lg.valueDim) rep[(size_t)i * lg.rep_w + 2 * lg.convDim + (c - lg.convDim - lg.valueDim)] = v;
+        return;
+    }
+    const float* e = lring + (size_t)j * (K - 1) * lg.convDim + c;
+    float x[K];   // the window: rows i-K+1 .. i
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int t = i - (K - 1) + k;
+        x[k] = t >= 0 ? plane_col(part, splits, M, lg.N, jb.row0 + t, col, row_scale(rs, jb.row0 + t))
+                      : e[(size_t)(K - 1 + t) * lg.convDim];
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < K; k++) acc = acc + conv[(size_t)c * K + k] * x[k];
+    const float sg = 1.0f / (1.0f + expf(-acc));
+    const float out = acc * sg;
+    lraw[(size_t)m * lg.W + c] = out;
+    if (jb.snap) {
+        rep[(size_t)i * lg.rep_w + c] = x[K - 1];
+        rep[(size_t)i * lg.rep_w + lg.convDim + c] = out;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_lin_ring_post(const float* __restrict__ part, int splits, int M,
+                                                       const JobDev* __restrict__ jobs, RowScale rs, LinGeom lg,
+                                                       float* __restrict__ state, const float* __restrict__ lring) {
+    constexpr int K = LIN_CONV_K;
+    const int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= lg.convDim) return;
+    const int j = blockIdx.y;
+    const JobDev jb = jobs[j];
+    float* cur = state + (size_t)jb.slot * lg.sstride + lg.hist_off + c;
+    const float* e = lring + (size_t)j * (K - 1) * lg.convDim + c;
+#pragma unroll
+    for (int r = 0; r < K - 1; r++) {
+        const int t = jb.n - (K - 1) + r;   // the ring's row r after the job
+        cur[(size_t)r * lg.convDim] = t >= 0 ? plane_col(part, splits, M, lg.N, jb.row0 + t, c, row_scale(rs, jb.row0 + t))
+                                             : e[(size_t)(K - 1 + t) * lg.convDim];
+    }
+}
+
+void launch_lin_conv_rows(hipStream_t st, const float* part, int splits, int M, int njobs, const int32_t* row_job,
+                          const JobDev* jobs, const RowScale& rs, const float* conv, const LinGeom& lg, float* state,
+                          float* lraw, float* lrep, float* lring) {
+    if (njobs <= 0 || M <= 0) return;
+    const int bw = (lg.W + 255) / 256;
+    hipLaunchKernelGGL(k_lin_ring_pre, dim3(bw, njobs), dim3(256), 0, st, jobs, lg, state, lrep, lring);
+    hipLaunchKernelGGL(k_lin_conv_rows, dim3(bw, M), dim3(256), 0, st, part, splits, M, row_job, jobs, rs, conv, lg,
+                       state, lring, lraw);
+    hipLaunchKernelGGL(k_lin_ring_post, dim3((lg.convDim + 255) / 256, njobs), dim3(256), 0, st, part, splits, M, jobs,
+                       rs, lg, state, lring);
+    CHECK_LAUNCH();
+}
+
 // gated_delta_net_step (kernels.js:1672-1805) for every row of a job, on its
 // session's S [nV][Dk][Dv]: one workgroup per (value-column tile, value head,
 // job), GDN_KS k-groups x GDN_TV columns; each thread holds DK/GDN_KS rows of

@@ -208,3 +208,50 @@ def test_hybrid_refuses_what_it_cannot_replay(gpu):
         _run(c, [dict(slot=0, past=8, n=1, ids=_ids(rng, 1, V), sampled=1, keep=3)])
     finally:
         c.close()
+
+
+def test_hybrid_long_jobs_take_the_row_parallel_conv_bitwise(gpu):
+    """A prompt longer than 16 rows runs the conv parallel over rows (ring
+    stashed, rows, ring advanced); cut into short jobs it runs the
+    one-thread-per-channel conv. Both give the same logits, bit for bit."""
+    d = HW.SPIKE
+    rng = np.random.default_rng(41)
+    prompt = _ids(rng, 40, d["vocab"])
+    got = []
+    for cuts in ([40], [16, 16, 8], [1, 39], [3, 20, 17]):
+        c, _ = _pair(d, slots=1)
+        try:
+            past = 0
+            for n in cuts:
+                c.step([dict(slot=0, past=past, n=n, ids=prompt[past:past + n], sampled=1)], topk=2)
+                past += n
+            got.append(c.read_logits(1).copy())
+        finally:
+            c.close()
+    for g in got[1:]:
+        assert np.array_equal(g.view(np.uint32), got[0].view(np.uint32))
+
+
+def test_hybrid_long_rollback_job_matches_oracle(gpu):
+    """A 40-row prefill beside a short one, a verify on the short session,
+    then a 20-row job that rolls it back (keep 1) beside a decode: the long
+    path's ring stash, rollback copies and snapshot, against the oracle."""
+    d = HW.WIDE
+    c, om = _pair(d)
+    rng = np.random.default_rng(42)
+    V = d["vocab"]
+    try:
+        jobs = [dict(slot=0, past=0, n=40, ids=_ids(rng, 40, V), sampled=1, topk=4),
+                dict(slot=1, past=0, n=3, ids=_ids(rng, 3, V), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        _check(vals, ids, om.pass_(jobs), c)
+        jobs = [dict(slot=1, past=3, n=4, ids=_ids(rng, 4, V), sampled=4, topk=4, snap=True),
+                dict(slot=0, past=40, n=1, ids=_ids(rng, 1, V), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        _check(vals, ids, om.pass_(jobs), c)
+        jobs = [dict(slot=1, past=4, n=20, ids=_ids(rng, 20, V), sampled=1, topk=4, keep=1),
+                dict(slot=0, past=41, n=1, ids=_ids(rng, 1, V), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        _check(vals, ids, om.pass_(jobs), c)
+    finally:
+        c.close()
