@@ -908,15 +908,17 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
     // q_norm / k_norm (model.js:388-394): rmsnorm over the head's D values
     // (lane partials, then a wave reduction), before RoPE reads neighbouring
     // channels
-    if (ex.qn && live && hidx < nH + nKV) {
-        const float* w = hidx < nH ? ex.qn : ex.kn;
-        float ss = 0.0f;
-        for (int d = lane; d < D; d += 64) ss += buf[wave][d] * buf[wave][d];
-        ss = wave_sum(ss);
-        const float scale = 1.0f / sqrtf(ss / (float)D + ex.eps);
-        for (int d = lane; d < D; d += 64) buf[wave][d] = buf[wave][d] * scale * w[d];
+    if (ex.qn) {   // a kernel argument: the barrier is uniform
+        if (live && hidx < nH + nKV) {
+            const float* w = hidx < nH ? ex.qn : ex.kn;
+            float ss = 0.0f;
+            for (int d = lane; d < D; d += 64) ss += buf[wave][d] * buf[wave][d];
+            ss = wave_sum(ss);
+            const float scale = 1.0f / sqrtf(ss / (float)D + ex.eps);
+            for (int d = lane; d < D; d += 64) buf[wave][d] = buf[wave][d] * scale * w[d];
+        }
+        __syncthreads();
     }
-    __syncthreads();
     if (live && hidx < nH) {
         if (do_q) {
             for (int d = lane; d < D; d += 64) rq[wave][d] = rope_at(buf[wave], d, rot, tbl, pos);
@@ -1653,6 +1655,7 @@ void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev
 // loads in flight), one row's 8 columns a thread, and the quarters are added
 // in order through LDS.
 constexpr int COMBINE_CMAX = 512, COMBINE_SPLIT = 4;
+template <int D>
 __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict__ jobs, const float* __restrict__ part,
                                                        KVGeom g, int nH, int group, int KU, uint4* __restrict__ Xp,
                                                        float* __restrict__ ctx_out,
@@ -1663,7 +1666,7 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
     __shared__ float4 red[COMBINE_SPLIT - 1][256][2];
     const int job = wg_job[3 * blockIdx.x], kvh = wg_job[3 * blockIdx.x + 1], mt = wg_job[3 * blockIdx.x + 2];
     const JobDev jb = jobs[job];
-    const int D = g.D, W = D + 4;
+    constexpr int W = D + 4;
     const int R = jb.n * group;
     const int nc = jb.nchunk;
     const size_t pstride = (size_t)16 * W;
@@ -1689,7 +1692,7 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
     // 16 rows x D columns, 8 a thread, in chunks of at most 128 columns (one
     // chunk up to D = 128, two at D = 256); every thread reaches every barrier
     const int sub = threadIdx.x >> 8, t = threadIdx.x & 255;
-    const int CW = D < 128 ? D : 128;
+    constexpr int CW = D < 128 ? D : 128;
     const int rl = t / (CW / 8);
     const bool live = rl < 16 && mt * 16 + rl < R;
     const int rho = mt * 16 + rl;
@@ -1749,15 +1752,22 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
             }
             write_hilo(Xp, r, k / 8, KU, v);
         }
-        __syncthreads();   // `red` is reused by the next chunk
+        if (c0 + CW < D) __syncthreads();   // `red` is reused by the next chunk
     }
 }
 
 void launch_attn_combine(hipStream_t st, const JobDev* jobs, const float* part, const KVGeom& g, int nH, int group,
                          int KU, uint4* Xp, float* ctx_out, const int32_t* wg_job, int nwg, const float* gate) {
     if (nwg <= 0) return;
-    hipLaunchKernelGGL(k_attn_combine, dim3(nwg), dim3(1024), 0, st, jobs, part, g, nH, group, KU, Xp, ctx_out,
-                       wg_job, gate);
+    if (g.D == 256)
+        hipLaunchKernelGGL(k_attn_combine<256>, dim3(nwg), dim3(1024), 0, st, jobs, part, g, nH, group, KU, Xp, ctx_out,
+                           wg_job, gate);
+    else if (g.D == 128)
+        hipLaunchKernelGGL(k_attn_combine<128>, dim3(nwg), dim3(1024), 0, st, jobs, part, g, nH, group, KU, Xp, ctx_out,
+                           wg_job, gate);
+    else
+        hipLaunchKernelGGL(k_attn_combine<64>, dim3(nwg), dim3(1024), 0, st, jobs, part, g, nH, group, KU, Xp, ctx_out,
+                           wg_job, gate);
     CHECK_LAUNCH();
 }
 
