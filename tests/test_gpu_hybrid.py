@@ -255,3 +255,35 @@ def test_hybrid_long_rollback_job_matches_oracle(gpu):
         _check(vals, ids, om.pass_(jobs), c)
     finally:
         c.close()
+
+
+def test_hybrid_split_over_two_peers_bitwise(gpu):
+    """Two contexts holding positions [0, 3) and [3, 6) of a 4-block hybrid
+    model, rows handed on as f16 bits (stage.js:1340-1346): prefill, a
+    verify and a rollback crossing both, each context tracking its own
+    recurrent blocks. The head's logits equal the single context's."""
+    from chattorrent_amd.ccdecode import Context
+    d = HW.SPIKE
+    w = HW.make(d, SEED)
+    rng = np.random.default_rng(51)
+    V = d["vocab"]
+    prompt, ver, x = _ids(rng, 9, V), _ids(rng, 4, V), _ids(rng, 1, V)
+    plan = [dict(past=0, n=9, ids=prompt), dict(past=9, n=4, ids=ver, snap=True, sampled=4),
+            dict(past=11, n=1, ids=x, keep=2)]
+    whole = Context(d, n_max=256, t_max=16, slots=1)
+    a = Context(d, n_max=256, t_max=16, slots=1, lo=0, hi=3)
+    b = Context(d, n_max=256, t_max=16, slots=1, lo=3, hi=6)
+    try:
+        for c, lo, hi in ((whole, 0, 6), (a, 0, 3), (b, 3, 6)):
+            HW.upload(c, w, d, lo, hi)
+        for j in plan:
+            job = dict(slot=0, sampled=j.get("sampled", 1), **{k: v for k, v in j.items() if k != "sampled"})
+            whole.step([job], topk=2)
+            want = whole.read_logits(job["sampled"]).copy()
+            rows = a.step([dict(job, sampled=0)], at=0, to=3)
+            b.step([dict(job, ids=None, hidden=rows)], at=3, to=6, topk=2)
+            got = b.read_logits(job["sampled"])
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), j
+    finally:
+        for c in (whole, a, b):
+            c.close()
