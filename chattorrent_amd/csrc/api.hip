@@ -1016,8 +1016,9 @@ static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, 
         jd.item0 = (int32_t)p.items.size();
         for (int h = 0; h < ctx->geom.nKV; h++)
             for (int mt = 0; mt < jd.mtq; mt++) {
+                const int32_t qb = jd.qp_off + ((h * jd.mtq + mt) * ng) * 128;
                 for (int c = 0; c < jd.nchunk; c++) {
-                    p.items.push_back(AttnItem{j, h, c, (int32_t)ap, mt});
+                    p.items.push_back(AttnItem{jd.slot, jd.past, jd.n, mt, qb, (int32_t)ap, h, c * ctx->ppw});
                     ap += (size_t)16 * (ctx->D + 4);
                 }
                 p.cwg.push_back(j);
@@ -1098,7 +1099,7 @@ static void full_attn_half(cc_ctx* ctx, Layer& L, float* x, int T, int Mpad, con
     launch_gemm(st, L.qkv, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
     launch_fin_qkv(st, ctx->part, L.qkv.P, T, pm.row_job, pm.jobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
                    L.kpool, L.vpool, ctx->page_table, ctx->qp, rs, 1, 1, ex);
-    launch_attn(st, pm.items, pm.nitems, pm.jobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
+    launch_attn(st, pm.items, pm.nitems, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
                 ctx->ppw, ctx->apart);
     launch_attn_combine(st, pm.jobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU, ctx->xp_o, nullptr, pm.cwg,
                         pm.ncwg, ctx->hybrid ? ctx->gbuf : nullptr);
@@ -1256,7 +1257,7 @@ static void prof_replay(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, in
                 for (int b = b0; b < b1; b++) {
                     const Layer& L = ctx->layers[b - ctx->L0];
                     if (!L.kpool) continue;
-                    launch_attn(st, ditems, p.nitems, djobs, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom,
+                    launch_attn(st, ditems, p.nitems, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom,
                                 ctx->group, ctx->ppw, ctx->apart);
                 }
             });
@@ -1770,7 +1771,7 @@ cc_status cc_op_attend(cc_ctx* ctx, int32_t layer, int32_t slot, const float* q,
     const AttnItem* di = (const AttnItem*)(ctx->d_meta + ml.items);
     launch_fin_qkv(st, dr, 1, n, (const int32_t*)(ctx->d_meta + ml.row_job), dj, d.n_heads, ctx->group, ctx->geom,
                    ctx->tbl, ctx->rot, L.kpool, L.vpool, ctx->page_table, ctx->qp, RowScale{}, 1, 0);
-    launch_attn(st, di, p.nitems, dj, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->ppw,
+    launch_attn(st, di, p.nitems, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->ppw,
                  ctx->apart);
     launch_attn_combine(st, dj, ctx->apart, ctx->geom, d.n_heads, ctx->group, KU, dXp, dctx,
                          (const int32_t*)(ctx->d_meta + ml.cwg), p.ncwg);

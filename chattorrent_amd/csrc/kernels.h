@@ -42,9 +42,15 @@ struct JobDev {
     int32_t keep;                  // >= 0: roll back to the snapshot, re-run `keep` rows
 };
 
+// One attention work item carries its job's fields itself (32 bytes, one
+// scalar load), so a wave reaches its page table without a second
+// dependent load.
 struct AttnItem {
-    int32_t job, kvh, chunk, part; // part: float offset of the partial block
+    int32_t slot, past, n;         // the job's session and rows
     int32_t mt;                    // query m-tile (16 rows rho = i*group + gi)
+    int32_t qb;                    // Q operand base of (kv head, m-tile), uint4 units
+    int32_t part;                  // float offset of the partial block
+    int32_t kvh, p0;               // kv head, first page of the chunk
 };
 
 struct KVGeom {
@@ -158,7 +164,7 @@ void launch_resid_w(hipStream_t st, float* x, const float* part, int splits, int
                     const float* w, int KU, uint4* Xp, float* ssp);
 void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const float* part, int splits, int M,
                        int Mpad, int H, int round, const float* w, float eps, int KU, uint4* Xp, float* y);
-void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
+void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const uint4* Qp,
                   const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
                   int ppw, float* part);
 // `gate` (a hybrid checkpoint's, [rows][nH*D], or null): the output is

@@ -1430,7 +1430,7 @@ void launch_lin_norm(hipStream_t st, const float* core, const float* lraw, const
 // mask, and a still fully masked row (max -inf) just takes alpha = 0, p = 0.
 template <int NG>
 __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __restrict__ items, int nitems,
-                                                 const JobDev* __restrict__ jobs, const uint4* __restrict__ Qp,
+                                                 const uint4* __restrict__ Qp,
                                                  const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
                                                  const uint32_t* __restrict__ page_table, KVGeom g, int group, int ppw,
                                                  float* __restrict__ part) {
@@ -1445,11 +1445,10 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
     const int wid = blockIdx.x * 4 + wv;
     if (wid >= nitems) return;   // no barriers below: a finished wave may leave
     const AttnItem it = items[wid];
-    const JobDev jb = jobs[it.job];
-    const int T_act = jb.past + jb.n;
-    const int R = jb.n * group;
+    const int T_act = it.past + it.n;
+    const int R = it.n * group;
     const int npg = (T_act + 63) >> 6;
-    const int p0 = it.chunk * ppw;
+    const int p0 = it.p0;
     const int p1 = min(npg, p0 + ppw);
     const int mtq = it.mt;
     // scores in log2 units: exp(s/sqrt(D)) = exp2(s * log2(e)/sqrt(D)), one v_exp_f32 each
@@ -1457,7 +1456,7 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
 
     uint4 qh[NG], ql[NG];
     {
-        const size_t qb = (size_t)jb.qp_off + (((size_t)it.kvh * jb.mtq + mtq) * NG) * 128 + lane;
+        const size_t qb = (size_t)it.qb + lane;
 #pragma unroll
         for (int gg = 0; gg < NG; gg++) {
             qh[gg] = Qp[qb + (size_t)gg * 128];
@@ -1465,8 +1464,8 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
         }
     }
     const int rho = mtq * 16 + l16;
-    const int lim = rho < R ? jb.past + rho / group : -1;   // last visible token of this row
-    const uint32_t* pt = page_table + (size_t)jb.slot * g.max_pages;
+    const int lim = rho < R ? it.past + rho / group : -1;   // last visible token of this row
+    const uint32_t* pt = page_table + (size_t)it.slot * g.max_pages;
     const size_t hoff = (size_t)it.kvh * g.blk;
     const size_t pstride = (size_t)g.nKV * g.blk;
     // The chunk's page indices, one a lane (ppw <= 64): a page reads its own
@@ -1627,19 +1626,19 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
     }
 }
 
-void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const JobDev* jobs, const uint4* Qp,
+void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const uint4* Qp,
                  const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
                  int ppw, float* part) {
     if (nitems <= 0) return;
     const int blocks = (nitems + 3) / 4;
     if (g.ng == 8)
-        hipLaunchKernelGGL(k_attn<8>, dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool, page_table, g,
+        hipLaunchKernelGGL(k_attn<8>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
                      group, ppw, part);
     else if (g.ng == 4)
-        hipLaunchKernelGGL(k_attn<4>, dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool, page_table, g,
+        hipLaunchKernelGGL(k_attn<4>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
                      group, ppw, part);
     else
-        hipLaunchKernelGGL(k_attn<2>, dim3(blocks), dim3(256), 0, st, items, nitems, jobs, Qp, kpool, vpool, page_table, g,
+        hipLaunchKernelGGL(k_attn<2>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
                      group, ppw, part);
     CHECK_LAUNCH();
 }
