@@ -82,6 +82,19 @@ class PagePool:
         return n
 
 
+def compose_block(x, ln1, ln2, eps, attention, mlp):
+    """One full-attention block's residual stream, in place on x [T, H] f32,
+    before the block's f16 round: web/model/model.js:368-409 fullBlockSegs
+    (rmsnorm(x) with ln1 -> the attention sublayer -> x += its output) and
+    :307-316 ffnBlock (rmsnorm(x) with ln2 -> the MLP -> x += its output).
+    `attention(h)` and `mlp(h)` return their sublayer's [T, H] output; the
+    parity tests also run this with the reference's dumped sublayer outputs
+    in their place, which pins the order of norms and residual adds."""
+    L.add_inplace(x, attention(L.rmsnorm(x, ln1, eps)))
+    L.add_inplace(x, mlp(L.rmsnorm(x, ln2, eps)))
+    return x
+
+
 class Model:
     """A full-attention Llama-style model with q8 weights and an int8 paged KV pool."""
 
@@ -181,22 +194,22 @@ class Model:
     def block(self, layer, x, segs):
         d, g = self.d, self.group
         lw = self.w["layers"][layer]
-        h = L.rmsnorm(x, lw["ln1"], d["rms_eps"])
-        q = L.matmul_q8(h, *lw["q"], group=g)
-        k = L.matmul_q8(h, *lw["k"], group=g)
-        v = L.matmul_q8(h, *lw["v"], group=g)
-        merged = np.empty_like(q)
-        for s in segs:
-            a, b = s["row"], s["row"] + s["n"]
-            merged[a:b] = self.attend(layer, s["slot"], q[a:b], k[a:b], v[a:b], s["past"])
-        attn = L.matmul_q8(merged, *lw["o"], group=g)
-        L.add_inplace(x, attn)
-        h = L.rmsnorm(x, lw["ln2"], d["rms_eps"])
-        gt = L.matmul_q8(h, *lw["gate"], group=g)
-        up = L.matmul_q8(h, *lw["up"], group=g)
-        act = L.silu_mul(gt, up)
-        dn = L.matmul_q8(act, *lw["down"], group=g)
-        L.add_inplace(x, dn)
+
+        def attention(h):
+            q = L.matmul_q8(h, *lw["q"], group=g)
+            k = L.matmul_q8(h, *lw["k"], group=g)
+            v = L.matmul_q8(h, *lw["v"], group=g)
+            merged = np.empty_like(q)
+            for s in segs:
+                a, b = s["row"], s["row"] + s["n"]
+                merged[a:b] = self.attend(layer, s["slot"], q[a:b], k[a:b], v[a:b], s["past"])
+            return L.matmul_q8(merged, *lw["o"], group=g)
+
+        def mlp(h):
+            act = L.silu_mul(L.matmul_q8(h, *lw["gate"], group=g), L.matmul_q8(h, *lw["up"], group=g))
+            return L.matmul_q8(act, *lw["down"], group=g)
+
+        compose_block(x, lw["ln1"], lw["ln2"], d["rms_eps"], attention, mlp)
         L.lib().orc_round_f16(L._p(x), x.size)
         return x
 

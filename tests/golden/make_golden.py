@@ -1,4 +1,4 @@
-"""Copies the reference's own weight-free RoPE golden vectors into tests/golden/.
+"""Copies the reference's own weight-free golden vectors into tests/golden/.
 
     python tests/golden/make_golden.py /path/to/reference
 
@@ -6,8 +6,11 @@ These are data files the reference's tests hold (HF intermediates dumped by
 its tools/dump_*_oracle.py and read by web/dev/verify.js): a block's q/k
 projections before RoPE and the split-half RoPE of them computed in f64, plus
 the Qwen spike's cos/sin table. They pin the oracle's RoPE table and rotation
-(oracle/ccoracle.c orc_rope_table / orc_rope) without any weights. Only
-arrays are copied (numpy.load with allow_pickle=False); nothing is run.
+(oracle/ccoracle.c orc_rope_table / orc_rope) without any weights. Block 0's
+residual-stream dumps (the embedding rows, both norms' outputs, the attention
+and MLP sublayers' outputs, the residual between them and the block's output)
+pin the block's composition (oracle/model.py compose_block) the same way.
+Only arrays are copied (numpy.load with allow_pickle=False); nothing is run.
 """
 import json
 import os
@@ -26,6 +29,13 @@ FILES = {
     "llama-3.1-8b-instruct/block00_k.npy": "llama31_k.npy",
     "llama-3.1-8b-instruct/block00_k_rope.npy": "llama31_k_rope.npy",
     "qwen3.8-27b-spike/rope_cos.npy": "qwen_spike_rope_cos.npy",
+    # block 0's residual stream (HF, f32): embeddings -> ln1 -> attention ->
+    # +residual -> ln2 -> MLP -> +residual
+    **{f"{src}/{a}.npy": f"{dst}_{b}.npy"
+       for src, dst in (("smollm2", "smollm2"), ("llama-3.1-8b-instruct", "llama31"))
+       for a, b in (("embeddings", "embeddings"), ("block00_ln1", "ln1"), ("block00_attn_out", "attn_out"),
+                    ("block00_after_attn_resid", "after_attn_resid"), ("block00_ln2", "ln2"),
+                    ("block00_mlp_out", "mlp_out"), ("block_00_out", "block_out"))},
     "qwen3.8-27b-spike/rope_sin.npy": "qwen_spike_rope_sin.npy",
 }
 
@@ -35,8 +45,8 @@ FILES = {
 # original 8192; tools/dump_llama_oracle.py:41-51 reads it from HF), and the
 # Qwen spike's spike_config.json (theta 1e7, head_dim 64, rot 16).
 PARAMS = {
-    "smollm2": {"theta": 100000.0, "head_dim": 64, "n_heads": 9, "n_kv_heads": 3, "rot": 64},
-    "llama31": {"theta": 500000.0, "head_dim": 128, "n_heads": 32, "n_kv_heads": 8, "rot": 128,
+    "smollm2": {"theta": 100000.0, "head_dim": 64, "n_heads": 9, "n_kv_heads": 3, "rot": 64, "rms_eps": 1e-5},
+    "llama31": {"theta": 500000.0, "head_dim": 128, "n_heads": 32, "n_kv_heads": 8, "rot": 128, "rms_eps": 1e-5,
                 "scaling": {"factor": 8.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
                             "original_max_position_embeddings": 8192}},
     "qwen_spike": {"theta": 10000000.0, "head_dim": 64, "rot": 16},

@@ -378,3 +378,100 @@ def test_oracle_batched_pass_equals_alone():
         assert np.array_equal(alone["logits"].view(np.uint32), r["logits"].view(np.uint32))
     swapped = m.pass_([dict(jobs[0], slot=1, past=40)])[0]
     assert not np.array_equal(swapped["logits"], both[0]["logits"])
+
+
+# ------------------------------------------------- block composition pins ---
+def _gold(name, part):
+    return np.load(os.path.join(GOLD, f"{name}_{part}.npy"), allow_pickle=False)
+
+
+def _norm_fit(norm_out, unit):
+    """How far `norm_out` is from `unit` (an rmsnorm output with unit
+    weights) times one weight per channel: the weight is fitted by least
+    squares over the tokens (the dumps carry no weights), and the worst
+    residual is returned relative to max |norm_out|. The right input fits to
+    f32 rounding; any other tensor leaves a residual of order one."""
+    u = unit.astype(np.float64)
+    y = norm_out.astype(np.float64)
+    w = (y * u).sum(axis=0) / np.maximum((u * u).sum(axis=0), 1e-300)
+    return float(np.abs(y - u * w).max() / np.abs(y).max())
+
+
+def _composition_errors(name, compose):
+    """Runs `compose` (compose_block's signature) on the reference's block-0
+    embedding rows with the dumped attention and MLP outputs in place of the
+    sublayers and unit norm weights, and measures, against the dumps:
+    ln1 - what the attention sublayer was given, up to a per-channel weight;
+    ln2 - what the MLP was given, up to a per-channel weight (this pins its
+          input as the residual after attention);
+    out - the block's output before the f16 round (block_00_out)."""
+    eps = _params()[name]["rms_eps"]
+    emb = _gold(name, "embeddings")
+    seen = {}
+
+    def attention(h):
+        seen["h1"] = np.array(h)
+        return _gold(name, "attn_out")
+
+    def mlp(h):
+        seen["h2"] = np.array(h)
+        return _gold(name, "mlp_out")
+
+    ones = np.ones(emb.shape[1], np.float32)
+    x = np.ascontiguousarray(emb.copy())
+    out = compose(x, ones, ones, eps, attention, mlp)
+    want = _gold(name, "block_out")
+    return {
+        "ln1": _norm_fit(_gold(name, "ln1"), seen["h1"]),
+        "ln2": _norm_fit(_gold(name, "ln2"), seen["h2"]),
+        "out": float(np.abs(out.astype(np.float64) - want).max() / np.abs(want).max()),
+    }
+
+
+@pytest.mark.parametrize("name", ["smollm2", "llama31"])
+def test_block_composition_matches_reference_dumps(name):
+    """oracle/model.py compose_block (model.js:368-409, :307-316) against the
+    reference's own HF dumps of block 0 (oracle/<model>/block00_*.npy,
+    block_00_out.npy): rmsnorm of the block input feeds attention, the
+    attention output is added to the residual, rmsnorm of that residual feeds
+    the MLP, and the MLP output is added to it. The dumps agree with these
+    relations to f32 rounding; the f16 round after the block (pinned by the
+    f16 tests above) is the reference's own addition, absent from HF."""
+    # the dumps themselves: the residual adds hold as sums of the dumped parts
+    emb, att, mid = _gold(name, "embeddings"), _gold(name, "attn_out"), _gold(name, "after_attn_resid")
+    assert np.abs(mid.astype(np.float64) - emb - att).max() <= 1e-7 * np.abs(mid).max()
+    err = _composition_errors(name, Mo.compose_block)
+    assert err["ln1"] <= 2e-7 and err["ln2"] <= 2e-7 and err["out"] <= 2e-7, err
+
+
+def test_block_composition_check_catches_misplaced_parts():
+    """The check above has teeth: compositions with a plausible mistake
+    planted (the MLP's norm reading the block input, a dropped attention
+    residual, the MLP output added to the block input, the MLP norm's input
+    taken after the MLP residual) each fail it by orders of magnitude."""
+    def ln2_from_input(x, ln1, ln2, eps, attention, mlp):
+        x0 = x.copy()
+        L.add_inplace(x, attention(L.rmsnorm(x, ln1, eps)))
+        L.add_inplace(x, mlp(L.rmsnorm(x0, ln2, eps)))
+        return x
+
+    def no_attn_residual(x, ln1, ln2, eps, attention, mlp):
+        x[:] = attention(L.rmsnorm(x, ln1, eps))
+        L.add_inplace(x, mlp(L.rmsnorm(x, ln2, eps)))
+        return x
+
+    def mlp_on_entry(x, ln1, ln2, eps, attention, mlp):
+        a = attention(L.rmsnorm(x, ln1, eps))
+        h = L.rmsnorm(x + a, ln2, eps)
+        L.add_inplace(x, mlp(h))
+        return x
+
+    def attn_norm_of_nothing(x, ln1, ln2, eps, attention, mlp):
+        L.add_inplace(x, attention(L.rmsnorm(x * x, ln1, eps)))
+        L.add_inplace(x, mlp(L.rmsnorm(x, ln2, eps)))
+        return x
+
+    for name in ("smollm2", "llama31"):
+        for wrong in (ln2_from_input, no_attn_residual, mlp_on_entry, attn_norm_of_nothing):
+            err = _composition_errors(name, wrong)
+            assert max(err.values()) > 1e-3, (name, wrong.__name__, err)
