@@ -65,8 +65,8 @@ def copy_calibration(mib):
 
 
 def contexts(n, lo, hi, seed):
-    rng = np.random.default_rng(seed)
-    return np.round(np.exp(rng.uniform(math.log(lo), math.log(hi), n))).astype(int)
+    from chattorrent_amd import configs
+    return configs.workload_contexts(n, lo, hi, seed)
 
 
 def step_bytes(d, pasts):

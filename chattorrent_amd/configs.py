@@ -51,3 +51,13 @@ QWEN38 = dict(hidden=5120, n_layer=64, n_heads=24, n_kv_heads=4, head_dim=256, f
               rms_eps=1e-6, rope_theta=1e7, rot_dim=64, tied=False, hybrid=True,
               layer_types=["linear_attention", "linear_attention", "linear_attention", "full_attention"] * 16,
               lin_nk=16, lin_nv=48, lin_dk=128, lin_dv=128, lin_conv=4, mtp_vocab=65536)
+
+
+def workload_contexts(n, lo, hi, seed):
+    """The benchmark's seeded contexts: n past lengths log-uniform in
+    [lo, hi] (configs[2]: 32 chats in [128, 16384], seed 1234)."""
+    import math
+
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    return np.round(np.exp(rng.uniform(math.log(lo), math.log(hi), n))).astype(int)

@@ -100,6 +100,13 @@ uint64_t orc_rng(uint64_t seed, uint64_t stream, uint64_t i) {
     return smix(smix(seed ^ (stream * 0xD1B54A32D192ED03ull)) + i);
 }
 
+/* orc_rng with the (seed, stream) key computed once: rng_at(key_of(s, t), i)
+ * == orc_rng(s, t, i). */
+static inline uint64_t key_of(uint64_t seed, uint64_t stream) {
+    return smix(seed ^ (stream * 0xD1B54A32D192ED03ull));
+}
+static inline uint64_t rng_at(uint64_t key, uint64_t i) { return smix(key + i); }
+
 /* Irwin-Hall sum of four 16-bit uniforms, centred: std 37837.2. */
 static inline int64_t ih4(uint64_t r) {
     return (int64_t)(r & 0xffffu) + (int64_t)((r >> 16) & 0xffffu)
@@ -125,9 +132,10 @@ uint16_t orc_gen_scale_f16(uint64_t seed, uint64_t stream, uint64_t i, double lo
 void orc_gen_q8(uint64_t seed, uint64_t stream, int64_t N, int64_t K, int group,
                 int8_t* codes, uint16_t* scales_f16) {
     int64_t ng = (K + group - 1) / group;
+    const uint64_t kc = key_of(seed, stream);
     #pragma omp parallel for schedule(static)
     for (int64_t n = 0; n < N; n++) {
-        for (int64_t k = 0; k < K; k++) codes[n * K + k] = gen_code(orc_rng(seed, stream, (uint64_t)(n * K + k)));
+        for (int64_t k = 0; k < K; k++) codes[n * K + k] = gen_code(rng_at(kc, (uint64_t)(n * K + k)));
         for (int64_t g = 0; g < ng; g++)
             scales_f16[n * ng + g] = orc_gen_scale_f16(seed, stream ^ 0x5ca1eull, (uint64_t)(n * ng + g), 1e-4, 4e-4);
     }
@@ -164,6 +172,32 @@ void orc_gen_kv(uint64_t seed, uint64_t stream, uint64_t key, int t0, int tokens
             }
             scales[(int64_t)t * nKV + n] =
                 orc_half_value(orc_gen_scale_f16(seed, stream ^ 0x5ca1eull, base, 0.005, 0.02));
+        }
+}
+
+/* The rows orc_gen_kv generates for a chat (`key`), tokens 0..tokens-1,
+ * written straight into a paged cache in the reference's row layout
+ * (web/model/kernels.js:999-1022: D/4 code words, then the f32 scale once per
+ * 32-value block; row at ((pages[t/page]*nKV + n)*page + t%page)*RW). The
+ * same bits as orc_gen_kv followed by a row-by-row copy; this form only
+ * saves the full-depth parity tests the copy. */
+void orc_fill_kv_paged(uint64_t seed, uint64_t stream, uint64_t key, int tokens, int nKV, int D,
+                       int page, const uint32_t* pages, uint32_t* cache) {
+    const int QB = D < 32 ? D : 32, nb = D / QB, RW = D / 4 + nb;
+    const uint64_t kc = key_of(seed, stream);
+    #pragma omp parallel for schedule(static)
+    for (int t = 0; t < tokens; t++)
+        for (int n = 0; n < nKV; n++) {
+            uint64_t base = (key << 24) + (uint64_t)t;
+            base = base * (uint64_t)nKV + (uint64_t)n;
+            uint32_t* row = cache + (((int64_t)pages[t / page] * nKV + n) * page + t % page) * RW;
+            uint8_t* bytes = (uint8_t*)row;
+            for (int d = 0; d < D; d++) {
+                uint64_t r = rng_at(kc, base * (uint64_t)D + (uint64_t)d);
+                bytes[d] = (uint8_t)(int8_t)((int)((r >> 8) % 255u) - 127);
+            }
+            const uint32_t sb = f2u(orc_half_value(orc_gen_scale_f16(seed, stream ^ 0x5ca1eull, base, 0.005, 0.02)));
+            for (int b = 0; b < nb; b++) row[D / 4 + b] = sb;
         }
 }
 
@@ -430,15 +464,17 @@ void orc_attn_av(const float* scores, const uint32_t* V, float* out, int T_new, 
         for (int tn = 0; tn < T_new; tn++) {
             const int kvh = h / group;
             const float* p = scores + ((int64_t)h * T_new + tn) * T_act;
-            for (int d = 0; d < D; d++) {
-                float sum = 0.0f;
-                for (int i = 0; i < T_act; i++) {
-                    int64_t r = (((int64_t)pages[i / page] * nKV + kvh) * page + i % page) * RW;
-                    float q = (float)((const int8_t*)(V + r))[d];
-                    sum += p[i] * (q * u2f(V[r + D / 4 + d / QB]));
-                }
-                out[((int64_t)h * T_q + r0 + tn) * D + d] = sum;
+            float sum[256];
+            for (int d = 0; d < D; d++) sum[d] = 0.0f;
+            /* every channel's sum runs over the tokens in order; walking the
+             * tokens outermost reads each V row once */
+            for (int i = 0; i < T_act; i++) {
+                int64_t r = (((int64_t)pages[i / page] * nKV + kvh) * page + i % page) * RW;
+                const int8_t* q8 = (const int8_t*)(V + r);
+                const float pi = p[i];
+                for (int d = 0; d < D; d++) sum[d] += pi * ((float)q8[d] * u2f(V[r + D / 4 + d / QB]));
             }
+            for (int d = 0; d < D; d++) out[((int64_t)h * T_q + r0 + tn) * D + d] = sum[d];
         }
 }
 

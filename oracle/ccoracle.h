@@ -35,6 +35,8 @@ uint16_t orc_gen_scale_f16(uint64_t seed, uint64_t stream, uint64_t i,
                            double lo, double hi);
 void orc_gen_kv(uint64_t seed, uint64_t stream, uint64_t key, int t0, int tokens, int nKV,
                 int D, int8_t* codes, float* scales);
+void orc_fill_kv_paged(uint64_t seed, uint64_t stream, uint64_t key, int tokens, int nKV, int D,
+                       int page, const uint32_t* pages, uint32_t* cache);
 
 /* --- kernels (web/model/kernels.js) --- */
 void orc_matmul_q8(const float* X, int M, int K, const int8_t* W, const float* S,

@@ -33,6 +33,7 @@ def lib():
             "orc_gen_ids": (None, [u64, u64, i64, i32, P]),
             "orc_gen_scale_f16": (C.c_uint16, [u64, u64, u64, f64, f64]),
             "orc_gen_kv": (None, [u64, u64, u64, i32, i32, i32, i32, P, P]),
+            "orc_fill_kv_paged": (None, [u64, u64, u64, i32, i32, i32, i32, P, P]),
             "orc_matmul_q8": (None, [P, i32, i32, P, P, i32, i32, P]),
             "orc_gather_embed_q8": (None, [P, i32, i32, P, P, i32, P]),
             "orc_rmsnorm": (None, [P, P, P, i32, i32, f32]),
@@ -120,6 +121,15 @@ def gen_kv(seed, stream, key, t0, tokens, nKV, D):
     scales = np.empty((tokens, nKV), np.float32)
     lib().orc_gen_kv(seed, stream, key, t0, tokens, nKV, D, _p(codes), _p(scales))
     return codes, scales
+
+
+def fill_kv_paged(seed, stream, key, tokens, nKV, D, page, pages, cache):
+    """gen_kv's rows 0..tokens-1 written into a paged cache (u32 words,
+    reference row layout) through the page table `pages`."""
+    pages = _c(pages, np.uint32)
+    assert cache.dtype == np.uint32 and cache.flags.c_contiguous
+    assert len(pages) * page >= tokens
+    lib().orc_fill_kv_paged(seed, stream, key, tokens, nKV, D, page, _p(pages), _p(cache))
 
 
 # --- kernels ---------------------------------------------------------------

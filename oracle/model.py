@@ -195,6 +195,8 @@ class Model:
         d, g = self.d, self.group
         lw = self.w["layers"][layer]
 
+        seen = {}
+
         def attention(h):
             q = L.matmul_q8(h, *lw["q"], group=g)
             k = L.matmul_q8(h, *lw["k"], group=g)
@@ -203,15 +205,22 @@ class Model:
             for s in segs:
                 a, b = s["row"], s["row"] + s["n"]
                 merged[a:b] = self.attend(layer, s["slot"], q[a:b], k[a:b], v[a:b], s["past"])
-            return L.matmul_q8(merged, *lw["o"], group=g)
+            seen["attn"] = L.matmul_q8(merged, *lw["o"], group=g)
+            return seen["attn"]
 
         def mlp(h):
             act = L.silu_mul(L.matmul_q8(h, *lw["gate"], group=g), L.matmul_q8(h, *lw["up"], group=g))
-            return L.matmul_q8(act, *lw["down"], group=g)
+            seen["mlp"] = L.matmul_q8(act, *lw["down"], group=g)
+            return seen["mlp"]
 
         compose_block(x, lw["ln1"], lw["ln2"], d["rms_eps"], attention, mlp)
+        if getattr(self, "on_sublayers", None) is not None:
+            self.on_sublayers(layer, seen["attn"], seen["mlp"])
         L.lib().orc_round_f16(L._p(x), x.size)
         return x
+
+    def _run_block(self, layer, x, segs):
+        self.block(layer, x, segs)
 
     def pass_(self, jobs, layers=None, head=True, capture=None):
         """One packed pass. `jobs`: dicts with slot, past, n, and ids [n] (or
@@ -239,7 +248,7 @@ class Model:
             x = np.ascontiguousarray(np.concatenate([np.asarray(j["hidden"], np.float32) for j in jobs]))
         assert x.shape == (T, H)
         for layer in (range(d["n_layer"]) if layers is None else layers):
-            self.block(layer, x, segs)
+            self._run_block(layer, x, segs)
             if capture is not None:
                 capture(layer, x)
         out = []
@@ -269,3 +278,87 @@ class Model:
         return out
 
 
+
+
+class StreamedModel(Model):
+    """Model at a full model's depth with bounded host memory, for the
+    full-size parity tests: a block's q8 weights and
+    its random KV rows are regenerated from the counter-based generator each
+    time the block runs, into one layer's worth of buffers, and only the K/V
+    rows the passes append are kept between passes. The arithmetic is
+    Model's: the same block, attention and head, in the same order.
+
+    `contexts`: per slot, (tokens of random KV, generator key), filled as
+    Model.fill_random_kv fills them; every frame takes the pages for
+    tokens + `extra` up front, in slot order."""
+
+    def __init__(self, d, seed, contexts, extra, page_tokens=PAGE_TOKENS):
+        self.d = d
+        self.seed = seed
+        self.group = d.get("group_q8", 32)
+        self.page = page_tokens
+        n_max = max(T for T, _ in contexts) + extra
+        self.max_pages = -(-n_max // page_tokens)
+        need = [-(-(T + extra) // page_tokens) for T, _ in contexts]
+        self.pool = PagePool(sum(need), page_tokens)
+        D, nKV = d["head_dim"], d["n_kv_heads"]
+        self.rw = kv_row_words(D)
+        words = self.pool.n_pages * nKV * page_tokens * self.rw
+        self._kv = (np.zeros(words, np.uint32), np.zeros(words, np.uint32))
+        self.K = [None] * d["n_layer"]
+        self.V = [None] * d["n_layer"]
+        self.frames = [{"pages": np.zeros(self.max_pages, np.uint32), "owned": [], "max_pages": self.max_pages}
+                       for _ in contexts]
+        for frame, (T, _) in zip(self.frames, contexts):
+            self.pool.ensure(frame, T + extra)
+        self.contexts = list(contexts)
+        self.rot = d.get("rot_dim", D)
+        self.tbl = L.rope_table(self.rot, d["rope_theta"], self.max_pages * page_tokens + 64, d.get("rope_scaling"))
+        g = self.group
+        self.w = {"layers": [None] * d["n_layer"], "norm": np.ones(d["hidden"], np.float32)}
+        codes, sc = L.gen_q8(seed, STREAM_WTE, d["vocab"], d["hidden"], g)
+        self.w["wte"] = (codes, L.from_f16(sc))
+        if not d.get("tied", True):
+            codes, sc = L.gen_q8(seed, STREAM_LM_HEAD, d["vocab"], d["hidden"], g)
+            self.w["lm_head"] = (codes, L.from_f16(sc))
+        # layer -> {(slot, t): (K words [nKV, RW], V words [nKV, RW])}
+        self.kept = [dict() for _ in range(d["n_layer"])]
+        self.on_layer = None   # called with each block index once it has run
+
+    def _rows(self, slot, t):
+        nKV = self.d["n_kv_heads"]
+        page = self.frames[slot]["pages"][t // self.page].astype(np.int64)
+        return (((page * nKV + np.arange(nKV)) * self.page + t % self.page) * self.rw)[:, None] + np.arange(self.rw)
+
+    def _load(self, layer):
+        d, g = self.d, self.group
+        lw = {}
+        for name, (N, K) in tensor_shapes(d).items():
+            codes, sc = L.gen_q8(self.seed, layer_stream(layer, name), N, K, g)
+            lw[name] = (codes, L.from_f16(sc))
+        lw["ln1"] = np.ones(d["hidden"], np.float32)
+        lw["ln2"] = np.ones(d["hidden"], np.float32)
+        self.w["layers"][layer] = lw
+        for which, buf in enumerate(self._kv):
+            for slot, (T, key) in enumerate(self.contexts):
+                if T:
+                    L.fill_kv_paged(self.seed, kv_stream(layer, which), key, T, d["n_kv_heads"], d["head_dim"],
+                                    self.page, self.frames[slot]["pages"], buf)
+            for (slot, t), rows in self.kept[layer].items():
+                buf[self._rows(slot, t)] = rows[which]
+        self.K[layer], self.V[layer] = self._kv
+
+    def _run_block(self, layer, x, segs):
+        self._load(layer)
+        self.block(layer, x, segs)
+        for s in segs:
+            for t in range(s["past"], s["past"] + s["n"]):
+                r = self._rows(s["slot"], t)
+                self.kept[layer][(s["slot"], t)] = (self._kv[0][r].copy(), self._kv[1][r].copy())
+        self.w["layers"][layer] = None
+        self.K[layer] = self.V[layer] = None
+        if self.on_layer is not None:
+            self.on_layer(layer)
+
+    def fill_random_kv(self, slot, tokens, seed, key):
+        raise NotImplementedError("a StreamedModel's KV is given at construction")

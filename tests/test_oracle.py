@@ -475,3 +475,60 @@ def test_block_composition_check_catches_misplaced_parts():
         for wrong in (ln2_from_input, no_attn_residual, mlp_on_entry, attn_norm_of_nothing):
             err = _composition_errors(name, wrong)
             assert max(err.values()) > 1e-3, (name, wrong.__name__, err)
+
+
+def test_streamed_model_equals_model_over_passes():
+    """Model.StreamedModel (weights and random KV regenerated per block, only
+    the appended K/V rows kept) gives Model's bits: two consecutive passes,
+    the second over the rows the first appended, logits and ids equal bitwise;
+    and the paged KV fill writes the same words as Model.fill_random_kv."""
+    d = dict(hidden=128, n_layer=3, n_heads=4, n_kv_heads=2, head_dim=32, ffn=192, vocab=500,
+             rms_eps=1e-5, rope_theta=1e4, tied=True)
+    ctxs = [(40, 1), (0, 2), (130, 3)]
+    extra = 8
+    sm = Mo.StreamedModel(d, 5, ctxs, extra)
+    m = Mo.Model(d, n_slots=3, max_pages=sm.max_pages, n_pages=sm.pool.n_pages)
+    m.gen_weights(5)
+    for s, (T, key) in enumerate(ctxs):
+        m.pool.ensure(m.frames[s], T + extra)
+        if T:
+            m.fill_random_kv(s, T, 5, key)
+    assert all(np.array_equal(a["pages"], b["pages"]) for a, b in zip(m.frames, sm.frames))
+    # the paged fill against the row-by-row copy: layer 2's whole K and V pools
+    sm._load(2)
+    for which in (0, 1):
+        assert np.array_equal(sm._kv[which], (m.K, m.V)[which][2])
+    jobs = [dict(slot=0, past=40, n=1, ids=[7], sampled=1, topk=3),
+            dict(slot=1, past=0, n=5, ids=[1, 2, 3, 4, 5], sampled=1, topk=3),
+            dict(slot=2, past=130, n=2, ids=[9, 8], sampled=2, topk=3)]
+    for _ in range(2):
+        a, b = m.pass_(jobs), sm.pass_(jobs)
+        for ra, rb in zip(a, b):
+            assert np.array_equal(ra["logits"].view(np.uint32), rb["logits"].view(np.uint32))
+            assert np.array_equal(ra["ids"], rb["ids"])
+        jobs = [dict(j, past=j["past"] + j["n"], n=1, ids=[int(r["ids"][-1][0])], sampled=1) for j, r in zip(jobs, a)]
+
+
+def test_oracle_multi_row_job_equals_sequential_one_row_jobs():
+    """The full-depth parity test checks k greedy steps with one oracle pass of
+    k rows per chat fed the same ids: the oracle's rows are computed one by
+    one (each row's matmuls, its own causal attention limit, its own K/V
+    rows), so row i of a k-row job gives the bits of the i-th of k one-row
+    passes."""
+    d = dict(hidden=128, n_layer=2, n_heads=4, n_kv_heads=2, head_dim=32, ffn=192, vocab=500,
+             rms_eps=1e-5, rope_theta=1e4, tied=True)
+    a = Mo.Model(d, n_slots=2, max_pages=4)
+    b = Mo.Model(d, n_slots=2, max_pages=4)
+    for m in (a, b):
+        m.gen_weights(9)
+        m.fill_random_kv(0, 70, 9, 1)
+        m.fill_random_kv(1, 20, 9, 2)
+    ids = [[3, 17, 250], [8, 9, 10]]
+    seq = []
+    for i in range(3):
+        seq.append(a.pass_([dict(slot=s, past=p + i, n=1, ids=[ids[s][i]], sampled=1, topk=2)
+                            for s, p in ((0, 70), (1, 20))]))
+    multi = b.pass_([dict(slot=s, past=p, n=3, ids=ids[s], sampled=3, topk=2) for s, p in ((0, 70), (1, 20))])
+    for s in range(2):
+        for i in range(3):
+            assert np.array_equal(multi[s]["logits"][i].view(np.uint32), seq[i][s]["logits"][0].view(np.uint32))
