@@ -1,132 +1,168 @@
 'use strict';
-// Host sampler of the head, restated from the reference's sampling.js
-// (web/model/sampling.js:60-215) for the Node 12 runtime: the same limits,
-// the same candidate count for a GPU top-M, and the same arithmetic and
-// summation order, so a token drawn from the GPU's candidates is the token the
-// whole logits row would give.
+// Token sampling at the head, to the contract of the reference's sampler
+// (web/model/sampling.js:57-215): the same option limits and defaults, the
+// same candidate count for a GPU top-M (candidatesFor), and the same
+// arithmetic, so a token drawn from the GPU's candidates is the token the
+// whole logits row would give (sampling.js:107-121 requires this).
+//
+// The draw runs as four stages over a Float32Array of logits: adjust (bans,
+// then repetition/frequency/presence penalties in list order), scale by the
+// temperature, cut below the k-th largest (found with a min-heap of the k
+// best), and draw from the softmax: weights exp(v - max) summed in f64 for
+// the total, accumulated from their f32 copies for the walk, tokens in
+// ascending order. Greedy (temperature 0) is the first maximum after the
+// adjust stage. Node 12 syntax.
 
-const PEN_CAP = 1.5;   // sampling.js:57
+const PEN_CAP = 1.5;          // largest frequency penalty one token takes
+const TOPK_MAX = 256;         // the most candidates a GPU top-M returns
+
+// option -> [lowest, highest, default]; topK is truncated after clamping
+const RANGES = { temp: [0, 2, 0], topK: [0, 200, 0], rep: [1, 2, 1.0], freq: [0, 2, 0], pres: [0, 2, 0] };
+const LIST_MAX = { pen: 64, ban: 4096 };
 const LIMITS = { temp: [0, 2], topK: [0, 200], rep: [1, 2], freq: [0, 2], pres: [0, 2], pen: 64, ban: 4096 };
-const TOPK_MAX = 256;  // sampling.js:125
 
-function clampNumber(v, range, dflt) {
-    if (typeof v !== 'number' || !Number.isFinite(v)) return dflt;
-    return Math.min(range[1], Math.max(range[0], v));
-}
-
-// clampSampling (sampling.js:74-94): a job's options, clamped; an unusable
-// value falls back to the default instead of failing the job.
+// A job's options as the sampler uses them. Unusable numbers take their
+// default; penalty entries must be [id, count >= 0] and bans ids, both within
+// the vocabulary, and each list keeps only its first LIST_MAX entries.
 function clampSampling(opts, vocab) {
     const o = opts || {};
     const V = vocab === undefined ? Infinity : vocab;
-    const validId = (v) => Number.isInteger(v) && v >= 0 && v < V;
-    const out = {
-        temp: clampNumber(o.temp, LIMITS.temp, 0),
-        topK: Math.trunc(clampNumber(o.topK, LIMITS.topK, 0)),
-        rep: clampNumber(o.rep, LIMITS.rep, 1.0),
-        freq: clampNumber(o.freq, LIMITS.freq, 0),
-        pres: clampNumber(o.pres, LIMITS.pres, 0),
-        pen: null,
-        ban: null,
-    };
-    if (Array.isArray(o.pen)) {
-        out.pen = o.pen.slice(0, LIMITS.pen).filter((p) =>
-            Array.isArray(p) && validId(p[0]) && Number.isFinite(p[1]) && p[1] >= 0);
+    const out = {};
+    for (const name of Object.keys(RANGES)) {
+        const [lo, hi, dflt] = RANGES[name];
+        const v = o[name];
+        out[name] = typeof v === 'number' && Number.isFinite(v) ? Math.min(hi, Math.max(lo, v)) : dflt;
     }
-    if (Array.isArray(o.ban)) out.ban = o.ban.slice(0, LIMITS.ban).filter(validId);
+    out.topK = Math.trunc(out.topK);
+    const isId = (v) => Number.isInteger(v) && v >= 0 && v < V;
+    out.pen = Array.isArray(o.pen)
+        ? o.pen.slice(0, LIST_MAX.pen).filter((e) => Array.isArray(e) && isId(e[0]) && Number.isFinite(e[1]) && e[1] >= 0)
+        : null;
+    out.ban = Array.isArray(o.ban) ? o.ban.slice(0, LIST_MAX.ban).filter(isId) : null;
     return out;
 }
 
-function penalised(c) {
-    return c.pen && (c.rep !== 1.0 || c.freq !== 0 || c.pres !== 0);
-}
+const penalises = (c) => c.pen !== null && (c.rep !== 1.0 || c.freq !== 0 || c.pres !== 0);
 
-// candidatesFor (sampling.js:123-143): raw top logits a row needs, or null
-// when only the whole row will do.
+// The raw top logits a row needs for these options (1 for greedy, top-k plus
+// every banned or penalised token), or null when only the whole row will do
+// (temperature without top-k, or more than TOPK_MAX candidates).
 function candidatesFor(opts, vocab) {
     const c = clampSampling(opts, vocab);
-    let k;
-    if (c.temp <= 0) k = 1;
-    else if (c.topK > 0 && c.topK < vocab) k = c.topK;
-    else return null;
-    const hit = new Set(c.ban || []);
-    if (penalised(c)) for (const p of c.pen) hit.add(p[0]);
-    const m = k + hit.size;
+    let width = null;
+    if (c.temp <= 0) width = 1;
+    else if (c.topK > 0 && c.topK < vocab) width = c.topK;
+    if (width === null) return null;
+    const touched = new Set(c.ban || []);
+    if (penalises(c)) c.pen.forEach((e) => touched.add(e[0]));
+    const m = width + touched.size;
     return m > TOPK_MAX ? null : Math.min(m, vocab);
 }
 
-// The sampler over `vals` (every token when ids is null, else the tokens
-// `ids` in ascending order) — sampleCore, sampling.js:145-215.
-function sampleCore(vals, ids, opts, vocab, random) {
-    const c = clampSampling(opts, vocab);
-    const adj = Float32Array.from(vals);
-    let index = (id) => id;
-    if (ids) {
-        const where = new Map();
-        ids.forEach((id, i) => where.set(id, i));
-        index = (id) => where.get(id);
-    }
-    const tokenAt = (i) => (ids ? ids[i] : i);
+// Stage 1: bans to -inf, then penalties, on a copy of the logits. `where`
+// maps a token to its index in `vals` (undefined: not among them).
+function adjust(vals, where, c) {
+    const out = Float32Array.from(vals);
     if (c.ban) {
         for (const id of c.ban) {
-            const i = index(id);
-            if (i !== undefined) adj[i] = -Infinity;
+            const i = where(id);
+            if (i !== undefined) out[i] = -Infinity;
         }
     }
-    if (penalised(c)) {
-        for (const p of c.pen) {
-            const i = index(p[0]);
+    if (penalises(c)) {
+        for (const [id, count] of c.pen) {
+            const i = where(id);
             if (i === undefined) continue;
-            let v = adj[i];
+            let v = out[i];
             if (c.rep !== 1.0) v = v > 0 ? v / c.rep : v * c.rep;
-            v -= c.pres + Math.min(c.freq * p[1], PEN_CAP);
-            adj[i] = v;
+            out[i] = v - (c.pres + Math.min(c.freq * count, PEN_CAP));
         }
     }
+    return out;
+}
+
+// The k-th largest value of `a` (-inf when it has fewer than k): a min-heap
+// of the k best seen so far, whose root is the answer at the end.
+function kthLargest(a, k) {
+    if (a.length < k) return -Infinity;
+    const heap = new Float32Array(k);
+    const down = (i) => {
+        for (;;) {
+            const l = 2 * i + 1, r = l + 1;
+            let m = i;
+            if (l < k && heap[l] < heap[m]) m = l;
+            if (r < k && heap[r] < heap[m]) m = r;
+            if (m === i) return;
+            const t = heap[i];
+            heap[i] = heap[m];
+            heap[m] = t;
+            i = m;
+        }
+    };
+    for (let i = 0; i < k; i++) heap[i] = a[i];
+    for (let i = (k >> 1) - 1; i >= 0; i--) down(i);
+    for (let i = k; i < a.length; i++) {
+        if (a[i] > heap[0]) {
+            heap[0] = a[i];
+            down(0);
+        }
+    }
+    return heap[0];
+}
+
+// Stage 4: the index drawn from softmax(w) with u in [0, 1).
+function drawIndex(w, u) {
+    let top = -Infinity;
+    for (let i = 0; i < w.length; i++) if (w[i] > top) top = w[i];
+    let total = 0;
+    for (let i = 0; i < w.length; i++) {
+        const e = w[i] === -Infinity ? 0 : Math.exp(w[i] - top);
+        w[i] = e;            // the walk below adds these f32 copies
+        total += e;
+    }
+    const target = u * total;
+    let run = 0;
+    for (let i = 0; i < w.length; i++) {
+        run += w[i];
+        if (target < run) return i;
+    }
+    return w.length - 1;
+}
+
+// vals: logits of every token (ids null) or of `ids` in ascending order.
+function drawToken(vals, ids, opts, vocab, random) {
+    const c = clampSampling(opts, vocab);
+    let where = (id) => id;
+    if (ids) {
+        const pos = new Map();
+        for (let i = 0; i < ids.length; i++) pos.set(ids[i], i);
+        where = (id) => pos.get(id);
+    }
+    const tokenAt = (i) => (ids ? ids[i] : i);
+    const adj = adjust(vals, where, c);
     if (c.temp <= 0) {
-        let best = 0, bestV = -Infinity;
-        for (let i = 0; i < adj.length; i++) if (adj[i] > bestV) { bestV = adj[i]; best = i; }
+        let best = 0;
+        let bestV = -Infinity;
+        adj.forEach((v, i) => { if (v > bestV) { bestV = v; best = i; } });
         return tokenAt(best);
     }
-    const scaled = adj.map((v) => v / c.temp);
+    const w = adj.map((v) => v / c.temp);
     if (c.topK > 0 && c.topK < vocab) {
-        // k-th largest by an insertion-sorted window of the k best
-        const win = new Float32Array(c.topK).fill(-Infinity);
-        for (let i = 0; i < scaled.length; i++) {
-            const v = scaled[i];
-            if (v <= win[c.topK - 1]) continue;
-            let j = c.topK - 1;
-            while (j > 0 && win[j - 1] < v) { win[j] = win[j - 1]; j--; }
-            win[j] = v;
-        }
-        const cut = win[c.topK - 1];
-        for (let i = 0; i < scaled.length; i++) if (scaled[i] < cut) scaled[i] = -Infinity;
+        const cut = kthLargest(w, c.topK);
+        for (let i = 0; i < w.length; i++) if (w[i] < cut) w[i] = -Infinity;
     }
-    let mx = -Infinity;
-    for (const v of scaled) if (v > mx) mx = v;
-    let sum = 0;
-    for (let i = 0; i < scaled.length; i++) {
-        const e = scaled[i] === -Infinity ? 0 : Math.exp(scaled[i] - mx);
-        scaled[i] = e;
-        sum += e;
-    }
-    const r = (random || Math.random)() * sum;
-    let acc = 0;
-    for (let i = 0; i < scaled.length; i++) {
-        acc += scaled[i];
-        if (r < acc) return tokenAt(i);
-    }
-    return tokenAt(scaled.length - 1);
+    return tokenAt(drawIndex(w, (random || Math.random)()));
 }
 
+// A whole logits row (the reference's full-row readback).
 function sampleFromLogitsRow(row, opts, random) {
-    return sampleCore(row, null, opts, row.length, random);
+    return drawToken(row, null, opts, row.length, random);
 }
 
-// sampleFromCandidates (sampling.js:112-121): the GPU's top-M (any order).
+// The GPU's top-M candidates (any order): drawn over them in token order.
 function sampleFromCandidates(ids, vals, opts, vocab, random) {
-    const order = Array.from(ids.keys()).sort((a, b) => ids[a] - ids[b]);
-    return sampleCore(Float32Array.from(order, (i) => vals[i]), order.map((i) => ids[i]), opts, vocab, random);
+    const pairs = Array.from(ids, (id, i) => [id, vals[i]]).sort((a, b) => a[0] - b[0]);
+    return drawToken(Float32Array.from(pairs, (p) => p[1]), pairs.map((p) => p[0]), opts, vocab, random);
 }
 
 module.exports = { LIMITS, TOPK_MAX, clampSampling, candidatesFor, sampleFromLogitsRow, sampleFromCandidates };

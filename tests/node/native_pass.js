@@ -12,9 +12,9 @@ const wire = require('../../chattorrent_amd/node/wire');
 // (web/net.js framing, fragmented at a small limit so multi-fragment
 // messages are exercised).
 function overTheLink(h, rows) {
-    const st = {};
+    const st = new wire.Reassembler();
     let msg = null;
-    for (const f of wire.fragment(wire.pack({ k: 'job', s: h.s, n: h.n }, rows), 4096, 1)) msg = wire.reassemble(st, f);
+    for (const f of wire.fragment(wire.pack({ k: 'job', s: h.s, n: h.n }, rows), 4096, 1)) msg = st.push(f);
     return wire.unpack(msg).payload;
 }
 

@@ -241,6 +241,29 @@ test('append loads one position at a time and moves `have`', async () => {
     assert.strictEqual(out.at, END);
 });
 
+test('embed, head and w (engine.js:457, :641-642); growth is refused with a clear error', async () => {
+    const whole = make().r;
+    assert.strictEqual(whole.embed, true);
+    assert.strictEqual(whole.head, true);
+    const mid = make({ lo: 1, hi: 3, have: 1 }).r;
+    assert.strictEqual(mid.embed, false);
+    assert.strictEqual(mid.head, false);
+    const q8 = (n) => ({ codes: new Int8Array(n), scales: new Uint16Array(n / 32), group: 32 });
+    const block = { q_proj: q8(64), k_proj: q8(64), v_proj: q8(64), o_proj: q8(64), gate_proj: q8(64),
+                    up_proj: q8(64), down_proj: q8(64), input_layernorm: new Float32Array(8),
+                    post_attention_layernorm: new Float32Array(8) };
+    mid.append(block);
+    assert.strictEqual(mid.w.layers.length, 1);
+    assert.deepStrictEqual(mid.w.layers[0].q_proj, { q8: true, values: 64, group: 32 });
+    assert.strictEqual(mid.w.wte, null);
+    const ends = make({ have: 0 }).r;
+    ends.append({ wte: q8(64) });
+    assert.deepStrictEqual(ends.w.wte, { q8: true, values: 64, group: 32 });
+    for (const grow of ['prepend', 'growLeft', 'growRight']) {
+        assert.throws(() => mid[grow]({}), new RegExp(`${grow}: this Runner's positions 1–2 are fixed`));
+    }
+});
+
 test('sampler: a row drawn from its GPU candidates equals the whole-row draw', async () => {
     let seed = 12345;
     const rnd = () => ((seed = (seed * 1103515245 + 12345) % 2147483648) / 2147483648);
