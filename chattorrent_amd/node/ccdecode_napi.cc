@@ -21,7 +21,8 @@ namespace {
 
 struct Ctx {
     cc_ctx* ctx = nullptr;
-    bool busy = false;
+    bool busy = false;       // a step runs on a worker thread
+    bool orphan = false;     // finalized during a step: the step's completion frees it
     int32_t hidden = 0, vocab = 0;
 };
 
@@ -95,11 +96,30 @@ Ctx* unwrap(napi_env env, napi_value v) {
     return c;
 }
 
-void finalize_ctx(napi_env, void* data, void*) {
-    Ctx* c = (Ctx*)data;
-    if (c->ctx && !c->busy) cc_destroy(c->ctx);
+// A context that is not running a step: every call but step() and
+// destroy() goes through here, so none races the worker thread's cc_step.
+Ctx* idle(napi_env env, napi_value v, const char* what) {
+    Ctx* c = unwrap(env, v);
+    if (c && c->busy) {
+        throw_status(env, CC_EARG, std::string(what) + "() while a step is running on this context");
+        return nullptr;
+    }
+    return c;
+}
+
+void destroy_ctx(Ctx* c) {
+    if (c->ctx) cc_destroy(c->ctx);
     c->ctx = nullptr;
     delete c;
+}
+
+// A running step holds a reference to its context's external, so this runs
+// during a step only when the environment itself goes away; the step's
+// completion then frees the context.
+void finalize_ctx(napi_env, void* data, void*) {
+    Ctx* c = (Ctx*)data;
+    if (c->busy) c->orphan = true;
+    else destroy_ctx(c);
 }
 
 // Typed-array contents (pointer, element count, type).
@@ -250,7 +270,7 @@ napi_value FillRandom(napi_env env, napi_callback_info info) {
     size_t argc = 2;
     napi_value argv[2];
     NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
-    Ctx* c = unwrap(env, argv[0]);
+    Ctx* c = idle(env, argv[0], "fillRandom");
     if (!c) return nullptr;
     return status_result(env, c, cc_fill_random(c->ctx, argc > 1 ? u64(env, argv[1]) : 1));
 }
@@ -260,7 +280,7 @@ napi_value FillRandomKV(napi_env env, napi_callback_info info) {
     size_t argc = 5;
     napi_value argv[5];
     NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
-    Ctx* c = unwrap(env, argv[0]);
+    Ctx* c = idle(env, argv[0], "fillRandomKV");
     if (!c) return nullptr;
     int32_t slot = 0, tokens = 0;
     napi_get_value_int32(env, argv[1], &slot);
@@ -275,7 +295,7 @@ napi_value Upload(napi_env env, napi_callback_info info) {
     size_t argc = 6;
     napi_value argv[6];
     NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
-    Ctx* c = unwrap(env, argv[0]);
+    Ctx* c = idle(env, argv[0], "upload");
     if (!c) return nullptr;
     int32_t layer = 0, tensor = 0;
     napi_get_value_int32(env, argv[1], &layer);
@@ -304,6 +324,7 @@ napi_value Upload(napi_env env, napi_callback_info info) {
 // ---- step (async) ----
 struct StepWork {
     Ctx* c = nullptr;
+    napi_ref keep = nullptr;        // the context's external, alive until the step completes
     napi_deferred deferred = nullptr;
     napi_async_work work = nullptr;
     std::vector<cc_job> jobs;
@@ -339,6 +360,8 @@ napi_value copy_out(napi_env env, const std::vector<T>& v, napi_typedarray_type 
 void step_complete(napi_env env, napi_status, void* data) {
     StepWork* w = (StepWork*)data;
     w->c->busy = false;
+    if (w->keep) napi_delete_reference(env, w->keep);
+    if (w->c->orphan) destroy_ctx(w->c);
     napi_value res;
     napi_create_object(env, &res);
     napi_value code;
@@ -423,6 +446,7 @@ napi_value Step(napi_env env, napi_callback_info info) {
     NAPI_OK(napi_create_promise(env, &w->deferred, &promise));
     napi_create_string_utf8(env, "ccdecode.step", NAPI_AUTO_LENGTH, &name);
     NAPI_OK(napi_create_async_work(env, nullptr, name, step_execute, step_complete, w, &w->work));
+    NAPI_OK(napi_create_reference(env, argv[0], 1, &w->keep));
     c->busy = true;
     NAPI_OK(napi_queue_async_work(env, w->work));
     return promise;
@@ -432,7 +456,7 @@ napi_value Release(napi_env env, napi_callback_info info) {
     size_t argc = 2;
     napi_value argv[2];
     NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
-    Ctx* c = unwrap(env, argv[0]);
+    Ctx* c = idle(env, argv[0], "release");
     if (!c) return nullptr;
     int32_t slot = 0;
     napi_get_value_int32(env, argv[1], &slot);
@@ -443,7 +467,7 @@ napi_value SlotPages(napi_env env, napi_callback_info info) {
     size_t argc = 2;
     napi_value argv[2];
     NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
-    Ctx* c = unwrap(env, argv[0]);
+    Ctx* c = idle(env, argv[0], "slotPages");
     if (!c) return nullptr;
     int32_t slot = 0;
     napi_get_value_int32(env, argv[1], &slot);
@@ -456,7 +480,7 @@ napi_value FreePages(napi_env env, napi_callback_info info) {
     size_t argc = 1;
     napi_value argv[1];
     NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
-    Ctx* c = unwrap(env, argv[0]);
+    Ctx* c = idle(env, argv[0], "freePages");
     if (!c) return nullptr;
     napi_value r;
     napi_create_int32(env, cc_free_pages(c->ctx), &r);
@@ -468,7 +492,7 @@ napi_value ReadLogits(napi_env env, napi_callback_info info) {
     size_t argc = 2;
     napi_value argv[2];
     NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
-    Ctx* c = unwrap(env, argv[0]);
+    Ctx* c = idle(env, argv[0], "readLogits");
     if (!c) return nullptr;
     int32_t rows = 0;
     napi_get_value_int32(env, argv[1], &rows);
@@ -495,7 +519,7 @@ napi_value MtpDraft(napi_env env, napi_callback_info info) {
         napi_throw_type_error(env, nullptr, "mtpDraft(ctx, slot, row, token, pos, k)");
         return nullptr;
     }
-    Ctx* c = unwrap(env, argv[0]);
+    Ctx* c = idle(env, argv[0], "mtpDraft");
     if (!c) return nullptr;
     int32_t a[5] = {0, 0, 0, 0, 0};
     for (int i = 0; i < 5; i++) napi_get_value_int32(env, argv[1 + i], &a[i]);
@@ -513,7 +537,7 @@ napi_value Stats(napi_env env, napi_callback_info info) {
     size_t argc = 1;
     napi_value argv[1];
     NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
-    Ctx* c = unwrap(env, argv[0]);
+    Ctx* c = idle(env, argv[0], "stats");
     if (!c) return nullptr;
     cc_stats s{};
     cc_stats_get(c->ctx, &s);
@@ -535,7 +559,7 @@ napi_value LastError(napi_env env, napi_callback_info info) {
     size_t argc = 1;
     napi_value argv[1];
     NAPI_OK(napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
-    Ctx* c = unwrap(env, argv[0]);
+    Ctx* c = idle(env, argv[0], "lastError");
     if (!c) return nullptr;
     const char* m = cc_last_error(c->ctx);
     napi_value r;
