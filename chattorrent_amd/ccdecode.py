@@ -27,7 +27,7 @@ EXPORTS = [
     "cc_create", "cc_destroy", "cc_last_error", "cc_upload", "cc_fill_random", "cc_step", "cc_release",
     "cc_slot_pages", "cc_free_pages", "cc_fill_random_kv", "cc_read_kv", "cc_write_kv", "cc_read_pages",
     "cc_stats_get", "cc_op_matmul_q8", "cc_op_store_kv", "cc_op_round_f16", "cc_op_topk", "cc_op_rmsnorm",
-    "cc_op_attend", "cc_profile", "cc_profile_read", "cc_read_logits", "cc_mtp_draft",
+    "cc_op_attend", "cc_profile", "cc_profile_read", "cc_read_logits", "cc_mtp_draft", "cc_topk_noalloc",
 ]
 
 

@@ -119,6 +119,7 @@ struct cc_ctx {
     float* logits = nullptr;       // LM-head planes [P][rows][vocab]
     int head_planes = 1, head_rows = 0;
     uint64_t* tk_a = nullptr;
+    uint64_t* tk_scratch = nullptr;   // this device's static scratch (cc_topk_noalloc)
     uint64_t* tk_b = nullptr;
     float* d_vals = nullptr;
     uint32_t* d_ids = nullptr;
@@ -403,6 +404,8 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
     }
     auto body = [&]() -> cc_status {
         HIPCHK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+        // the allocation-free top-k's scratch address on this device (looked up once per device)
+        HIPCHK(topk_scratch_setup(o.device, &ctx->tk_scratch));
         {
             hipDeviceProp_t prop;
             HIPCHK(hipGetDeviceProperties(&prop, o.device));
@@ -1651,6 +1654,26 @@ cc_status cc_op_topk(cc_ctx* ctx, const float* logits, int32_t rows, int32_t V, 
     HIPCHK(hipMemcpy(vals, dv, (size_t)rows * M * 4, hipMemcpyDeviceToHost));
     HIPCHK(hipMemcpy(ids, di, (size_t)rows * M * 4, hipMemcpyDeviceToHost));
     for (void* v : {(void*)dL, (void*)a, (void*)b, (void*)dv, (void*)di}) hipFree(v);
+    return CC_OK;
+}
+
+cc_status cc_topk_noalloc(cc_ctx* ctx, const float* logits, int32_t rows, int32_t V, int32_t M, float* vals,
+                          uint32_t* ids, void* stream) {
+    if (!ctx) return CC_EARG;
+    if (!logits || !vals || !ids || rows < 1 || V < 1 || M < 1 || M > TOPK_MAX || M > V)
+        return fail(ctx, CC_EARG, "bad topk: rows >= 1, 1 <= M <= min(V, 256), and device buffers");
+    if (!ctx->tk_scratch) return fail(ctx, CC_EDEVICE, "no scratch address on this device");
+    size_t a = 0, b = 0;
+    topk_stage_keys(rows, V, M, &a, &b);
+    if (a + b > TOPK_SCRATCH_KEYS)
+        return fail(ctx, CC_EARG, "topk of " + std::to_string(rows) + " rows x " + std::to_string(V) + " logits, M " +
+                                      std::to_string(M) + " stages " + std::to_string(a + b) +
+                                      " keys, above the allocation-free scratch of " +
+                                      std::to_string(TOPK_SCRATCH_KEYS) + " keys");
+    launch_topk(stream ? (hipStream_t)stream : ctx->stream, logits, 1, rows, V, M, ctx->tk_scratch,
+                ctx->tk_scratch + a, vals, ids);
+    const hipError_t e = take_launch_error();
+    if (e != hipSuccess) return fail(ctx, CC_EDEVICE, std::string("topk launch: ") + hipGetErrorString(e));
     return CC_OK;
 }
 

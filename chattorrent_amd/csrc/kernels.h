@@ -139,6 +139,15 @@ void launch_gather_rows(hipStream_t st, const float* x, const float* alt, const 
 void launch_topk(hipStream_t st, const float* logits, int planes, int rows, int V, int M, uint64_t* a,
                  uint64_t* b, float* vals, uint32_t* ids);
 void launch_round_f16(hipStream_t st, float* a, int64_t n);
+// The keys launch_topk stages for (rows, V, M): a_keys for its first buffer,
+// b_keys for its second.
+void topk_stage_keys(int rows, int V, int M, size_t* a_keys, size_t* b_keys);
+// The allocation-free top-k's scratch: a static device array of
+// TOPK_SCRATCH_KEYS keys (4 MiB) per GPU. topk_scratch_setup looks up its
+// address on `device` (which must be current) once, and returns it.
+constexpr size_t TOPK_SCRATCH_KEYS = (size_t)1 << 19;
+constexpr int TOPK_SCRATCH_DEVICES = 64;
+hipError_t topk_scratch_setup(int device, uint64_t** out);
 void launch_alloc_pages(hipStream_t st, const int32_t* plan, int njobs, const uint32_t* free_stack,
                         int top, uint32_t* page_table, int max_pages);
 void launch_release_pages(hipStream_t st, int slot, int owned, uint32_t* free_stack, int top,

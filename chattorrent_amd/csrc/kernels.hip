@@ -11,6 +11,7 @@
 #include "common.h"
 #include "kernels.h"
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 // The first launch error since the last take_launch_error(); cc_step and the
@@ -1962,6 +1963,46 @@ void launch_topk(hipStream_t st, const float* logits, int planes, int rows, int 
     }
     hipLaunchKernelGGL(k_topk_unpack, dim3((rows * M + 255) / 256), dim3(256), 0, st, out, rows, M, vals, ids);
     CHECK_LAUNCH();
+}
+
+// The staged keys launch_topk needs for (rows, V, M): the first half (`a`,
+// stages 1, 3, ...) and the second (`b`, stages 2, 4, ...), in keys.
+void topk_stage_keys(int rows, int V, int M, size_t* a_keys, size_t* b_keys) {
+    size_t sa = 0, sb = 0;
+    int n = V;
+    for (bool to_a = true;; to_a = !to_a) {
+        const int groups = (n + TOPK_CH - 1) / TOPK_CH;
+        const size_t k = (size_t)rows * groups * M;
+        if (to_a) sa = std::max(sa, k);
+        else sb = std::max(sb, k);
+        if (groups == 1) break;
+        n = M == 1 ? groups : groups * M;
+    }
+    *a_keys = sa;
+    *b_keys = sb;
+}
+
+// Scratch of the allocation-free top-k entry point (cc_topk_noalloc): the
+// staged keys, both halves. Each GPU the library runs on holds its own copy
+// until the process ends. Every key a stage reads was written by the stage
+// before it in the same call, so nothing in it needs clearing between calls.
+// In host code `scratch` names a host-side stand-in, never device memory:
+// kernels get the per-device address topk_scratch_setup() looks up.
+static __device__ __align__(256) uint64_t scratch[TOPK_SCRATCH_KEYS];
+
+hipError_t topk_scratch_setup(int device, uint64_t** out) {
+    static std::mutex mu;
+    static uint64_t* ptrs[TOPK_SCRATCH_DEVICES] = {};
+    if (device < 0 || device >= TOPK_SCRATCH_DEVICES) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptrs[device]) {
+        uint64_t* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress((void**)&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        ptrs[device] = p;
+    }
+    *out = ptrs[device];
+    return hipSuccess;
 }
 
 // ============================================================ small kernels ===

@@ -260,6 +260,20 @@ cc_status cc_op_round_f16(cc_ctx* ctx, float* a, int64_t n);
 /* topkRows — web/model/kernels.js:2129-2144: rows x V logits → M pairs. */
 cc_status cc_op_topk(cc_ctx* ctx, const float* logits, int32_t rows, int32_t V, int32_t M,
                      float* vals, uint32_t* ids);
+/* No counterpart in the reference: an allocation-free cc_op_topk for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). `logits` [rows, V] f32,
+ * `vals` and `ids` [rows, M] are DEVICE pointers the caller owns; the stages'
+ * keys go to a static 4 MiB scratch array per GPU (TOPK_SCRATCH_KEYS keys),
+ * and calls needing more are refused with CC_EARG (it holds, for example,
+ * 256 rows of 2^20 logits at M = 1, or 30 rows of 262144 at M = 256). Runs
+ * asynchronously on
+ * `stream` (a hipStream_t; NULL: the context's stream): the caller
+ * synchronises before reading `vals`/`ids`. Calls no hipMalloc, hipFree or
+ * allocating routine. Every call on one GPU shares that GPU's scratch, so
+ * calls that overlap on one GPU (different streams or contexts) race. */
+cc_status cc_topk_noalloc(cc_ctx* ctx, const float* logits, int32_t rows, int32_t V, int32_t M, float* vals,
+                          uint32_t* ids, void* stream);
 /* rmsnorm — web/model/kernels.js:1927-1932. */
 cc_status cc_op_rmsnorm(cc_ctx* ctx, const float* x, const float* w, int32_t T, int32_t H,
                         float* y);
