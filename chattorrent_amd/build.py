@@ -17,6 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libccdecode.so")
+PROBE = os.path.join(HERE, "libccprobe.so")
 ADDON_DIR = os.path.join(HERE, "node")
 ADDON = os.path.join(ADDON_DIR, "ccdecode.node")
 
@@ -51,6 +52,16 @@ def build_lib():
     return LIB
 
 
+def build_probe():
+    """The bandwidth probes the benchmark reports beside its roofline
+    (csrc/probe.hip): a library of their own, so the decode library carries
+    no measurement code."""
+    tmp = PROBE + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, os.path.join(CSRC, "probe.hip"), "-o", tmp])
+    os.replace(tmp, PROBE)
+    return PROBE
+
+
 def build_addon():
     """The N-API addon (node/ccdecode_napi.cc) linked against libccdecode.so.
     Needs the Node headers (/usr/include/node); skipped when they are absent."""
@@ -74,6 +85,7 @@ def build_oracle():
 
 def main():
     build_lib()
+    build_probe()
     if "--no-addon" not in sys.argv:
         build_addon()
     print(LIB)

@@ -28,6 +28,7 @@ EXPORTS = [
     "cc_slot_pages", "cc_free_pages", "cc_fill_random_kv", "cc_read_kv", "cc_write_kv", "cc_read_pages",
     "cc_stats_get", "cc_op_matmul_q8", "cc_op_store_kv", "cc_op_round_f16", "cc_op_topk", "cc_op_rmsnorm",
     "cc_op_attend", "cc_profile", "cc_profile_read", "cc_read_logits", "cc_mtp_draft", "cc_topk_noalloc",
+    "cc_decode_steps",
 ]
 
 
@@ -96,6 +97,7 @@ def load():
         "cc_op_attend": (i32, [P, i32, i32, P, i32, i32, P]),
         "cc_read_logits": (i32, [P, i32, P]),
         "cc_mtp_draft": (i32, [P, i32, i32, i32, i32, i32, P]),
+        "cc_decode_steps": (i32, [P, C.POINTER(Job), i32, i32, i32, P, P]),
         "cc_profile": (i32, [P, i32]),
         "cc_profile_read": (i32, [P, i32, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.POINTER(C.c_double)]),
     }
@@ -309,6 +311,22 @@ class Context:
             e.statuses = status
             raise e
         return hid
+
+    def decode_steps(self, slots, pasts, ids, steps, topk=1):
+        """cc_decode_steps: `steps` greedy passes on the device for one-row
+        jobs (slot, past, first id); returns (vals, ids) [steps, jobs, topk]."""
+        n = len(slots)
+        arr = (Job * n)()
+        keep = []
+        for i in range(n):
+            a = np.array([int(ids[i])], np.int32)
+            keep.append(a)
+            arr[i].slot, arr[i].past, arr[i].n, arr[i].sampled = int(slots[i]), int(pasts[i]), 1, 1
+            arr[i].ids = a.ctypes.data_as(C.POINTER(C.c_int32))
+        vals = np.empty((steps, n, topk), np.float32)
+        out = np.empty((steps, n, topk), np.uint32)
+        self._chk(self.lib.cc_decode_steps(self.h, arr, n, steps, topk, _p(vals), _p(out)))
+        return vals, out
 
     # --- kernel-level ops (parity tests) ---------------------------------------------
     def op_matmul_q8(self, X, W, scales_f16):

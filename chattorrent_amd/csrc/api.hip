@@ -123,6 +123,10 @@ struct cc_ctx {
     uint64_t* tk_b = nullptr;
     float* d_vals = nullptr;
     uint32_t* d_ids = nullptr;
+    // cc_decode_steps' per-step outputs, grown to the largest call
+    float* dec_vals = nullptr;
+    uint32_t* dec_ids = nullptr;
+    size_t dec_cap = 0;
     uint16_t* d_hbits = nullptr;
     // per-step metadata (device) and its pinned host staging
     uint8_t* d_meta = nullptr;
@@ -270,6 +274,8 @@ cc_status check_dims(cc_ctx* ctx, const cc_dims& d, const cc_opts& o) {
     if (o.lo < 0 || o.hi > positions || o.lo >= o.hi) return fail(ctx, CC_EARG, "bad position range");
     if (o.n_max <= 0 || o.t_max <= 0 || o.slots <= 0 || o.sessions <= 0 || o.max_jobs <= 0)
         return fail(ctx, CC_EARG, "n_max, t_max, slots, sessions and max_jobs must be positive");
+    if (o.max_jobs > PACK_MAX_JOBS)
+        return fail(ctx, CC_EARG, "max_jobs is at most " + std::to_string(PACK_MAX_JOBS));
     if (o.page_tokens != 64) return fail(ctx, CC_EARG, "page_tokens must be 64 (web/split.js:75)");
     if (o.t_max > 4096) return fail(ctx, CC_EARG, "t_max above 4096 rows is not supported");
     // attention chunks of ceil(pages/512) pages, at most 64 (one page index a lane)
@@ -286,10 +292,13 @@ struct StepPlan {
     double kv_bytes = 0;   // K and V rows one layer's attention reads (reference row size)
 };
 
-// Per-step metadata: jobs, items, row_job, plan, head_rows, combine
-// workgroups (job, kv head, m-tile), ids | hidden.
+// Per-step metadata. First what the host writes each pass (the page plan,
+// the jobs for the device packer, ids | hidden rows, the MTP fill's rows),
+// copied in one transfer; then what the device packer builds (jobs, items,
+// row_job, head_rows, combine workgroups (job, kv head, m-tile)).
 struct MetaLayout {
-    size_t jobs, items, row_job, plan, head_rows, cwg, ids, mtp_jobs, mtp_row_job, mtp_src, mtp_ids, hidden, total;
+    size_t plan, pack, ids, mtp_jobs, mtp_row_job, mtp_src, mtp_ids, hidden;
+    size_t jobs, items, row_job, head_rows, cwg, total;
 };
 
 // (job, kv head, m-tile) triples a pass can hold.
@@ -302,12 +311,8 @@ MetaLayout meta_layout(const cc_ctx* ctx) {
     MetaLayout m{};
     size_t at = 0;
     auto take = [&](size_t bytes) { size_t r = at; at += (bytes + 255) & ~(size_t)255; return r; };
-    m.jobs = take(sizeof(JobDev) * max_jobs);
-    m.items = take(sizeof(AttnItem) * ctx->items_cap);
-    m.row_job = take(4 * (size_t)t_max);
     m.plan = take(16 * (size_t)max_jobs);
-    m.head_rows = take(4 * (size_t)t_max);
-    m.cwg = take(12 * max_cwg_for(ctx));
+    m.pack = take(sizeof(PackJob) * max_jobs);
     m.ids = take(4 * (size_t)t_max);
     // the MTP fill's rows (the MTP jobs' rows, packed): jobs, row -> job,
     // hidden-row source (x row, or -1 - slot for the session's kept row), ids
@@ -316,6 +321,11 @@ MetaLayout meta_layout(const cc_ctx* ctx) {
     m.mtp_src = take(4 * (size_t)t_max);
     m.mtp_ids = take(4 * (size_t)t_max);
     m.hidden = take(2 * (size_t)t_max * H);
+    m.jobs = take(sizeof(JobDev) * max_jobs);
+    m.items = take(sizeof(AttnItem) * ctx->items_cap);
+    m.row_job = take(4 * (size_t)t_max);
+    m.head_rows = take(4 * (size_t)t_max);
+    m.cwg = take(12 * max_cwg_for(ctx));
     m.total = at;
     return m;
 }
@@ -988,18 +998,17 @@ cc_status cc_profile_read(const cc_ctx* ctx, int32_t kind, double* ms, int64_t* 
     return CC_OK;
 }
 
-// Build the step plan: rows packed in job order (stage.js:1319-1325), the Q
-// operand offsets, the attention work items, head rows.
-static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, bool head) {
+// The step plan (stage.js:1319-1325): the per-job table with rows packed in
+// job order, and the pass's counts (rows, sampled rows, attention work
+// items, combine triples, Q operand and partial sizes). Work item counts:
+// per (kv head, m-tile) one per chunk of ppw pages; k_pack writes the same
+// tables on the device, plan_tables on the host.
+static void plan_jobs(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, bool head) {
     p.jobs.resize(njobs);
     p.kv_bytes = 0;
-    p.items.clear();
-    p.row_job.clear();
-    p.head_rows.clear();
-    p.cwg.clear();
     const int ng = ctx->geom.ng;
-    size_t qp = 0, ap = 0;
-    int row = 0;
+    size_t qp = 0;
+    int row = 0, items = 0, cwg = 0, S = 0;
     for (int j = 0; j < njobs; j++) {
         JobDev& jd = p.jobs[j];
         jd.slot = jobs[j].slot;
@@ -1013,16 +1022,38 @@ static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, 
         qp += (size_t)ctx->geom.nKV * jd.mtq * ng * 128;
         const int T_act = jd.past + jd.n;
         p.kv_bytes += 2.0 * T_act * ctx->geom.nKV * (ctx->D + 4.0 * ctx->geom.ng);
-        // Work items: (kv head, m-tile, chunk of ppw pages), chunk fastest,
-        // so item0 + (kvh*mtq + mt)*nchunk + c.
-        jd.nchunk = ceil_div(ceil_div(T_act, 64), ctx->ppw);
-        jd.item0 = (int32_t)p.items.size();
+        jd.nchunk = ceil_div(ceil_div(T_act, ctx->geom.page), ctx->ppw);
+        jd.item0 = items;
+        items += ctx->geom.nKV * jd.mtq * jd.nchunk;
+        cwg += ctx->geom.nKV * jd.mtq;
+        if (head) S += jobs[j].sampled;
+        row += jd.n;
+    }
+    p.T = row;
+    p.S = S;
+    p.nitems = items;
+    p.ncwg = cwg;
+    p.qp_units = qp;
+    p.apart_floats = (size_t)items * 16 * (ctx->D + 4);
+}
+
+// The pass's tables on the host, for the passes that upload them (the MTP
+// draft chain, the kernel-level ops).
+static void plan_tables(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, bool head) {
+    p.items.clear();
+    p.row_job.clear();
+    p.head_rows.clear();
+    p.cwg.clear();
+    const int ng = ctx->geom.ng;
+    for (int j = 0; j < njobs; j++) {
+        const JobDev& jd = p.jobs[j];
         for (int h = 0; h < ctx->geom.nKV; h++)
             for (int mt = 0; mt < jd.mtq; mt++) {
                 const int32_t qb = jd.qp_off + ((h * jd.mtq + mt) * ng) * 128;
                 for (int c = 0; c < jd.nchunk; c++) {
-                    p.items.push_back(AttnItem{jd.slot, jd.past, jd.n, mt, qb, (int32_t)ap, h, c * ctx->ppw});
-                    ap += (size_t)16 * (ctx->D + 4);
+                    const int32_t idx = (int32_t)p.items.size();
+                    p.items.push_back(AttnItem{jd.slot, jd.past, jd.n, mt, qb, idx * 16 * (ctx->D + 4), h,
+                                               c * ctx->ppw});
                 }
                 p.cwg.push_back(j);
                 p.cwg.push_back(h);
@@ -1030,15 +1061,13 @@ static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, 
             }
         for (int i = 0; i < jd.n; i++) p.row_job.push_back(j);
         if (head)
-            for (int i = jd.n - jobs[j].sampled; i < jd.n; i++) p.head_rows.push_back(row + i);
-        row += jd.n;
+            for (int i = jd.n - jobs[j].sampled; i < jd.n; i++) p.head_rows.push_back(jd.row0 + i);
     }
-    p.T = row;
-    p.S = (int)p.head_rows.size();
-    p.nitems = (int)p.items.size();
-    p.ncwg = (int)p.cwg.size() / 3;
-    p.qp_units = qp;
-    p.apart_floats = ap;
+}
+
+static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, bool head) {
+    plan_jobs(ctx, jobs, njobs, p, head);
+    plan_tables(ctx, jobs, njobs, p, head);
 }
 
 static cc_status grow(cc_ctx* ctx, const StepPlan& p) {
@@ -1274,6 +1303,15 @@ static void prof_replay(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, in
     }
 }
 
+// k_pack over the PackJobs the pass uploaded, each past advanced by `step`.
+static void pack_on_device(cc_ctx* ctx, const MetaLayout& ml, int njobs, int step, bool head) {
+    PackGeom g{ctx->geom.nKV, ctx->group, ctx->geom.ng, ctx->D, ctx->ppw, ctx->geom.page, head ? 1 : 0};
+    uint8_t* dm = ctx->d_meta;
+    launch_pack(ctx->stream, (const PackJob*)(dm + ml.pack), njobs, step, g, (JobDev*)(dm + ml.jobs),
+                (AttnItem*)(dm + ml.items), (int32_t*)(dm + ml.row_job), (int32_t*)(dm + ml.head_rows),
+                (int32_t*)(dm + ml.cwg));
+}
+
 cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, int32_t to, int32_t topk,
                   float* top_vals, uint32_t* top_ids, uint16_t* hidden_out, int32_t* status) {
     if (!ctx) return CC_EARG;
@@ -1349,18 +1387,18 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
     if (T > ctx->o.t_max) return bad(-1, "the pass has " + std::to_string(T) + " rows, above t_max");
 
     StepPlan p;
-    build_plan(ctx, jobs, njobs, p, head);
+    plan_jobs(ctx, jobs, njobs, p, head);
     if (p.nitems > (int)ctx->items_cap || (size_t)p.ncwg > max_cwg_for(ctx))
         return bad(-1, "too many attention items");
     cc_status gs = grow(ctx, p);
     if (gs != CC_OK) return gs;
     MetaLayout ml = meta_layout(ctx);
     uint8_t* hm = ctx->h_meta;
-    std::memcpy(hm + ml.jobs, p.jobs.data(), p.jobs.size() * sizeof(JobDev));
-    std::memcpy(hm + ml.items, p.items.data(), p.items.size() * sizeof(AttnItem));
-    std::memcpy(hm + ml.row_job, p.row_job.data(), p.row_job.size() * 4);
-    std::memcpy(hm + ml.head_rows, p.head_rows.data(), p.head_rows.size() * 4);
-    std::memcpy(hm + ml.cwg, p.cwg.data(), p.cwg.size() * 4);
+    // the jobs for the device packer (k_pack builds the pass's tables)
+    PackJob* pk = (PackJob*)(hm + ml.pack);
+    for (int j = 0; j < njobs; j++)
+        pk[j] = PackJob{jobs[j].slot, jobs[j].past, jobs[j].n, head ? jobs[j].sampled : 0, p.jobs[j].snap,
+                        p.jobs[j].keep};
     std::vector<std::pair<int, int>> want;
     for (int j = 0; j < njobs; j++) want.push_back({jobs[j].slot, jobs[j].past + jobs[j].n});
     {
@@ -1420,6 +1458,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
     hipStream_t st = ctx->stream;
     HIPCHK(hipEventRecord(ctx->ev0, st));
     HIPCHK(hipMemcpyAsync(ctx->d_meta, hm, copy_bytes, hipMemcpyHostToDevice, st));
+    pack_on_device(ctx, ml, njobs, 0, head);
     cc_status ps = take_pages(ctx, want, (int32_t*)(ctx->d_meta + ml.plan), (int32_t*)(hm + ml.plan), status);
     if (ps != CC_OK) {
         hipStreamSynchronize(st);
@@ -1492,6 +1531,121 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
         std::memcpy(top_ids, (uint8_t*)hout + (size_t)p.S * topk * 4, (size_t)p.S * topk * 4);
     } else if (!at_end) {
         std::memcpy(hidden_out, hout, (size_t)T * d.hidden * 2);
+    }
+    return CC_OK;
+}
+
+cc_status cc_decode_steps(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t steps, int32_t topk,
+                          float* top_vals, uint32_t* top_ids) {
+    if (!ctx) return CC_EARG;
+    const cc_dims& d = ctx->d;
+    const int positions = d.n_layer + 2;
+    if (ctx->o.lo != 0 || ctx->o.hi != positions)
+        return fail(ctx, CC_EARG, "a decode loop needs every position (0.." + std::to_string(positions - 1) + ") here");
+    if (ctx->any_linear || ctx->mtp)
+        return fail(ctx, CC_EARG, "a decode loop runs full-attention models without an MTP head");
+    if (!jobs || njobs < 1 || njobs > ctx->o.max_jobs) return fail(ctx, CC_EARG, "1..max_jobs jobs per pass");
+    if (steps < 1) return fail(ctx, CC_EARG, "steps must be positive");
+    if (topk < 1 || topk > TOPK_MAX) return fail(ctx, CC_EARG, "topk must be 1..256");
+    if (!top_vals || !top_ids) return fail(ctx, CC_EARG, "a decode loop needs top_vals and top_ids");
+    if (njobs > ctx->o.t_max) return fail(ctx, CC_EARG, "the pass has more rows than t_max");
+    std::vector<char> seen(ctx->owned.size(), 0);
+    for (int j = 0; j < njobs; j++) {
+        const cc_job& jb = jobs[j];
+        if (jb.slot < 0 || jb.slot >= (int)ctx->owned.size()) return fail(ctx, CC_EARG, "slot out of range");
+        if (seen[jb.slot]) return fail(ctx, CC_EARG, "one job per session in a pass");
+        seen[jb.slot] = 1;
+        if (jb.n != 1 || jb.sampled != 1 || jb.snap || jb.rollback || jb.mtp)
+            return fail(ctx, CC_EARG, "a decode loop takes one-row jobs, each sampled");
+        if (!jb.ids || jb.ids[0] < 0 || jb.ids[0] >= d.vocab)
+            return fail(ctx, CC_EARG, "a job at position 0 needs 1 token ids");
+        if (jb.past < 0 || jb.past + steps > ctx->o.n_max)
+            return fail(ctx, CC_EARG, "context " + std::to_string(jb.past + steps) + " exceeds " +
+                                          std::to_string(ctx->o.n_max));
+    }
+    // plans of the first and the last step: the last needs the most items
+    std::vector<cc_job> last(jobs, jobs + njobs);
+    for (auto& j : last) j.past += steps - 1;
+    StepPlan pl;
+    plan_jobs(ctx, last.data(), njobs, pl, true);
+    if (pl.nitems > (int)ctx->items_cap || (size_t)pl.ncwg > max_cwg_for(ctx))
+        return fail(ctx, CC_EARG, "too many attention items");
+    cc_status gs = grow(ctx, pl);
+    if (gs != CC_OK) return gs;
+    const int S = njobs;
+    const size_t per = (size_t)S * topk;
+    if (per * steps > ctx->dec_cap) {
+        float* v = nullptr;
+        uint32_t* i = nullptr;
+        HIPCHK(dalloc(ctx, &v, per * steps * 4, &ctx->scratch_bytes));
+        HIPCHK(dalloc(ctx, &i, per * steps * 4, &ctx->scratch_bytes));
+        ctx->dec_vals = v;
+        ctx->dec_ids = i;
+        ctx->dec_cap = per * steps;
+    }
+    MetaLayout ml = meta_layout(ctx);
+    uint8_t* hm = ctx->h_meta;
+    PackJob* pk = (PackJob*)(hm + ml.pack);
+    int32_t* ids0 = (int32_t*)(hm + ml.ids);
+    std::vector<std::pair<int, int>> want;
+    int32_t* plan = (int32_t*)(hm + ml.plan);
+    int total = 0;
+    for (int j = 0; j < njobs; j++) {
+        pk[j] = PackJob{jobs[j].slot, jobs[j].past, 1, 1, 0, -1};
+        ids0[j] = jobs[j].ids[0];
+        want.push_back({jobs[j].slot, jobs[j].past + steps});
+        const int need = ceil_div(jobs[j].past + steps, ctx->geom.page);
+        const int nw = std::max(0, need - ctx->owned[jobs[j].slot]);
+        plan[4 * j] = jobs[j].slot;
+        plan[4 * j + 1] = ctx->owned[jobs[j].slot];
+        plan[4 * j + 2] = nw;
+        plan[4 * j + 3] = total;
+        total += nw;
+    }
+    hipStream_t st = ctx->stream;
+    HIPCHK(hipEventRecord(ctx->ev0, st));
+    HIPCHK(hipMemcpyAsync(ctx->d_meta, hm, ml.hidden, hipMemcpyHostToDevice, st));
+    cc_status ps = take_pages(ctx, want, (int32_t*)(ctx->d_meta + ml.plan), plan, nullptr);
+    if (ps != CC_OK) {
+        hipStreamSynchronize(st);
+        return ps;
+    }
+    const QTensor& hw = d.tied ? ctx->wte : ctx->lm_head;
+    QTensor emb = ctx->wte;
+    emb.K = d.hidden;
+    int32_t* d_ids_in = (int32_t*)(ctx->d_meta + ml.ids);
+    const int Mpad = 32 * ceil_div(S, 32);
+    std::vector<cc_job> cur(jobs, jobs + njobs);
+    for (int k = 0; k < steps; k++) {
+        // step k: every job one row further, fed the token step k-1 sampled
+        StepPlan p;
+        plan_jobs(ctx, cur.data(), njobs, p, true);
+        pack_on_device(ctx, ml, njobs, k, true);
+        if (k > 0) launch_ids_col0(st, ctx->dec_ids + (k - 1) * per, S, topk, d_ids_in);
+        launch_embed(st, d_ids_in, nullptr, p.T, emb, ctx->x);
+        run_blocks(ctx, p, ml, 0, d.n_layer);
+        launch_resid_norm(st, ctx->x, (const int32_t*)(ctx->d_meta + ml.head_rows), nullptr, 0, S, Mpad, d.hidden, 0,
+                          ctx->norm, d.rms_eps, hw.KU, ctx->xp_h, nullptr);
+        launch_gemm(st, hw, ctx->xp_h, ctx->mt_alloc, ctx->logits, S, ctx->ncu);
+        launch_topk(st, ctx->logits, hw.P, S, d.vocab, topk, ctx->tk_a, ctx->tk_b, ctx->dec_vals + k * per,
+                    ctx->dec_ids + k * per);
+        for (auto& j : cur) j.past++;
+    }
+    ctx->head_rows = S;
+    HIPCHK(hipMemcpyAsync(top_vals, ctx->dec_vals, per * steps * 4, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipMemcpyAsync(top_ids, ctx->dec_ids, per * steps * 4, hipMemcpyDeviceToHost, st));
+    HIPCHK(hipEventRecord(ctx->ev1, st));
+    HIPCHK(hipStreamSynchronize(st));
+    HIPCHK(take_launch_error());
+    float ms = 0;
+    hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1);
+    ctx->last_ms = ms;
+    ctx->passes += steps;
+    ctx->rows += (int64_t)steps * njobs;
+    ctx->last_T = njobs;
+    for (int j = 0; j < njobs; j++) {
+        ctx->fed[jobs[j].slot] = jobs[j].past + steps;
+        ctx->spec_n[jobs[j].slot] = -1;
     }
     return CC_OK;
 }
@@ -1718,7 +1872,7 @@ static cc_status one_job(cc_ctx* ctx, int32_t layer, int32_t slot, int32_t n, in
     int32_t* plan = (int32_t*)(hm + ml.plan);
     const int need = ceil_div(past + n, ctx->geom.page);
     plan[0] = slot; plan[1] = ctx->owned[slot]; plan[2] = std::max(0, need - ctx->owned[slot]); plan[3] = 0;
-    HIPCHK(hipMemcpyAsync(ctx->d_meta, hm, ml.ids, hipMemcpyHostToDevice, ctx->stream));
+    HIPCHK(hipMemcpyAsync(ctx->d_meta, hm, ml.total, hipMemcpyHostToDevice, ctx->stream));
     std::vector<std::pair<int, int>> want{{slot, past + n}};
     return take_pages(ctx, want, (int32_t*)(ctx->d_meta + ml.plan), plan, nullptr);
 }

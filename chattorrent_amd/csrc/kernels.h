@@ -53,6 +53,20 @@ struct AttnItem {
     int32_t kvh, p0;               // kv head, first page of the chunk
 };
 
+// A job as the host hands it to the device packer (k_pack): the pass's rows
+// are packed in job order from these alone.
+struct PackJob {
+    int32_t slot, past, n, sampled;
+    int32_t snap, keep;
+};
+// What the packer needs of the pass's geometry: kv heads, q heads per kv
+// head, Q operand groups per head (ng), head_dim, pages per attention work
+// item, and whether the pass reaches the head (its sampled rows).
+constexpr int PACK_MAX_JOBS = 1024;   // jobs one pass may pack
+struct PackGeom {
+    int nKV, group, ng, D, ppw, page, head;
+};
+
 struct KVGeom {
     int nKV, D, ng, page, blk;     // blk: bytes per (page, kv head) block
     int max_pages;
@@ -139,6 +153,14 @@ void launch_gather_rows(hipStream_t st, const float* x, const float* alt, const 
 void launch_topk(hipStream_t st, const float* logits, int planes, int rows, int V, int M, uint64_t* a,
                  uint64_t* b, float* vals, uint32_t* ids);
 void launch_round_f16(hipStream_t st, float* a, int64_t n);
+void launch_ids_col0(hipStream_t st, const uint32_t* ids, int rows, int stride, int32_t* out);
+// Runner.#pass's packing (web/model/stage.js:1319-1346) on the device: from
+// `njobs` PackJobs (each past advanced by `step`), the job table, the
+// attention work items (kv head, m-tile, chunk of ppw pages; chunk fastest),
+// row -> job, the sampled rows and the combine's (job, kv head, m-tile)
+// triples, in the order the host planner writes them.
+void launch_pack(hipStream_t st, const PackJob* in, int njobs, int step, const PackGeom& g, JobDev* jobs,
+                 AttnItem* items, int32_t* row_job, int32_t* head_rows, int32_t* cwg);
 // The keys launch_topk stages for (rows, V, M): a_keys for its first buffer,
 // b_keys for its second.
 void topk_stage_keys(int rows, int V, int M, size_t* a_keys, size_t* b_keys);

@@ -2054,6 +2054,101 @@ void launch_alloc_pages(hipStream_t st, const int32_t* plan, int njobs, const ui
     CHECK_LAUNCH();
 }
 
+// The next pass's ids from this pass's top-M output: column 0 (the greedy
+// token) of each sampled row.
+__global__ void k_ids_col0(const uint32_t* __restrict__ ids, int rows, int stride, int32_t* __restrict__ out) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < rows) out[r] = (int32_t)ids[(size_t)r * stride];
+}
+
+void launch_ids_col0(hipStream_t st, const uint32_t* ids, int rows, int stride, int32_t* out) {
+    if (rows <= 0) return;
+    hipLaunchKernelGGL(k_ids_col0, dim3((rows + 255) / 256), dim3(256), 0, st, ids, rows, stride, out);
+    CHECK_LAUNCH();
+}
+
+// ================================================================ packing ===
+// One workgroup: per-job counts in parallel, their prefix sums in job order
+// (one thread; a pass holds at most a few hundred jobs), then every table
+// written by all threads. A job of n rows at past p needs ceil(n*group/16)
+// Q m-tiles, ceil(ceil((p+n)/64)/ppw) chunks of pages per (kv head, m-tile),
+// one combine triple per (kv head, m-tile), and nKV*mtq*ng*128 Q-operand
+// units; each work item's softmax partial takes 16*(D+4) floats.
+constexpr int PACK_THREADS = 256;
+
+__global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict__ in, int njobs, int step,
+                                                       PackGeom g, JobDev* __restrict__ jobs,
+                                                       AttnItem* __restrict__ items, int32_t* __restrict__ row_job,
+                                                       int32_t* __restrict__ head_rows, int32_t* __restrict__ cwg) {
+    __shared__ int32_t s_row0[PACK_MAX_JOBS], s_item0[PACK_MAX_JOBS], s_cwg0[PACK_MAX_JOBS],
+        s_qp0[PACK_MAX_JOBS], s_head0[PACK_MAX_JOBS], s_mtq[PACK_MAX_JOBS], s_nch[PACK_MAX_JOBS];
+    for (int j = threadIdx.x; j < njobs; j += blockDim.x) {
+        const int n = in[j].n, tact = in[j].past + step + n;
+        s_mtq[j] = (n * g.group + 15) / 16;
+        s_nch[j] = ((tact + g.page - 1) / g.page + g.ppw - 1) / g.ppw;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int row = 0, item = 0, c = 0, qp = 0, head = 0;
+        for (int j = 0; j < njobs; j++) {
+            s_row0[j] = row;
+            s_item0[j] = item;
+            s_cwg0[j] = c;
+            s_qp0[j] = qp;
+            s_head0[j] = head;
+            row += in[j].n;
+            item += g.nKV * s_mtq[j] * s_nch[j];
+            c += g.nKV * s_mtq[j];
+            qp += g.nKV * s_mtq[j] * g.ng * 128;
+            head += g.head ? in[j].sampled : 0;
+        }
+    }
+    __syncthreads();
+    const int part = 16 * (g.D + 4);
+    for (int j = 0; j < njobs; j++) {
+        const PackJob pj = in[j];
+        const int past = pj.past + step, mtq = s_mtq[j], nch = s_nch[j];
+        if (threadIdx.x == 0) {
+            JobDev jd;
+            jd.slot = pj.slot;
+            jd.past = past;
+            jd.n = pj.n;
+            jd.row0 = s_row0[j];
+            jd.qp_off = s_qp0[j];
+            jd.mtq = mtq;
+            jd.item0 = s_item0[j];
+            jd.nchunk = nch;
+            jd.snap = pj.snap;
+            jd.keep = pj.keep;
+            jobs[j] = jd;
+        }
+        const int nit = g.nKV * mtq * nch;
+        for (int x = threadIdx.x; x < nit; x += blockDim.x) {
+            const int c = x % nch, hm = x / nch, mt = hm % mtq, h = hm / mtq;
+            const int idx = s_item0[j] + x;
+            items[idx] = AttnItem{pj.slot, past, pj.n, mt, s_qp0[j] + (hm * g.ng) * 128, idx * part, h, c * g.ppw};
+        }
+        for (int x = threadIdx.x; x < g.nKV * mtq; x += blockDim.x) {
+            const int at = 3 * (s_cwg0[j] + x);
+            cwg[at] = j;
+            cwg[at + 1] = x / mtq;
+            cwg[at + 2] = x % mtq;
+        }
+        for (int i = threadIdx.x; i < pj.n; i += blockDim.x) row_job[s_row0[j] + i] = j;
+        if (g.head)
+            for (int i = threadIdx.x; i < pj.sampled; i += blockDim.x)
+                head_rows[s_head0[j] + i] = s_row0[j] + pj.n - pj.sampled + i;
+    }
+}
+
+void launch_pack(hipStream_t st, const PackJob* in, int njobs, int step, const PackGeom& g, JobDev* jobs,
+                 AttnItem* items, int32_t* row_job, int32_t* head_rows, int32_t* cwg) {
+    if (njobs <= 0 || njobs > PACK_MAX_JOBS) return;
+    hipLaunchKernelGGL(k_pack, dim3(1), dim3(PACK_THREADS), 0, st, in, njobs, step, g, jobs, items, row_job,
+                       head_rows, cwg);
+    CHECK_LAUNCH();
+}
+
 // freePages (web/model/model.js:204-211): push the frame's pages back, last
 // owned first, so the next pop returns its first page.
 __global__ void k_release_pages(int slot, int owned, uint32_t* __restrict__ free_stack, int top,

@@ -182,6 +182,19 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
                   int32_t topk, float* top_vals, uint32_t* top_ids, uint16_t* hidden_out,
                   int32_t* status);
 
+/* `steps` greedy passes of Runner.#pass (web/model/stage.js:1314-1481) run
+ * back to back on the device, the route's closed decode loop
+ * (web/route.js:865-952) without a host round trip between passes: every
+ * job is one row, sampled; pass k runs each job at past + k with the token
+ * pass k-1 sampled (column 0 of its candidates; pass 0 takes jobs[j].ids[0]),
+ * and packs its rows and attention work on the device. The pages for
+ * past + steps tokens are taken first. Outputs: top_vals / top_ids
+ * [steps][njobs][topk], best first. Each pass's results equal cc_step's for
+ * the same jobs. A context holding every position of a full-attention model
+ * without an MTP head. */
+cc_status cc_decode_steps(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t steps, int32_t topk,
+                          float* top_vals, uint32_t* top_ids);
+
 /* After sampling `token` from row `row` of the last pass (Runner.#mtpAfter,
  * web/model/stage.js:296-320): the session keeps that row's hidden state
  * (row -1: keep the one it has) and, for k_drafts > 0 (at most 7), the MTP

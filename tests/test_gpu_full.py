@@ -328,3 +328,32 @@ def test_config2_128_steps_batch_invariant_and_deterministic(model27b):
     assert np.array_equal(a_last.view(np.uint32), b_last.view(np.uint32))
     _report("configs[2] 128 steps", {"steps": steps, "alone_chats": alone, "distinct_ids_per_chat":
                                      float(np.mean([len(set(a_ids[:, s])) for s in range(CHATS)]))})
+
+
+def test_config2_decode_loop_equals_stepwise(model27b):
+    """The device decode loop (cc_decode_steps: 8 passes back to back, rows
+    packed on the device, each pass fed the previous pass's token) at the
+    metric's workload gives the ids and top logit bits of 8 cc_step calls."""
+    d, c, pasts, ids0 = model27b
+    steps = 8
+
+    def fill():
+        for s, T in enumerate(pasts):
+            c.fill_random_kv(s, int(T), SEED27, s + 1)
+
+    fill()
+    vals, ids = c.decode_steps(list(range(CHATS)), [int(T) for T in pasts], [int(x) for x in ids0], steps, topk=2)
+    for s in range(CHATS):
+        c.release(s)
+    fill()
+    toks = [int(x) for x in ids0]
+    try:
+        for k in range(steps):
+            v, i = c.step([dict(slot=s, past=int(T) + k, n=1, ids=[toks[s]], sampled=1) for s, T in enumerate(pasts)],
+                          topk=2)
+            assert np.array_equal(i, ids[k]), k
+            assert np.array_equal(v.view(np.uint32), vals[k].view(np.uint32)), k
+            toks = [int(x) for x in i[:, 0]]
+    finally:
+        for s in range(CHATS):
+            c.release(s)

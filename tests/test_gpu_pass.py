@@ -312,3 +312,22 @@ def test_error_classes(gpu):
         assert e.value.status == CC_EARG
     finally:
         c.close()
+
+
+def test_decode_steps_equal_step_by_step(smol):
+    """cc_decode_steps (K greedy passes back to back on the device, each
+    pass's rows packed by k_pack and fed the previous pass's token) gives, pass
+    for pass, the ids and candidate bits of K cc_step calls fed the same way."""
+    d, c, om = smol
+    # past every context the module's other tests wrote, so both runs read the same rows
+    slots, pasts = [0, 1, 2, 3], [600, 601, 602, 603]
+    first = [int(x) for x in _ids(4, d["vocab"], 90)]
+    steps = 6
+    vals, ids = c.decode_steps(slots, pasts, first, steps, topk=3)
+    toks = first
+    for k in range(steps):
+        v, i = c.step([dict(slot=s, past=p + k, n=1, ids=[toks[j]], sampled=1) for j, (s, p) in
+                       enumerate(zip(slots, pasts))], topk=3)
+        assert np.array_equal(i, ids[k]), k
+        assert np.array_equal(v.view(np.uint32), vals[k].view(np.uint32)), k
+        toks = [int(x) for x in i[:, 0]]
