@@ -423,60 +423,26 @@ def bench_c5(args, ceil):
     n_max = 4096 + 512 + 64
     ctx = Context(d, n_max=n_max, t_max=t_max, slots=slots, sessions=slots, max_jobs=slots)
     ctx.fill_random(args.seed)
-    rng = np.random.default_rng(args.seed + 5)
-    chats = {}
-    stats = {"prefill": 0, "decode": 0, "arrived": 0, "retired": 0, "rows": 0}
+    churn = configs.Churn(d["vocab"], slots, chunk, t_max, args.seed + 5)
 
     def one_step():
-        for _ in range(rng.poisson(2.0)):
-            free = [f for f in range(slots) if f not in chats]
-            if not free:
-                break
-            chats[free[0]] = {"prompt": int(np.exp(rng.uniform(np.log(32), np.log(4096)))), "fed": 0, "gen": 0,
-                              "stop": int(rng.integers(64, 513)), "last": 1}
-            stats["arrived"] += 1
-        jobs, rows, chunks = [], 0, 0
-        for f in sorted(chats):                       # every decode row
-            ch = chats[f]
-            if ch["fed"] >= ch["prompt"]:
-                jobs.append(dict(slot=f, past=ch["fed"], n=1, ids=[ch["last"]], sampled=1))
-                rows += 1
-        for f in sorted(chats):                       # then up to two prompt chunks
-            ch = chats[f]
-            if ch["fed"] < ch["prompt"] and chunks < 2 and rows + chunk <= t_max:
-                n = min(chunk, ch["prompt"] - ch["fed"])
-                jobs.append(dict(slot=f, past=ch["fed"], n=n, ids=[(ch["fed"] + i) % d["vocab"] for i in range(n)],
-                                 sampled=1 if ch["fed"] + n == ch["prompt"] else 0))
-                rows += n
-                chunks += 1
+        jobs = churn.jobs()
         if not jobs:
             return
-        jobs.sort(key=lambda j: j["slot"])
         _, ids = ctx.step(jobs, topk=1)
-        at = 0
-        for j in jobs:
-            ch = chats[j["slot"]]
-            stats["decode" if ch["fed"] >= ch["prompt"] else "prefill"] += j["n"]
-            ch["fed"] += j["n"]
-            if j["sampled"]:
-                ch["last"] = int(ids[at, 0]) % d["vocab"]
-                ch["gen"] += 1
-                at += 1
-        stats["rows"] += rows
-        for f in [f for f, ch in chats.items() if ch["gen"] >= ch["stop"]]:
+        for f in churn.advance(jobs, ids[:, 0]):
             ctx.release(f)
-            del chats[f]
-            stats["retired"] += 1
 
     for _ in range(args.warmup):
         one_step()
+    stats = churn.stats
     for k in stats:
         stats[k] = 0
     t0 = time.perf_counter()
     for k in range(args.steps):
         one_step()
         if k % 50 == 49:
-            log(f"c5: {k + 1} steps, {len(chats)} chats")
+            log(f"c5: {k + 1} steps, {len(churn.chats)} chats")
     secs = time.perf_counter() - t0
     ctx.close()
     ms = secs * 1000.0 / args.steps

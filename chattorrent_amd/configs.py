@@ -61,3 +61,74 @@ def workload_contexts(n, lo, hi, seed):
     import numpy as np
     rng = np.random.default_rng(seed)
     return np.round(np.exp(rng.uniform(math.log(lo), math.log(hi), n))).astype(int)
+
+
+class Churn:
+    """configs[4]'s continuous-batching workload, one pass at a time: `slots`
+    chat frames, Poisson(`rate`) arrivals a pass, prompts log-uniform in
+    [32, 4096] ids fed as `chunk`-token chunks beside the decode rows (at most
+    two chunks a pass, rows <= t_max), chats retiring after U[64, 512]
+    generated tokens. Seeded: the same seed gives the same jobs for the same
+    sampled ids.
+
+        ch = Churn(vocab, slots=64, chunk=512, t_max=1088, seed=1239)
+        jobs = ch.jobs()                # this pass's jobs, in slot order
+        done = ch.advance(jobs, ids)    # feed the sampled ids; frames retired
+    """
+
+    def __init__(self, vocab, slots, chunk, t_max, seed, rate=2.0, prompt=(32, 4096), stop=(64, 512)):
+        import numpy as np
+        self.vocab, self.slots, self.chunk, self.t_max = vocab, slots, chunk, t_max
+        self.rate, self.prompt, self.stop = rate, prompt, stop
+        self.rng = np.random.default_rng(seed)
+        self.chats = {}   # frame -> {"prompt", "fed", "gen", "stop", "last"}
+        self.stats = {"prefill": 0, "decode": 0, "arrived": 0, "retired": 0, "rows": 0}
+
+    def jobs(self):
+        import math
+        rng = self.rng
+        for _ in range(rng.poisson(self.rate)):
+            free = [f for f in range(self.slots) if f not in self.chats]
+            if not free:
+                break
+            lo, hi = self.prompt
+            self.chats[free[0]] = {"prompt": int(math.exp(rng.uniform(math.log(lo), math.log(hi)))), "fed": 0,
+                                   "gen": 0, "stop": int(rng.integers(self.stop[0], self.stop[1] + 1)), "last": 1}
+            self.stats["arrived"] += 1
+        jobs, rows, chunks = [], 0, 0
+        for f in sorted(self.chats):                  # every decode row
+            ch = self.chats[f]
+            if ch["fed"] >= ch["prompt"]:
+                jobs.append(dict(slot=f, past=ch["fed"], n=1, ids=[ch["last"]], sampled=1))
+                rows += 1
+        for f in sorted(self.chats):                  # then up to two prompt chunks
+            ch = self.chats[f]
+            if ch["fed"] < ch["prompt"] and chunks < 2 and rows + self.chunk <= self.t_max:
+                n = min(self.chunk, ch["prompt"] - ch["fed"])
+                jobs.append(dict(slot=f, past=ch["fed"], n=n,
+                                 ids=[(ch["fed"] + i) % self.vocab for i in range(n)],
+                                 sampled=1 if ch["fed"] + n == ch["prompt"] else 0))
+                rows += n
+                chunks += 1
+        jobs.sort(key=lambda j: j["slot"])
+        return jobs
+
+    def advance(self, jobs, ids):
+        """Feeds the pass's sampled ids (one per sampled job, in job order)
+        back; returns the frames whose chats retired (the caller releases
+        them)."""
+        at = 0
+        for j in jobs:
+            ch = self.chats[j["slot"]]
+            self.stats["decode" if ch["fed"] >= ch["prompt"] else "prefill"] += j["n"]
+            self.stats["rows"] += j["n"]
+            ch["fed"] += j["n"]
+            if j["sampled"]:
+                ch["last"] = int(ids[at]) % self.vocab
+                ch["gen"] += 1
+                at += 1
+        done = [f for f, ch in self.chats.items() if ch["gen"] >= ch["stop"]]
+        for f in done:
+            del self.chats[f]
+            self.stats["retired"] += 1
+        return done

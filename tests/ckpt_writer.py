@@ -40,13 +40,17 @@ def pack_file(path, filename, tensors):
     return entries
 
 
-def q8(rng, N, K, group):
+def q8(rng, N, K, group, f32_scales=False):
+    """Codes and scales drawn directly. By default the scales are f16 values;
+    with f32_scales they are what the converter writes (amax / 127 in f32,
+    tools/convert_hf.py:493), which f16 does not hold exactly."""
     codes = rng.integers(-127, 128, (N, K)).astype(np.int8)
-    scales = f16_exact(rng.uniform(1e-4, 4e-4, (N, -(-K // group))))
+    amax = rng.uniform(127e-4, 508e-4, (N, -(-K // group)))
+    scales = (amax.astype(np.float32) / np.float32(127)) if f32_scales else f16_exact(amax / 127)
     return codes, scales, group
 
 
-def make(path, d, seed=11, group=64):
+def make(path, d, seed=11, group=64, f32_scales=False):
     """A q8 checkpoint of dims `d` (this build's key names) at `path`.
     Returns {filename: {name: tensor}} with what was written."""
     os.makedirs(path, exist_ok=True)
@@ -68,15 +72,15 @@ def make(path, d, seed=11, group=64):
             if name.endswith("layernorm"):
                 ts.append((name, f16_exact(rng.uniform(0.5, 1.5, H))))
             else:
-                ts.append((name, q8(rng, *shapes[name], group)))
+                ts.append((name, q8(rng, *shapes[name], group, f32_scales)))
         fn = f"block_{i:02d}.bin"
         manifest["files"][fn] = pack_file(path, fn, ts)
         written[fn] = dict(ts)
-    client = [("wte", q8(rng, V, H, group)), ("norm", f16_exact(rng.uniform(0.5, 1.5, H)))]
+    client = [("wte", q8(rng, V, H, group, f32_scales)), ("norm", f16_exact(rng.uniform(0.5, 1.5, H)))]
     manifest["files"]["client.bin"] = pack_file(path, "client.bin", client)
     written["client.bin"] = dict(client)
     if not d.get("tied", True):
-        head = [("lm_head", q8(rng, V, H, group))]
+        head = [("lm_head", q8(rng, V, H, group, f32_scales))]
         manifest["files"]["lm_head.bin"] = pack_file(path, "lm_head.bin", head)
         written["lm_head.bin"] = dict(head)
     with open(os.path.join(path, "manifest.json"), "w") as f:

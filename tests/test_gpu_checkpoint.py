@@ -83,6 +83,78 @@ def test_checkpoint_pass_matches_oracle(gpu, tmp_path, tied):
         c.close()
 
 
+def _rounded(written):
+    """The checkpoint's tensors with every q8 scale rounded to f16, the
+    device's scale format (what cc_upload keeps of an f32 scale)."""
+    return {fn: {n: ((t[0], W.f16_exact(t[1]), t[2]) if isinstance(t, tuple) else t) for n, t in ts.items()}
+            for fn, ts in written.items()}
+
+
+def test_checkpoint_f32_scales_against_oracle_at_f32(gpu, tmp_path):
+    """A checkpoint whose q8 scales are the converter's f32 values (amax/127,
+    not f16 values), configs[0]'s model (SmolLM2 shape, all 30 layers, tied
+    head), 4 chats x 8 greedy passes. The device keeps each scale as f16
+    (relative change <= 2^-11). Each pass is checked twice:
+    * against the oracle holding the device's f16-rounded scales, to the usual
+      bar (logits within 1e-2, greedy ids equal above a 1e-3 margin): the
+      kernels are exact up to f32 summation order;
+    * against the oracle at the checkpoint's own f32 scales (the reference's
+      arithmetic, web/model/kernels.js:116-126 keeps them f32): the logit
+      error and the greedy agreement are reported, the error must stay within
+      the two oracles' own distance plus 1e-2, and the ids must agree on every
+      row whose f32 margin exceeds twice that error.
+    Every pass feeds the device's sampled ids to all three."""
+    from chattorrent_amd.ccdecode import Context
+    from oracle import model as Mo
+    d = dict(configs.SMOLLM2)
+    written = W.make(str(tmp_path), d, group=64, f32_scales=True)
+    scales = np.concatenate([t[1].ravel() for ts in written.values() for t in ts.values() if isinstance(t, tuple)])
+    moved = float(np.abs(W.f16_exact(scales) / scales - 1).max())
+    assert 0 < moved <= 2.0 ** -11, moved
+    ctxs = [17, 130, 511, 1024]
+    n_max = 1024 + 64
+    c = Context(d, n_max=n_max, t_max=8, slots=4)
+    om32 = Mo.Model(d, n_slots=4, max_pages=-(-n_max // 64))
+    om16 = Mo.Model(d, n_slots=4, max_pages=-(-n_max // 64))
+    rec = {"passes": 8, "rows": 0, "ids_equal_f32": 0, "max_err_vs_f32": 0.0, "max_f32_vs_f16_oracles": 0.0,
+           "max_err_vs_f16": 0.0, "min_margin_f32": 1e9, "scale_max_rel_change": moved}
+    try:
+        C.upload(c, str(tmp_path))
+        _oracle_weights(om32, written, d)
+        _oracle_weights(om16, _rounded(written), d)
+        for s, T in enumerate(ctxs):
+            for x in (c, om32, om16):
+                x.fill_random_kv(s, T, SEED, s + 1)
+        toks = [int(_ids(1, d["vocab"], 720 + s)[0]) for s in range(4)]
+        for k in range(rec["passes"]):
+            jobs = [dict(slot=s, past=T + k, n=1, ids=[toks[s]], sampled=1, topk=2) for s, T in enumerate(ctxs)]
+            vals, ids = c.step(jobs, topk=2)
+            got = c.read_logits(len(jobs))
+            w16 = np.concatenate([w["logits"] for w in om16.pass_(jobs)])
+            w32 = np.concatenate([w["logits"] for w in om32.pass_(jobs)])
+            _check_head(d, vals, ids, [{"logits": w16[r:r + 1]} for r in range(len(jobs))], ctx=c)
+            e32 = float(np.abs(got - w32).max())
+            gap = float(np.abs(w32 - w16).max())
+            assert e32 <= gap + 1e-2, (k, e32, gap)
+            for r in range(len(jobs)):
+                order = np.argsort(-w32[r], kind="stable")
+                margin = float(w32[r, order[0]] - w32[r, order[1]])
+                rec["min_margin_f32"] = min(rec["min_margin_f32"], margin)
+                rec["ids_equal_f32"] += int(ids[r, 0] == order[0])
+                if margin > 2 * e32:
+                    assert ids[r, 0] == order[0], (k, r, margin, e32)
+            rec["rows"] += len(jobs)
+            rec["max_err_vs_f32"] = max(rec["max_err_vs_f32"], e32)
+            rec["max_f32_vs_f16_oracles"] = max(rec["max_f32_vs_f16_oracles"], gap)
+            rec["max_err_vs_f16"] = max(rec["max_err_vs_f16"], float(np.abs(got - w16).max()))
+            toks = [int(i) for i in ids[:, 0]]
+    finally:
+        c.close()
+    import json
+    import warnings
+    warnings.warn("checkpoint f32 scales: " + json.dumps(rec))
+
+
 def test_checkpoint_split_over_two_contexts(gpu, tmp_path):
     """Two peers over one checkpoint (positions [0, 2) and [2, 4) of a
     2-block model): each uploads only its own files' tensors, and the f16

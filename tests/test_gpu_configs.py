@@ -218,3 +218,50 @@ def test_churn_pages_and_tokens_over_passes(gpu):
         assert arrived >= 6 and retired >= 3, (arrived, retired)
     finally:
         c.close()
+
+
+def test_config4_churn_at_scale_pages_every_pass(gpu):
+    """configs[4]'s churn at its own scale: the 8B shape (32 layers, untied
+    head, llama3 RoPE scaling), 64 chat frames over one shared pool, Poisson(2)
+    arrivals a pass, prompts log-uniform in [32, 4096] fed as 512-token chunks
+    beside the decode rows, retirement after U[64, 512] tokens, 220 passes
+    (chattorrent_amd.configs.Churn, the bench's c5 workload). After every pass
+    each frame's device page table equals the oracle's replay of ensurePages /
+    freePages (web/model/model.js:185-211) over the same jobs, page for page,
+    and the free count agrees; every sampled id is a vocabulary id."""
+    from chattorrent_amd.ccdecode import Context
+    from oracle import model as Mo
+    d = dict(configs.LLAMA8B)
+    slots, chunk, t_max = 64, 512, 64 + 2 * 512
+    n_max = 4096 + 512 + 64
+    max_pages = -(-n_max // 64)
+    c = Context(d, n_max=n_max, t_max=t_max, slots=slots, sessions=slots, max_jobs=slots)
+    pool = Mo.PagePool(slots * max_pages)
+    frames = [{"pages": np.zeros(max_pages, np.uint32), "owned": [], "max_pages": max_pages} for _ in range(slots)]
+    churn = configs.Churn(d["vocab"], slots, chunk, t_max, SEED + 5)
+    passes = rows = most = 0
+    try:
+        c.fill_random(SEED)
+        for step in range(220):
+            jobs = churn.jobs()
+            if not jobs:
+                continue
+            for j in jobs:
+                assert pool.ensure(frames[j["slot"]], j["past"] + j["n"]), step
+            _, ids = c.step(jobs, topk=1)
+            assert ids.shape[0] == sum(j["sampled"] for j in jobs)
+            assert (ids[:, 0] < d["vocab"]).all(), step
+            passes += 1
+            rows += sum(j["n"] for j in jobs)
+            most = max(most, len(jobs))
+            for f in churn.advance(jobs, ids[:, 0]):
+                c.release(f)
+                pool.release(frames[f])
+            for f in range(slots):
+                assert list(c.pages(f)) == frames[f]["owned"], (step, f)
+            assert c.free_pages() == len(pool.free), step
+        st = churn.stats
+        assert passes >= 200 and st["arrived"] >= 64 and st["retired"] >= 10 and st["prefill"] > 0, st
+        print(f"churn at scale: {passes} passes, {rows} rows, up to {most} jobs a pass, {st}")
+    finally:
+        c.close()

@@ -232,6 +232,44 @@ def test_hybrid_long_jobs_take_the_row_parallel_conv_bitwise(gpu):
         assert np.array_equal(g.view(np.uint32), got[0].view(np.uint32))
 
 
+def test_hybrid_verify_beside_row_parallel_conv_then_rollback(gpu):
+    """A 4-row verify (snap) packed beside another session's 30-row prompt
+    chunk, so the pass runs the row-parallel conv (rows > 16), then a
+    rollback to keep 2 with the next token beside that session's decode.
+    The verifying session's logits equal, bit for bit, the same passes with
+    the other session's chunk cut to 3 rows (the one-thread-per-channel
+    conv, and the <= 32-row matmul), and every pass matches the oracle."""
+    d = HW.SPIKE
+    V = d["vocab"]
+    rng = np.random.default_rng(43)
+    p0, p1 = _ids(rng, 10, V), _ids(rng, 40, V)
+    ver, x, y = _ids(rng, 4, V), _ids(rng, 1, V), _ids(rng, 1, V)
+    runs = []
+    for long_n in (30, 3):
+        c, om = _pair(d)
+        try:
+            passes = [
+                [dict(slot=0, past=0, n=10, ids=p0, sampled=1, topk=4),
+                 dict(slot=1, past=0, n=5, ids=p1[:5], sampled=1, topk=4)],
+                [dict(slot=0, past=10, n=4, ids=ver, sampled=4, topk=4, snap=True),
+                 dict(slot=1, past=5, n=long_n, ids=p1[5:5 + long_n], sampled=1, topk=4)],
+                [dict(slot=0, past=12, n=1, ids=x, sampled=1, topk=4, keep=2),
+                 dict(slot=1, past=5 + long_n, n=1, ids=y, sampled=1, topk=4)],
+                [dict(slot=0, past=13, n=1, ids=y, sampled=1, topk=4)],
+            ]
+            mine = []
+            for jobs in passes:
+                vals, ids = c.step(jobs, topk=4)
+                logits = _check(vals, ids, om.pass_(jobs), c)
+                rows = jobs[0]["sampled"]
+                mine.append(c.read_logits(logits.shape[0])[:rows].copy())
+            runs.append(mine)
+        finally:
+            c.close()
+    for a, b in zip(*runs):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 def test_hybrid_long_rollback_job_matches_oracle(gpu):
     """A 40-row prefill beside a short one, a verify on the short session,
     then a 20-row job that rolls it back (keep 1) beside a decode: the long
