@@ -465,6 +465,29 @@ def bench_c5(args, ceil):
     return line
 
 
+def js_sample(d, lens, prompts, seed, steps=3):
+    """The "JS path" analogue: the single-threaded JavaScript restatement of
+    the pass (oracle/js/decode.js) on configs[0]'s model, decoding `steps`
+    greedy passes of the 4 chats at contexts `lens` over generated K/V rows
+    (the same shapes as after the prefill). None when node is absent."""
+    import shutil
+    import tempfile
+    from oracle import jsdecode as J
+    if J.node_binary() is None:
+        return None
+    path = tempfile.mkdtemp(prefix="ccjs-")
+    try:
+        t0 = time.perf_counter()
+        J.write_inputs(path, d, seed, lens, [int(p[-1]) for p in prompts], steps)
+        log(f"c1: JS inputs written in {time.perf_counter() - t0:.1f} s; running {steps} single-thread JS passes")
+        r = J.run(path, steps)
+    finally:
+        shutil.rmtree(path, ignore_errors=True)
+    return {"value": round(4 / (r["ms_per_step"] / 1000.0), 3), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"oracle/js/decode.js (Node, one thread): {steps} greedy passes of the 4 chats at contexts "
+                      f"{list(lens)} ({r['ms_per_step']:.0f} ms/pass)"}
+
+
 # ------------------------------------------------------------------ c1 ---
 def bench_c1(args, ceil):
     """the SmolLM2-shaped model (30 layers), 4 chats whose prompts
@@ -512,6 +535,7 @@ def bench_c1(args, ceil):
         cpu = cpu_line(round(4 / (ms_cpu / 1000.0), 3), "tok/s",
                        f"oracle (C restatement, OpenMP): all 32 decode steps of the 4 chats after its own prefill "
                        f"({ms_cpu:.1f} ms/step)")
+        cpu["js_single_thread"] = js_sample(d, lens, prompts, args.seed)
     line = base_line(args, "aggregate decode tok/s @4 ragged chats, SmolLM2-135M-shaped q8", 4 / (ms / 1000.0),
                      "tok/s", ms)
     line["steps"] = steps
