@@ -444,6 +444,7 @@ def bench_c5(args, ceil):
         if k % 50 == 49:
             log(f"c5: {k + 1} steps, {len(churn.chats)} chats")
     secs = time.perf_counter() - t0
+    prof = profiled(ctx, one_step, args.prof_steps)
     ctx.close()
     ms = secs * 1000.0 / args.steps
     params = configs.weight_bytes(d) / (1 + 2 / 32)
@@ -455,7 +456,8 @@ def bench_c5(args, ceil):
                       "decode_tok_s": round(stats["decode"] / secs, 2),
                       "prefill_tok_s": round(stats["prefill"] / secs, 2),
                       "rows_per_step": round(stats["rows"] / args.steps, 1), "arrived": stats["arrived"],
-                      "retired": stats["retired"]}
+                      "retired": stats["retired"],
+                      "per_kind_ms_per_step": {k: round(v[0] / args.prof_steps, 4) for k, v in prof.items()}}
     line["roofline"] = {"bound": "mfma", "achieved": round(tflops, 1), "peak": F16_MFMA_PEAK_TFLOPS,
                         "unit": "TFLOP/s", "frac": round(tflops / F16_MFMA_PEAK_TFLOPS, 4), "traffic": None,
                         "note": "algorithmic FLOPs 2 x rows x params per pass; the matmul issues each product twice "

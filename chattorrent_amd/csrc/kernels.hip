@@ -318,12 +318,20 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm(const uint8_t* __rest
     __shared__ u32x4 xs[2][MTL * 4][64];   // two units: block (m-tile, q = 2h + hl) of 1 KiB
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int r = blockIdx.x % P, pb = blockIdx.x / P;
     const int npairs = Nt / NT;
+    // Workgroup b runs on XCD b % 8 (dispatch is round-robin over the XCDs).
+    // Each (plane, pair group) goes to one XCD, which runs its row blocks back
+    // to back, so the row blocks after the first read its weight records from
+    // that XCD's L2 instead of HBM. The order of workgroups changes no sums.
+    const int nrb = (M + 16 * MTL - 1) / (16 * MTL), npg = (npairs + TM_PAIRS - 1) / TM_PAIRS;
+    const int kx = blockIdx.x / 8;
+    const int gx = (kx / nrb) * 8 + blockIdx.x % 8, gy = kx % nrb;
+    if (gx >= P * npg) return;   // the grid is rounded up to whole XCD rounds
+    const int r = gx % P, pb = gx / P;
     const int pair = pb * TM_PAIRS + wave % TM_PAIRS, mw = (wave / TM_PAIRS) * MTW;   // m-tiles mw .. mw+MTW-1
     const bool has = pair < npairs;
     const int ua = lx_plane_start(r, KU, P), len = lx_plane_start(r + 1, KU, P) - ua;
-    const int mt0 = blockIdx.y * MTL;
+    const int mt0 = gy * MTL;
     const int G2 = 2 * KU;
     const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)Wr, 0, 0x7fffffff, 0x00020000);
     // activation m-tiles past the operand's allocation read zero
@@ -479,7 +487,8 @@ void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtile
         // the same planes and cut points as k_gemm_lx (lx_groups)
         const int Gm = lx_groups(w, ncu) / w.P;
         const int npairs = w.Nt / 2;
-        dim3 grid(w.P * ((npairs + TM_PAIRS - 1) / TM_PAIRS), (M + 16 * TM_MT - 1) / (16 * TM_MT));
+        const int units = w.P * ((npairs + TM_PAIRS - 1) / TM_PAIRS), nrb = (M + 16 * TM_MT - 1) / (16 * TM_MT);
+        dim3 grid(8 * ((units + 7) / 8) * nrb);
         hipLaunchKernelGGL(k_gemm_tm, grid, dim3(64 * TM_WAVES), 0, st, (const uint8_t*)w.codes, Xp, xp_mtiles, out,
                            w.KU, M, w.N, w.Nt, w.P, Gm);
     }
