@@ -963,7 +963,8 @@ cc_status cc_read_logits(cc_ctx* ctx, int32_t rows, float* out) {
     const size_t n = (size_t)rows * ctx->d.vocab;
     std::vector<float> plane(n);
     HIPCHK(hipMemcpy(out, ctx->logits, n * 4, hipMemcpyDeviceToHost));
-    for (int q = 1; q < ctx->head_planes; q++) {
+    const int planes = gemm_planes(ctx->d.tied ? ctx->wte : ctx->lm_head, rows, ctx->ncu);
+    for (int q = 1; q < planes; q++) {
         HIPCHK(hipMemcpy(plane.data(), ctx->logits + q * n, n * 4, hipMemcpyDeviceToHost));
         for (size_t i = 0; i < n; i++) out[i] = out[i] + plane[i];
     }
@@ -1129,14 +1130,14 @@ static void full_attn_half(cc_ctx* ctx, Layer& L, float* x, int T, int Mpad, con
         ex.gate = ctx->gbuf;
     }
     launch_gemm(st, L.qkv, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-    launch_fin_qkv(st, ctx->part, L.qkv.P, T, pm.row_job, pm.jobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
+    launch_fin_qkv(st, ctx->part, gemm_planes(L.qkv, T, ctx->ncu), T, pm.row_job, pm.jobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
                    L.kpool, L.vpool, ctx->page_table, ctx->qp, rs, 1, 1, ex);
     launch_attn(st, pm.items, pm.nitems, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
                 ctx->ppw, ctx->apart);
     launch_attn_combine(st, pm.jobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU, ctx->xp_o, nullptr, pm.cwg,
                         pm.ncwg, ctx->hybrid ? ctx->gbuf : nullptr);
     launch_gemm(st, L.o, ctx->xp_o, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-    launch_resid_w(st, x, ctx->part, L.o.P, T, Mpad, H, 0, L.ln2, ceil_div(H, 64), ctx->xp_h, ctx->ssp);
+    launch_resid_w(st, x, ctx->part, gemm_planes(L.o, T, ctx->ncu), T, Mpad, H, 0, L.ln2, ceil_div(H, 64), ctx->xp_h, ctx->ssp);
 }
 
 // The SwiGLU MLP (model.js:307-315) from the operand x*ln2: gate|up GEMM,
@@ -1148,9 +1149,9 @@ static void ffn_half(cc_ctx* ctx, Layer& L, float* x, int T, int Mpad, int round
     const int H = d.hidden;
     const RowScale rs = row_scale_of(ctx);
     launch_gemm(st, L.gu, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-    launch_fin_swiglu(st, ctx->part, L.gu.P, T, Mpad, d.ffn, L.down.KU, ctx->xp_f, rs);
+    launch_fin_swiglu(st, ctx->part, gemm_planes(L.gu, T, ctx->ncu), T, Mpad, d.ffn, L.down.KU, ctx->xp_f, rs);
     launch_gemm(st, L.down, ctx->xp_f, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-    launch_resid_w(st, x, ctx->part, L.down.P, T, Mpad, H, round, next_ln1, next_ln1 ? ceil_div(H, 64) : 0,
+    launch_resid_w(st, x, ctx->part, gemm_planes(L.down, T, ctx->ncu), T, Mpad, H, round, next_ln1, next_ln1 ? ceil_div(H, 64) : 0,
                    next_ln1 ? ctx->xp_h : nullptr, ctx->ssp);
 }
 
@@ -1190,15 +1191,15 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
             const LinGeom& lg = ctx->lg;
             launch_gemm(st, L.lin, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
             if (longest > LIN_SEQ_ROWS)
-                launch_lin_conv_rows(st, ctx->part, L.lin.P, T, pm.njobs, pm.row_job, pm.jobs, rs, L.conv, lg, L.state,
+                launch_lin_conv_rows(st, ctx->part, gemm_planes(L.lin, T, ctx->ncu), T, pm.njobs, pm.row_job, pm.jobs, rs, L.conv, lg, L.state,
                                      ctx->lraw, ctx->lrep, ctx->lring);
             else
-                launch_lin_conv(st, ctx->part, L.lin.P, T, pm.njobs, pm.jobs, rs, L.conv, lg, L.state, ctx->lraw,
+                launch_lin_conv(st, ctx->part, gemm_planes(L.lin, T, ctx->ncu), T, pm.njobs, pm.jobs, rs, L.conv, lg, L.state, ctx->lraw,
                                 ctx->lrep);
             launch_gdn(st, ctx->lraw, ctx->lrep, pm.njobs, pm.jobs, L.gp, lg, L.state, ctx->lcore);
             launch_lin_norm(st, ctx->lcore, ctx->lraw, L.gnorm, d.rms_eps, T, lg, L.out.KU, ctx->xp_v);
             launch_gemm(st, L.out, ctx->xp_v, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-            launch_resid_w(st, ctx->x, ctx->part, L.out.P, T, Mpad, H, 0, L.ln2, KUH, ctx->xp_h, ctx->ssp);
+            launch_resid_w(st, ctx->x, ctx->part, gemm_planes(L.out, T, ctx->ncu), T, Mpad, H, 0, L.ln2, KUH, ctx->xp_h, ctx->ssp);
         } else {
             full_attn_half(ctx, L, ctx->x, T, Mpad, pm);
         }
@@ -1220,9 +1221,9 @@ static void mtp_input(cc_ctx* ctx, const int32_t* ids, float* hin, int T) {
                       nullptr);
     launch_resid_norm(st, hin, nullptr, nullptr, 0, T, Mpad, H, 0, ctx->hnorm, d.rms_eps, KUH, ctx->xp_hh, nullptr);
     launch_gemm(st, ctx->fc_e, ctx->xp_e, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-    launch_sum_splits(st, ctx->part, ctx->fc_e.P, T, H, ctx->mx);
+    launch_sum_splits(st, ctx->part, gemm_planes(ctx->fc_e, T, ctx->ncu), T, H, ctx->mx);
     launch_gemm(st, ctx->fc_h, ctx->xp_hh, ctx->mt_alloc, ctx->part, T, ctx->ncu);
-    launch_resid_w(st, ctx->mx, ctx->part, ctx->fc_h.P, T, Mpad, H, 0, ctx->mtpL.ln1, KUH, ctx->xp_h, ctx->ssp);
+    launch_resid_w(st, ctx->mx, ctx->part, gemm_planes(ctx->fc_h, T, ctx->ncu), T, Mpad, H, 0, ctx->mtpL.ln1, KUH, ctx->xp_h, ctx->ssp);
 }
 
 // The MTP layer's KV rows for a pass's MTP jobs (stage.js:1404-1421): each
@@ -1245,7 +1246,7 @@ static void mtp_fill(cc_ctx* ctx, const MetaLayout& ml, int Tm, int njobs) {
         ex.eps = d.rms_eps;
         ex.gate = ctx->gbuf;
     }
-    launch_fin_qkv(st, ctx->part, M.qkv.P, Tm, mrow, mj, d.n_heads, ctx->group, ctx->geom, ctx->tbl, ctx->rot, M.kpool,
+    launch_fin_qkv(st, ctx->part, gemm_planes(M.qkv, Tm, ctx->ncu), Tm, mrow, mj, d.n_heads, ctx->group, ctx->geom, ctx->tbl, ctx->rot, M.kpool,
                    M.vpool, ctx->page_table, ctx->qp, row_scale_of(ctx), 0, 1, ex);
     (void)njobs;
 }
@@ -1484,7 +1485,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
                           ctx->norm, d.rms_eps, hw.KU, ctx->xp_h, nullptr);
         launch_gemm(st, hw, ctx->xp_h, ctx->mt_alloc, ctx->logits, S, ctx->ncu);
         ctx->head_rows = S;
-        launch_topk(st, ctx->logits, hw.P, S, d.vocab, topk, ctx->tk_a, ctx->tk_b, ctx->d_vals, ctx->d_ids);
+        launch_topk(st, ctx->logits, gemm_planes(hw, S, ctx->ncu), S, d.vocab, topk, ctx->tk_a, ctx->tk_b, ctx->d_vals, ctx->d_ids);
         HIPCHK(hipMemcpyAsync(hout, ctx->d_vals, (size_t)S * topk * 4, hipMemcpyDeviceToHost, st));
         HIPCHK(hipMemcpyAsync((uint8_t*)hout + (size_t)S * topk * 4, ctx->d_ids, (size_t)S * topk * 4,
                               hipMemcpyDeviceToHost, st));
@@ -1627,7 +1628,7 @@ cc_status cc_decode_steps(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_
         launch_resid_norm(st, ctx->x, (const int32_t*)(ctx->d_meta + ml.head_rows), nullptr, 0, S, Mpad, d.hidden, 0,
                           ctx->norm, d.rms_eps, hw.KU, ctx->xp_h, nullptr);
         launch_gemm(st, hw, ctx->xp_h, ctx->mt_alloc, ctx->logits, S, ctx->ncu);
-        launch_topk(st, ctx->logits, hw.P, S, d.vocab, topk, ctx->tk_a, ctx->tk_b, ctx->dec_vals + k * per,
+        launch_topk(st, ctx->logits, gemm_planes(hw, S, ctx->ncu), S, d.vocab, topk, ctx->tk_a, ctx->tk_b, ctx->dec_vals + k * per,
                     ctx->dec_ids + k * per);
         for (auto& j : cur) j.past++;
     }
@@ -1730,7 +1731,7 @@ cc_status cc_mtp_draft(cc_ctx* ctx, int32_t slot, int32_t row, int32_t token, in
         launch_resid_norm(st, ctx->mx, nullptr, nullptr, 0, 1, 32, H, 0, ctx->mtp_norm, d.rms_eps, KUH, ctx->xp_h,
                           nullptr);
         launch_gemm(st, ctx->head_draft, ctx->xp_h, ctx->mt_alloc, ctx->mtp_logits, 1, ctx->ncu);
-        launch_topk(st, ctx->mtp_logits, ctx->head_draft.P, 1, d.mtp_vocab, 1, ctx->tk_a, ctx->tk_b, ctx->d_vals,
+        launch_topk(st, ctx->mtp_logits, gemm_planes(ctx->head_draft, 1, ctx->ncu), 1, d.mtp_vocab, 1, ctx->tk_a, ctx->tk_b, ctx->d_vals,
                     (uint32_t*)(ids + k + 1));
         if (k + 1 < K)
             HIPCHK(hipMemcpyAsync(ctx->mtp_in, ctx->mx, (size_t)H * 4, hipMemcpyDeviceToDevice, st));
@@ -1771,7 +1772,7 @@ cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K, con
     launch_tile_q8(st, dW, dS, N, K, 32, q, 0);
     launch_prep_rows(st, dX, K, M, Mt * 16, K, q.KU, dXp);
     launch_gemm(st, q, dXp, Mt, dP, M, ctx->ncu);
-    launch_sum_splits(st, dP, sp, M, N, dY);
+    launch_sum_splits(st, dP, gemm_planes(q, M, ctx->ncu), M, N, dY);
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(take_launch_error());
     HIPCHK(hipMemcpy(Y, dY, (size_t)M * N * 4, hipMemcpyDeviceToHost));

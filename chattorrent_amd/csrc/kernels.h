@@ -83,10 +83,13 @@ struct RowScale {
     float eps = 0.f;
 };
 
-// Y planes: out[(r*M + m)*N + n], r < w.P.
+// Y planes: out[(r*M + m)*N + n], r < gemm_planes(w, M, ncu).
 // Xp holds xp_mtiles m-tiles (16 rows each) of the operand; M > 32 reads
 // those past M only as zeros.
 void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtiles, float* out, int M, int ncu);
+// The partial planes launch_gemm writes for w at M rows, which its consumers
+// add in plane order: w.P, or 1 when the matmul adds them itself.
+int gemm_planes(const QTensor& w, int M, int ncu);
 int lx_groups(const QTensor& w, int ncu);
 void launch_prep_rows(hipStream_t st, const float* x, int ldx, int M, int Mpad, int K, int KU,
                       uint4* Xp);

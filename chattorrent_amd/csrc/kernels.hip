@@ -46,7 +46,8 @@ hipError_t take_launch_error() {
 // parts in unit order; the parts meet in LDS once every wave is past its last
 // step (the activations are dead by then). Every split point depends on N, K
 // and the CU count, never on M, so a row's result is the same in any batch.
-// Output: plane r to out[(r*M + m)*N + n]; consumers add planes 0..P-1 in order.
+// Output: plane r to out[(r*M + m)*N + n]; consumers add planes 0..P-1 in order
+// (gemm_planes: one plane when k_gemm_tm_sum has added them).
 constexpr int LX_WAVES = 8;
 constexpr int LX_R = 4;
 
@@ -480,6 +481,218 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm(const uint8_t* __rest
     }
 }
 
+// k_gemm_tm_sum: k_gemm_tm over every plane of its pairs and rows in one
+// workgroup, unit by unit in K order. Each plane is finished as k_gemm_tm
+// finishes it (the same segments and folds), and the finished planes are
+// added in plane order into the one plane it writes: the sum every consumer
+// forms from the P planes (in order from plane 0; those that pad with zero
+// loads pad this sum the same way when P < 16), so the bits are the same,
+// and the P-plane write and read are spared. For rows enough to fill the
+// GPU without the K split (gemm_planes).
+__global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm_sum(const uint8_t* __restrict__ Wr,
+                                                              const uint4* __restrict__ Xp, int xp_mtiles,
+                                                              float* __restrict__ out, int KU, int M, int N, int Nt,
+                                                              int P, int Gm) {
+    constexpr int NT = 2, R = TM_R, PW = R - 1, MTL = TM_MT, MTW = MTL * TM_PAIRS / TM_WAVES;
+    static_assert(MTW * TM_WAVES == MTL * TM_PAIRS, "waves cover pairs x m-tiles");
+    __shared__ u32x4 xs[2][MTL * 4][64];   // two units: block (m-tile, q = 2h + hl) of 1 KiB
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int npairs = Nt / NT;
+    // Each pair group goes to one XCD, which runs its row blocks back to back
+    // (the mapping of k_gemm_tm with one plane).
+    const int nrb = (M + 16 * MTL - 1) / (16 * MTL), npg = (npairs + TM_PAIRS - 1) / TM_PAIRS;
+    const int kx = blockIdx.x / 8;
+    const int gx = (kx / nrb) * 8 + blockIdx.x % 8, gy = kx % nrb;
+    if (gx >= npg) return;   // the grid is rounded up to whole XCD rounds
+    const int pb = gx;
+    const int pair = pb * TM_PAIRS + wave % TM_PAIRS, mw = (wave / TM_PAIRS) * MTW;   // m-tiles mw .. mw+MTW-1
+    const bool has = pair < npairs;
+    const int ua = 0, len = KU;   // every unit, planes in order
+    const int mt0 = gy * MTL;
+    const int G2 = 2 * KU;
+    const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)Wr, 0, 0x7fffffff, 0x00020000);
+    // activation m-tiles past the operand's allocation read zero
+    const uint32_t xbytes = (uint32_t)min((unsigned long long)xp_mtiles * G2 * 2048ull, 0xffffffffull);
+    const auto rx = __builtin_amdgcn_make_buffer_rsrc((void*)Xp, 0, xbytes, 0x00020000);
+    const auto ro = __builtin_amdgcn_make_buffer_rsrc((void*)out, 0, M * N * 4, 0x00020000);
+    const int vw = lane * 16, vs = NT * 1024 + (lane & 15) * NT * 4;
+    const int vo = (4 * (lane >> 4) * N + (lane & 15)) * 4;
+    const int pr0 = has ? pair : 0;
+    // the load cursor (units are loaded in increasing order, PW ahead of
+    // compute): the plane holding the next unit to load and its first record
+    int lp = 0, lend = lx_plane_start(1, KU, P), lbase = 0, lrec = pr0 * lend * LX_REC;
+    // the compute cursor: the plane being summed, its end and cut points
+    int cp = 0, cbase = 0, cend = lend;
+    uint32_t cuts = has ? lx_cuts(pair, npairs, Gm, cend) : 0u;
+
+    // this wave's share of a unit's activations: blocks BPW*wave .. +BPW-1
+    constexpr int BPW = MTL * 4 / TM_WAVES;
+    static_assert(BPW * TM_WAVES == MTL * 4, "activation blocks split evenly over the waves");
+    u32x4 st[BPW];
+    auto load_x = [&](int u) {
+        const int Uk = ua + (u < len ? u : len - 1);
+#pragma unroll
+        for (int k = 0; k < BPW; k++) {
+            const int b = BPW * wave + k, mt = b >> 2, q = b & 3;
+            const int src = ((mt0 + mt) * G2 + 2 * Uk + (q >> 1)) * 2 + (q & 1);
+            st[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, vw, src * 1024, 0);
+        }
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < BPW; k++) xs[buf][BPW * wave + k][lane] = st[k];
+    };
+    u32x4 w[R][NT];
+    uint32_t sc[R][NT];
+    auto load_w = [&](int u, u32x4 (&wv)[NT], uint32_t (&sv)[NT]) {
+        u = u < len ? u : len - 1;
+        while (u >= lend) {   // the next plane: records [plane][pair][unit]
+            lp++;
+            lbase = lend;
+            lend = lx_plane_start(lp + 1, KU, P);
+            lrec = (lbase * npairs + pr0 * (lend - lbase)) * LX_REC;
+        }
+        const int off = lrec + (u - lbase) * LX_REC;
+        wv[0] = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, off, 2);
+        wv[1] = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, off + 1024, 2);
+        const auto s2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vs, off, 0);
+        sv[0] = s2[0];
+        sv[1] = s2[1];
+    };
+    float4_t seg[MTW][NT], tot[MTW][NT], sum[MTW][NT];
+#pragma unroll
+    for (int mt = 0; mt < MTW; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) seg[mt][nt] = tot[mt][nt] = sum[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    bool started = false;   // tot holds the first segment(s)
+
+    load_x(0);
+#pragma unroll
+    for (int i = 0; i < PW; i++) load_w(i, w[i], sc[i]);
+    store_x(0);
+    load_x(1);
+    __syncthreads();
+
+    auto unit = [&](int u, const u32x4 (&wc)[NT], const uint32_t (&sv)[NT]) {
+        const int buf = u & 1;
+        // the unit k_gemm_lx begins a new partial sum at: fold the running one
+        if ((cuts >> (u - cbase)) & 1u) {
+#pragma unroll
+            for (int mt = 0; mt < MTW; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    if (started)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) tot[mt][nt][e] = tot[mt][nt][e] + seg[mt][nt][e];
+                    else
+                        tot[mt][nt] = seg[mt][nt];
+                    seg[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+                }
+            started = true;
+        }
+        half8_t b[2][NT];
+        float scale[2][NT];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                b[h][nt] = h ? dequant8_biased(wc[nt][2], wc[nt][3]) : dequant8_biased(wc[nt][0], wc[nt][1]);
+                const uint16_t s16 = h ? (uint16_t)(sv[nt] >> 16) : (uint16_t)(sv[nt] & 0xffffu);
+                scale[h][nt] = (float)__builtin_bit_cast(_Float16, s16);
+            }
+#pragma unroll
+        for (int mt = 0; mt < MTW; mt++) {
+            u32x4 xv[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) xv[q] = xs[buf][(mw + mt) * 4 + q][lane];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                float4_t pp[NT];
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h]), b[h][nt], float4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h + 1]), b[h][nt], pp[nt]);
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) seg[mt][nt][e] = __builtin_fmaf(scale[h][nt], pp[nt][e], seg[mt][nt][e]);
+            }
+        }
+        if (u + 1 == cend) {   // the plane's value (its last segment folded in) joins the sum
+#pragma unroll
+            for (int mt = 0; mt < MTW; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++) {
+                    float4_t v = seg[mt][nt];
+                    if (started)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) v[e] = tot[mt][nt][e] + seg[mt][nt][e];
+                    if (cp == 0)
+                        sum[mt][nt] = v;
+                    else
+#pragma unroll
+                        for (int e = 0; e < 4; e++) sum[mt][nt][e] = sum[mt][nt][e] + v[e];
+                    seg[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+                }
+            started = false;
+            if (cp + 1 < P) {
+                cp++;
+                cbase = cend;
+                cend = lx_plane_start(cp + 1, KU, P);
+                cuts = has ? lx_cuts(pair, npairs, Gm, cend - cbase) : 0u;
+            }
+        }
+    };
+    int u = 0;
+    for (; u + R <= len; u += R) {
+#pragma unroll
+        for (int I = 0; I < R; I++) {
+            load_w(u + I + PW, w[(I + PW) % R], sc[(I + PW) % R]);
+            unit(u + I, w[I], sc[I]);
+            // the next unit's activations go in the other buffer: every wave
+            // finished reading it (one unit ago) before the last barrier
+            store_x((I + 1) & 1);
+            load_x(u + I + 2);
+            __syncthreads();
+        }
+    }
+    // at most PW units remain, their records in ring slots 0 .. PW-1
+#pragma unroll
+    for (int I = 0; I < PW; I++) {
+        if (u + I < len) {
+            unit(u + I, w[I], sc[I]);
+            store_x((I + 1) & 1);
+            load_x(u + I + 2);
+            __syncthreads();
+        }
+    }
+    if (!has) return;
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int tile = pair * NT + nt;
+        if (tile * 16 >= N) continue;
+        if (tile * 16 + 16 > N && tile * 16 + (lane & 15) >= N) continue;
+#pragma unroll
+        for (int mt = 0; mt < MTW; mt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sum[mt][nt][e]), ro,
+                                                      vo + (((mt0 + mw + mt) * 16 + e) * N + tile * 16) * 4, 0, 0);
+    }
+}
+
+// The planes launch_gemm writes for w at M rows: w.P, or one when the many
+// rows give every CU two workgroups or more without the K split
+// (k_gemm_tm_sum, 2 <= P < 16).
+int gemm_planes(const QTensor& w, int M, int ncu) {
+    if (M <= 32 || w.P < 2 || w.P >= 16) return w.P;
+    const long long work = (long long)((w.Nt / 2 + TM_PAIRS - 1) / TM_PAIRS) * ((M + 16 * TM_MT - 1) / (16 * TM_MT));
+    return work >= 2LL * ncu ? 1 : w.P;
+}
+
 void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtiles, float* out, int M, int ncu) {
     if (M <= 16) launch_lx<1>(st, w, Xp, out, M, ncu);
     else if (M <= 32) launch_lx<2>(st, w, Xp, out, M, ncu);
@@ -487,10 +700,15 @@ void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtile
         // the same planes and cut points as k_gemm_lx (lx_groups)
         const int Gm = lx_groups(w, ncu) / w.P;
         const int npairs = w.Nt / 2;
-        const int units = w.P * ((npairs + TM_PAIRS - 1) / TM_PAIRS), nrb = (M + 16 * TM_MT - 1) / (16 * TM_MT);
+        const bool sum = gemm_planes(w, M, ncu) == 1;
+        const int units = (sum ? 1 : w.P) * ((npairs + TM_PAIRS - 1) / TM_PAIRS), nrb = (M + 16 * TM_MT - 1) / (16 * TM_MT);
         dim3 grid(8 * ((units + 7) / 8) * nrb);
-        hipLaunchKernelGGL(k_gemm_tm, grid, dim3(64 * TM_WAVES), 0, st, (const uint8_t*)w.codes, Xp, xp_mtiles, out,
-                           w.KU, M, w.N, w.Nt, w.P, Gm);
+        if (sum)
+            hipLaunchKernelGGL(k_gemm_tm_sum, grid, dim3(64 * TM_WAVES), 0, st, (const uint8_t*)w.codes, Xp, xp_mtiles,
+                               out, w.KU, M, w.N, w.Nt, w.P, Gm);
+        else
+            hipLaunchKernelGGL(k_gemm_tm, grid, dim3(64 * TM_WAVES), 0, st, (const uint8_t*)w.codes, Xp, xp_mtiles, out,
+                               w.KU, M, w.N, w.Nt, w.P, Gm);
     }
     CHECK_LAUNCH();
 }

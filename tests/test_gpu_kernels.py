@@ -100,6 +100,28 @@ def test_matmul_many_rows_bitwise(ctx):
         assert np.array_equal(few.view(np.uint32), rows[:32].view(np.uint32)), M
 
 
+@pytest.mark.parametrize("K", [2560, 5120])
+def test_matmul_summed_planes_bitwise(ctx, K):
+    """With rows enough to fill the GPU without the K split (here 2048 rows x
+    N 8192), the many-row matmul adds its K planes itself and writes one: the
+    rows keep the bits of the one-row, 32-row and 200-row calls, which write
+    the planes separately (K 2560: 2 planes; K 5120: 4, with the 32-row
+    kernel's cut points inside them)."""
+    from oracle import lib as L
+    rng = np.random.default_rng(41 + K)
+    N, M = 8192, 2048
+    W = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    S16 = L.to_f16((rng.random((N, K // 32)) * 2 - 1).astype(np.float32))
+    X = (rng.random((M, K), np.float32) * 2 - 1).astype(np.float32)
+    rows = ctx.op_matmul_q8(X, W, S16)
+    for i in (0, 1, 777, M - 1):
+        one = ctx.op_matmul_q8(X[i:i + 1], W, S16)
+        assert np.array_equal(one.view(np.uint32), rows[i:i + 1].view(np.uint32)), i
+    for a, n in ((0, 32), (1000, 200)):
+        part = ctx.op_matmul_q8(X[a:a + n], W, S16)
+        assert np.array_equal(part.view(np.uint32), rows[a:a + n].view(np.uint32)), (a, n)
+
+
 @pytest.mark.parametrize("V,M", [(1000, 1), (1000, 5), (49152, 40), (151936, 1), (151936, 256)])
 def test_topk_exact(ctx, V, M):
     """topk_stage/topkRows (web/model/kernels.js:1453-1507, :2129-2144): best M
