@@ -877,20 +877,32 @@ void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const floa
 // multiplies the summed planes by f (row_scale). This takes the row-wide
 // reduction off the path between the residual step and the matmul, so the
 // residual step spreads over (slice, row) workgroups instead of one per row.
-__device__ static inline float row_scale(const RowScale& rs, int m) {
-    if (!rs.ssp) return 1.0f;
-    // all RW_SMAX loads in flight at once through a resource sized to the nsl
-    // partials (past them a load reads zero, and adding +0 changes nothing)
-    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void*)(rs.ssp + (size_t)m * RW_SMAX), 0, rs.nsl * 4,
-                                                      0x00020000);
+// In two parts, so a caller can issue the loads beside its own:
+// row_scale_load puts all RW_SMAX loads of row m in flight at once (the
+// resource's base is the array's, uniform for any m; the slots past the nsl
+// partials read as zero), row_scale_of adds them in order.
+struct RowSS {
     float q[RW_SMAX];
+};
+__device__ static inline RowSS row_scale_load(const RowScale& rs, int m) {
+    RowSS r;
+    if (!rs.ssp) return r;
+    const auto rq = __builtin_amdgcn_make_buffer_rsrc((void*)rs.ssp, 0, 0x7fffffff, 0x00020000);
 #pragma unroll
-    for (int s = 0; s < RW_SMAX; s++) q[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rq, 4 * s, 0, 0));
+    for (int s = 0; s < RW_SMAX; s++) {
+        const float v = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rq, (m * RW_SMAX + s) * 4, 0, 0));
+        r.q[s] = s < rs.nsl ? v : 0.0f;
+    }
+    return r;
+}
+__device__ static inline float row_scale_of(const RowScale& rs, const RowSS& r) {
+    if (!rs.ssp) return 1.0f;
     float tot = 0.0f;
 #pragma unroll
-    for (int s = 0; s < RW_SMAX; s++) tot = tot + q[s];
+    for (int s = 0; s < RW_SMAX; s++) tot = tot + r.q[s];
     return 1.0f / sqrtf(tot / (float)rs.H + rs.eps);
 }
+__device__ static inline float row_scale(const RowScale& rs, int m) { return row_scale_of(rs, row_scale_load(rs, m)); }
 
 // Residual step (add_inplace, web/model/kernels.js:1334-1346: x plus the
 // projection's planes added in order; optional round_f16, :1356-1383, the
@@ -982,6 +994,10 @@ void launch_resid_w(hipStream_t st, float* x, const float* part, int splits, int
 
 // SwiGLU (web/model/kernels.js:1513-1529 silu_mul): act = g * (1/(1+exp(-g)))
 // * up over the fused gate|up projection, straight into the down operand.
+// SP > 0: at most SP planes, every plane's loads issued at once (through a
+// resource sized to the planes, so those past the last read zero and are not
+// added), before the row factor's; SP = 0: any plane count, in a loop.
+template <int SP>
 __global__ __launch_bounds__(256) void k_fin_swiglu(const float* __restrict__ part, int splits, int M, int Mpad,
                                                     int F, int KU, uint4* __restrict__ Xp, RowScale rs) {
     // one thread per (row, 8 columns); the planes are added in order
@@ -992,12 +1008,43 @@ __global__ __launch_bounds__(256) void k_fin_swiglu(const float* __restrict__ pa
     const size_t N2 = 2 * (size_t)F, plane = (size_t)M * N2;
     float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (m < M && k0 < F) {
-        // the gate|up operand carried x*w: rmsnorm's row factor goes on below
-        // (its loads issued here, beside the planes')
-        const float f = row_scale(rs, m);
         float g[8], u[8];
         const float* row = part + (size_t)m * N2 + k0;
-        if (k0 + 8 <= F && (F & 3) == 0) {
+        const bool fast = k0 + 8 <= F && (F & 3) == 0;
+        u32x4 q[SP > 0 ? SP : 1][4];
+        if constexpr (SP > 0) {
+            // issued by every thread (no branch to join): a thread off the fast
+            // path reads in-bounds or zero values it does not use
+            const auto rp = __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, (uint32_t)(splits * plane * 4),
+                                                              0x00020000);
+            const int at = (int)(((size_t)m * N2 + k0) * 4);
+#pragma unroll
+            for (int s = 0; s < SP; s++) {
+                const int so = (int)(s * plane * 4);
+                q[s][0] = __builtin_amdgcn_raw_buffer_load_b128(rp, at, so, 0);
+                q[s][1] = __builtin_amdgcn_raw_buffer_load_b128(rp, at + 16, so, 0);
+                q[s][2] = __builtin_amdgcn_raw_buffer_load_b128(rp, at + 4 * F, so, 0);
+                q[s][3] = __builtin_amdgcn_raw_buffer_load_b128(rp, at + 4 * F + 16, so, 0);
+            }
+        }
+        // the gate|up operand carried x*w: rmsnorm's row factor goes on below
+        // (its loads issued here, after the planes')
+        const RowSS rq = row_scale_load(rs, m);
+        if (SP > 0 && fast) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                g[j] = __uint_as_float(q[0][j >> 2][j & 3]);
+                u[j] = __uint_as_float(q[0][2 + (j >> 2)][j & 3]);
+            }
+#pragma unroll
+            for (int s = 1; s < SP; s++)
+                if (s < splits)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        g[j] = g[j] + __uint_as_float(q[s][j >> 2][j & 3]);
+                        u[j] = u[j] + __uint_as_float(q[s][2 + (j >> 2)][j & 3]);
+                    }
+        } else if (fast) {
             auto ld8 = [&](const float* p, float* x) {
                 const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
                 x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
@@ -1028,6 +1075,7 @@ __global__ __launch_bounds__(256) void k_fin_swiglu(const float* __restrict__ pa
                 }
             }
         }
+        const float f = row_scale_of(rs, rq);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             g[j] = g[j] * f;
@@ -1045,8 +1093,15 @@ __global__ __launch_bounds__(256) void k_fin_swiglu(const float* __restrict__ pa
 void launch_fin_swiglu(hipStream_t st, const float* part, int splits, int M, int Mpad, int F, int KU,
                        uint4* Xp, const RowScale& rs) {
     const int total = Mpad * 8 * KU;
-    hipLaunchKernelGGL(k_fin_swiglu, dim3((total + 255) / 256), dim3(256), 0, st, part, splits, M, Mpad, F,
-                       KU, Xp, rs);
+    const dim3 grid((total + 255) / 256);
+    // the buffer resource's offsets are 32-bit
+    const bool small = (size_t)splits * M * 2 * (size_t)F * 4 < (1ull << 31);
+    if (small && splits <= 1)
+        hipLaunchKernelGGL(k_fin_swiglu<1>, grid, dim3(256), 0, st, part, splits, M, Mpad, F, KU, Xp, rs);
+    else if (small && splits <= 4)
+        hipLaunchKernelGGL(k_fin_swiglu<4>, grid, dim3(256), 0, st, part, splits, M, Mpad, F, KU, Xp, rs);
+    else
+        hipLaunchKernelGGL(k_fin_swiglu<0>, grid, dim3(256), 0, st, part, splits, M, Mpad, F, KU, Xp, rs);
     CHECK_LAUNCH();
 }
 
@@ -1070,12 +1125,12 @@ __host__ __device__ static inline int vpos(int s) { return 16 * ((s & 15) >> 2) 
 // Bit-exact with the reference given the same q|k|v row: RoPE a*cs - o*sn
 // (no fused multiply-add: the build passes -ffp-contract=off), amax,
 // scale = amax/127, inv = scale > 0 ? 1/scale : 0, rint, clamp ±127.
-__device__ static inline float rope_at(const float* src, int c, int rot, const float* tbl, int pos) {
+// Channel c of one head after split-half RoPE, given the (cos, sin) of c's
+// pair at the row's position (tbl[(pos*(rot/2) + c mod rot/2)*2 + 0/1]);
+// channels from rot on pass through.
+__device__ static inline float rope_cs(const float* src, int c, int rot, float cs, float sn) {
     if (c >= rot) return src[c];
     const int half = rot >> 1;
-    const int i = c < half ? c : c - half;
-    const size_t k = ((size_t)pos * half + i) * 2;
-    const float cs = tbl[k], sn = tbl[k + 1];
     if (c < half) {
         const float a = src[c], o = src[c + half];
         return a * cs - o * sn;
@@ -1106,30 +1161,53 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
     const int hidx = blockIdx.x * 4 + wave;
     const bool live = hidx < nall;
     const int N = nall * D;
-    // the row's job and its page, looked up while the planes load
+    // every plane's load in flight at once, first, through a resource sized to
+    // the planes: past the last one a load reads zero (no branch), and adding
+    // +0 leaves the in-order sum as it is
+    constexpr int SU = 16, DH = D / 64;
+    float pv[DH][SU];
+    if (live) {
+        const auto rp = __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, splits * M * N * 4, 0x00020000);
+#pragma unroll
+        for (int h = 0; h < DH; h++) {
+            const int at = (m * N + hidx * D + 64 * h + lane) * 4;
+#pragma unroll
+            for (int s = 0; s < SU; s++)
+                pv[h][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, at, s * M * N * 4, 0));
+        }
+    }
+    // the row's job and its page, and rmsnorm's row factor (the q|k|v operand
+    // carried x*w), looked up while the planes load
     const JobDev jb = jobs[row_job[m]];
     const int i = m - jb.row0;
     const int pos = jb.past + i;
     const uint32_t page = page_table[(size_t)jb.slot * g.max_pages + pos / g.page];
-    // the q|k|v operand carried x*w: rmsnorm's row factor goes on here
     const float f = row_scale(rs, m);
+    // RoPE's (cos, sin) for this lane's channels 64h + lane at pos, loaded
+    // here so they are in flight beside the planes
+    float cs[DH], sn[DH];
+    {
+        const int half = rot >> 1;
+#pragma unroll
+        for (int h = 0; h < DH; h++) {
+            const int c = 64 * h + lane;
+            cs[h] = 1.0f;
+            sn[h] = 0.0f;
+            if (c < rot) {
+                const float2 t2 = *(const float2*)(tbl + ((size_t)pos * half + (c < half ? c : c - half)) * 2);
+                cs[h] = t2.x;
+                sn[h] = t2.y;
+            }
+        }
+    }
     if (live) {
-        // every plane's load in flight at once, through a resource sized to the
-        // planes: past the last one a load reads zero (no branch), and adding
-        // +0 leaves the in-order sum as it is
-        constexpr int SU = 16;
-        const auto rp = __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, splits * M * N * 4, 0x00020000);
 #pragma unroll
-        for (int d0 = 0; d0 < D; d0 += 64) {
-            const int at = (m * N + hidx * D + d0 + lane) * 4;
-            float pv[SU];
+        for (int h = 0; h < DH; h++) {
+            float p = pv[h][0];
 #pragma unroll
-            for (int s = 0; s < SU; s++) pv[s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, at, s * M * N * 4, 0));
-            float p = pv[0];
-#pragma unroll
-            for (int s = 1; s < SU; s++) p = p + pv[s];
-            for (int s = SU; s < splits; s++) p = p + part[((size_t)s * M + m) * N + hidx * D + d0 + lane];
-            buf[wave][d0 + lane] = p * f;
+            for (int s = 1; s < SU; s++) p = p + pv[h][s];
+            for (int s = SU; s < splits; s++) p = p + part[((size_t)s * M + m) * N + hidx * D + 64 * h + lane];
+            buf[wave][64 * h + lane] = p * f;
         }
     }
     __syncthreads();
@@ -1149,7 +1227,8 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
     }
     if (live && hidx < nH) {
         if (do_q) {
-            for (int d = lane; d < D; d += 64) rq[wave][d] = rope_at(buf[wave], d, rot, tbl, pos);
+#pragma unroll
+            for (int h = 0; h < DH; h++) rq[wave][64 * h + lane] = rope_cs(buf[wave], 64 * h + lane, rot, cs[h], sn[h]);
         }
     }
     __syncthreads();
@@ -1189,9 +1268,9 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
     const int s = pos % g.page;
     uint8_t* blk = (which ? vpool : kpool) + ((size_t)page * nKV + n) * g.blk;
 #pragma unroll
-    for (int q0 = 0; q0 < D; q0 += 64) {
-        const int d = q0 + lane;
-        const float v = which ? buf[wave][d] : rope_at(buf[wave], d, rot, tbl, pos);
+    for (int h = 0; h < DH; h++) {
+        const int d = 64 * h + lane;
+        const float v = which ? buf[wave][d] : rope_cs(buf[wave], d, rot, cs[h], sn[h]);
         float amax = fabsf(v);
         for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
         const float scale = amax / 127.0f;
@@ -1899,14 +1978,41 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
     const size_t pstride = (size_t)16 * W;
     const float* base = part + (size_t)(jb.item0 + (kvh * jb.mtq + mt) * nc) * pstride;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // 16 rows x D columns, 8 a thread, in chunks of at most 128 columns (one
+    // chunk up to D = 128, two at D = 256); every thread reaches every barrier
+    const int sub = threadIdx.x >> 8, t = threadIdx.x & 255;
+    constexpr int CW = D < 128 ? D : 128, PRE = 8;
+    const int rl2 = t / (CW / 8);
+    const bool live = rl2 < 16 && mt * 16 + rl2 < R;
+    const int ca = (sub * nc) / COMBINE_SPLIT, c1 = ((sub + 1) * nc) / COMBINE_SPLIT;
+    // the first PRE chunks' values of the first column chunk, loaded before
+    // the weights are formed (they do not depend on them)
+    float4 pa[PRE], pb[PRE];
+    if (live) {
+        const float* src = base + (size_t)rl2 * W + 4 + (t % (CW / 8)) * 8;
+#pragma unroll
+        for (int u = 0; u < PRE; u++)
+            if (ca + u < c1) {
+                pa[u] = *(const float4*)(src + (ca + u) * pstride);
+                pb[u] = *(const float4*)(src + (ca + u) * pstride + 4);
+            }
+    }
     // only the m-tile's query rows rho < R were written (k_attn skips the rest)
     if (mt * 16 + wave < R) {
         const int rl = wave;   // 16 waves, one row each
-        float mloc = -INFINITY;
-        for (int c = lane; c < nc; c += 64) mloc = fmaxf(mloc, base[c * pstride + rl * W]);
+        // (max, sum) of chunk `lane` loaded once; chunks past 64 in a loop
+        const float2 ml0 = lane < nc ? *(const float2*)(base + lane * pstride + rl * W)
+                                     : make_float2(-INFINITY, 0.0f);
+        float mloc = ml0.x;
+        for (int c = lane + 64; c < nc; c += 64) mloc = fmaxf(mloc, base[c * pstride + rl * W]);
         const float M = wave_max(mloc);
         float lloc = 0.0f;
-        for (int c = lane; c < nc; c += 64) {
+        if (lane < nc) {
+            const float w = ml0.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml0.x - M);
+            wgt[rl][lane] = w;
+            lloc += ml0.y * w;
+        }
+        for (int c = lane + 64; c < nc; c += 64) {
             const float2 ml = *(const float2*)(base + c * pstride + rl * W);
             const float w = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
             wgt[rl][c] = w;
@@ -1916,12 +2022,7 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
         if (lane == 0) Ls[rl] = L;
     }
     __syncthreads();
-    // 16 rows x D columns, 8 a thread, in chunks of at most 128 columns (one
-    // chunk up to D = 128, two at D = 256); every thread reaches every barrier
-    const int sub = threadIdx.x >> 8, t = threadIdx.x & 255;
-    constexpr int CW = D < 128 ? D : 128;
-    const int rl = t / (CW / 8);
-    const bool live = rl < 16 && mt * 16 + rl < R;
+    const int rl = rl2;
     const int rho = mt * 16 + rl;
     for (int c0 = 0; c0 < D; c0 += CW) {
         const int d0 = c0 + (t % (CW / 8)) * 8;
@@ -1932,8 +2033,13 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
                 O[0] += a.x * w; O[1] += a.y * w; O[2] += a.z * w; O[3] += a.w * w;
                 O[4] += b.x * w; O[5] += b.y * w; O[6] += b.z * w; O[7] += b.w * w;
             };
-            const int c1 = ((sub + 1) * nc) / COMBINE_SPLIT;
-            int c = (sub * nc) / COMBINE_SPLIT;
+            int c = ca;
+            if (c0 == 0) {
+#pragma unroll
+                for (int u = 0; u < PRE; u++)
+                    if (ca + u < c1) add(pa[u], pb[u], wgt[rl][ca + u]);
+                c = ca + PRE < c1 ? ca + PRE : c1;
+            }
             for (; c + 8 <= c1; c += 8) {
                 float4 a[8], b[8];
 #pragma unroll
