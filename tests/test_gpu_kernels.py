@@ -100,16 +100,19 @@ def test_matmul_many_rows_bitwise(ctx):
         assert np.array_equal(few.view(np.uint32), rows[:32].view(np.uint32)), M
 
 
-@pytest.mark.parametrize("K", [2560, 5120])
-def test_matmul_summed_planes_bitwise(ctx, K):
-    """With rows enough to fill the GPU without the K split (here 2048 rows x
-    N 8192), the many-row matmul adds its K planes itself and writes one: the
-    rows keep the bits of the one-row, 32-row and 200-row calls, which write
-    the planes separately (K 2560: 2 planes; K 5120: 4, with the 32-row
-    kernel's cut points inside them)."""
+@pytest.mark.parametrize("K,N", [(2560, 8192), (5120, 8192), (4160, 8240), (2112, 4144)])
+def test_matmul_summed_planes_bitwise(ctx, K, N):
+    """With rows enough to fill the GPU without the K split (2048 rows: 32
+    blocks of 64 rows times N/256 pair groups is two workgroups a CU or more),
+    the many-row matmul adds its K planes itself and writes one: the rows keep
+    the bits of the one-row, 32-row and 200-row calls, which write the planes
+    separately. K 2560: 2 planes of 20 units; K 5120: 4, with the 32-row
+    kernel's cut points inside them; K 4160: planes of 16, 16, 16 and 17
+    units; K 2112: 16 and 17. N 8240 and 4144 end in a partial pair group and
+    a partial tile."""
     from oracle import lib as L
     rng = np.random.default_rng(41 + K)
-    N, M = 8192, 2048
+    M = 2048
     W = rng.integers(-127, 128, (N, K)).astype(np.int8)
     S16 = L.to_f16((rng.random((N, K // 32)) * 2 - 1).astype(np.float32))
     X = (rng.random((M, K), np.float32) * 2 - 1).astype(np.float32)
