@@ -1110,14 +1110,27 @@ void launch_fin_swiglu(hipStream_t st, const float* part, int splits, int M, int
 //   K: codes [64 tokens][D] with column d at (D/4)*((d%32)/8) + 8*(d/32) + d%8,
 //      so one lane's fragment bytes for every group are contiguous; then f32
 //      scales [64 tokens][ng].
-//   V: codes [D][64] with token s at vpos(s) = 16*((s%16)/4) + 4*(s/16) + s%4,
-//      so a lane's P·V fragments are contiguous; then f32 scales [ng][64] at
-//      the same positions.
+//   V: codes [4][D][16]: with v = vpos(s) = 16*((s%16)/4) + 4*(s/16) + s%4,
+//      token s's code for channel d sits in 16-byte row (v/16, d) at byte
+//      v%16, so a lane's P·V fragment (16 tokens of one channel) is one
+//      contiguous 16-byte load, and one token's D codes lie in D*16 bytes
+//      (a new token dirties 16 lines of 128 B at D = 128, not the 64 of a
+//      [D][64] layout); then f32 scales [4][ng][16] at the same positions.
 // Codes are stored biased (code ^ 0x80, i.e. code + 128) so the MFMA dequant
 // puts them under an f16 exponent directly; they are the reference's store_kv
 // codes bit for bit once converted back (k_kv_ref: cc_read_kv, cc_write_kv).
 __host__ __device__ static inline int kpos(int d, int D) { return (D / 4) * ((d & 31) >> 3) + 8 * (d >> 5) + (d & 7); }
 __host__ __device__ static inline int vpos(int s) { return 16 * ((s & 15) >> 2) + 4 * (s >> 4) + (s & 3); }
+// byte of V code (channel d, token s) in its block, and float of V scale
+// (group b, token s) after the codes
+__host__ __device__ static inline int vcode_at(int d, int s, int D) {
+    const int v = vpos(s);
+    return ((v >> 4) * D + d) * 16 + (v & 15);
+}
+__host__ __device__ static inline int vscale_at(int b, int s, int ng) {
+    const int v = vpos(s);
+    return ((v >> 4) * ng + b) * 16 + (v & 15);
+}
 
 // store_kv (web/model/kernels.js:1024-1073) for a row's K and V, plus RoPE on
 // its Q (kernels.js:1093-1129) into the attention operand, after the q|k|v
@@ -1283,8 +1296,8 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
             blk[(size_t)s * D + kpos(d, D)] = (uint8_t)((uint8_t)code ^ 0x80u);
             if ((d & 31) == 0) *(float*)(blk + 64 * D + ((size_t)s * g.ng + b) * 4) = scale;
         } else {
-            blk[(size_t)d * 64 + vpos(s)] = (uint8_t)((uint8_t)code ^ 0x80u);
-            if ((d & 31) == 0) *(float*)(blk + 64 * D + ((size_t)b * 64 + vpos(s)) * 4) = scale;
+            blk[vcode_at(d, s, D)] = (uint8_t)((uint8_t)code ^ 0x80u);
+            if ((d & 31) == 0) *(float*)(blk + 64 * D + (size_t)vscale_at(b, s, g.ng) * 4) = scale;
         }
     }
 }
@@ -1784,8 +1797,8 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
     };
     // Lane offsets inside a block (layout of k_fin_qkv's writes):
     const int vk = l16 * D + (D / 4) * j4;   // K codes: token row l16 of a 16-token tile, lane's k-block
-    const int vv = l16 * 64 + 16 * j4;       // V codes: d row l16 of a d-tile, lane's token block
-    // Scale blocks sit at 64*D in both blocks: K [64 tokens][NG], V [NG][64 at vpos].
+    const int vv = j4 * D * 16 + l16 * 16;   // V codes: lane's token block, channel l16 of a d-tile
+    // Scale blocks sit at 64*D in both blocks: K [64 tokens][NG], V [4][NG][16] at vpos.
 
     float mrow = -INFINITY, lsum = 0.0f;
     float4_t o[DT];
@@ -1809,7 +1822,7 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
     };
     auto load_v = [&](__amdgpu_buffer_rsrc_t rv) {
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) vc[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, dt * 1024, 0);
+        for (int dt = 0; dt < DT; dt++) vc[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, dt * 256, 0);
     };
     // One page. Its scale blocks arrived in kst/vst during the previous page;
     // they go to this wave's LDS slice first (a wave's LDS accesses run in
@@ -1881,7 +1894,7 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
                 float sv[16];   // the lane's 16 tokens of 32-block b
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const float4 f = *(const float4*)&vsl[wv][b * 64 + 16 * j4 + 4 * q];
+                    const float4 f = *(const float4*)&vsl[wv][(j4 * NG + b) * 16 + 4 * q];
                     sv[4 * q] = f.x; sv[4 * q + 1] = f.y; sv[4 * q + 2] = f.z; sv[4 * q + 3] = f.w;
                 }
 #pragma unroll
@@ -2609,12 +2622,12 @@ __global__ void k_fill_kv(uint8_t* __restrict__ pool, const uint32_t* __restrict
         uint8_t* blk = pool + ((size_t)page * g.nKV + n) * g.blk;
         const uint8_t biased = (uint8_t)((uint8_t)code ^ 0x80u);
         if (which == 0) blk[(size_t)s * D + kpos(d, D)] = biased;
-        else blk[(size_t)d * 64 + vpos(s)] = biased;
+        else blk[vcode_at(d, s, D)] = biased;
         if ((d & 31) == 0) {
             const float sc = half_value(gen_scale_f16(seed, stream ^ 0x5ca1eull, base, 0.005, 0.02));
             const int b = d >> 5;
             if (which == 0) *(float*)(blk + 64 * D + ((size_t)s * g.ng + b) * 4) = sc;
-            else *(float*)(blk + 64 * D + ((size_t)b * 64 + vpos(s)) * 4) = sc;
+            else *(float*)(blk + 64 * D + (size_t)vscale_at(b, s, g.ng) * 4) = sc;
         }
     }
 }
@@ -2647,7 +2660,7 @@ __global__ void k_kv_ref(uint8_t* __restrict__ pool, const uint32_t* __restrict_
             uint8_t* p[4];
             for (int j = 0; j < 4; j++) {
                 const int d = 4 * w + j;
-                p[j] = which == 0 ? blk + (size_t)s * D + kpos(d, D) : blk + (size_t)d * 64 + vpos(s);
+                p[j] = which == 0 ? blk + (size_t)s * D + kpos(d, D) : blk + vcode_at(d, s, D);
             }
             if (to_ref) {
                 uint32_t word = 0;
@@ -2660,7 +2673,7 @@ __global__ void k_kv_ref(uint8_t* __restrict__ pool, const uint32_t* __restrict_
         } else {
             const int b = w - D / 4;
             uint32_t* sp = which == 0 ? (uint32_t*)(blk + 64 * D + ((size_t)s * g.ng + b) * 4)
-                                      : (uint32_t*)(blk + 64 * D + ((size_t)b * 64 + vpos(s)) * 4);
+                                      : (uint32_t*)(blk + 64 * D + (size_t)vscale_at(b, s, g.ng) * 4);
             if (to_ref) rows[i] = *sp;
             else *sp = rows[i];
         }
