@@ -1165,7 +1165,7 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
                                                   const uint32_t* __restrict__ page_table, uint4* __restrict__ Qp,
                                                   RowScale rs, int do_q, int do_kv, QkExtras ex) {
     __shared__ float buf[4][D];
-    __shared__ float rq[4][D];
+    __shared__ __attribute__((aligned(16))) float rq[4][D];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m = blockIdx.y;
     const int nKV = g.nKV;
@@ -1259,10 +1259,13 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
         if (lane < D / 8) {
             const int d0 = 8 * lane;
             half8_t hi, lo;
+            // the lane's 8 channels as two 16-byte reads
+            const float4 qa = *(const float4*)&rq[wave][d0], qb = *(const float4*)&rq[wave][d0 + 4];
+            const float qv[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 _Float16 a, b;
-                split_hilo(rq[wave][d0 + j], a, b);
+                split_hilo(qv[j], a, b);
                 hi[j] = a;
                 lo[j] = b;
             }
@@ -1980,9 +1983,11 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
                                                        float* __restrict__ ctx_out,
                                                        const int32_t* __restrict__ wg_job,
                                                        const float* __restrict__ gate) {
-    __shared__ float wgt[16][COMBINE_CMAX];
+    // rows padded by one float: the four rows a wave reads at one chunk fall in
+    // different banks; the quarters' halves in separate arrays, 16 B a thread
+    __shared__ float wgt[16][COMBINE_CMAX + 1];
     __shared__ float Ls[16];
-    __shared__ float4 red[COMBINE_SPLIT - 1][256][2];
+    __shared__ float4 red[COMBINE_SPLIT - 1][2][256];
     const int job = wg_job[3 * blockIdx.x], kvh = wg_job[3 * blockIdx.x + 1], mt = wg_job[3 * blockIdx.x + 2];
     const JobDev jb = jobs[job];
     constexpr int W = D + 4;
@@ -2065,15 +2070,15 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
             }
             for (; c < c1; c++) add(*(const float4*)(src + c * pstride), *(const float4*)(src + c * pstride + 4), wgt[rl][c]);
             if (sub > 0) {
-                red[sub - 1][t][0] = make_float4(O[0], O[1], O[2], O[3]);
-                red[sub - 1][t][1] = make_float4(O[4], O[5], O[6], O[7]);
+                red[sub - 1][0][t] = make_float4(O[0], O[1], O[2], O[3]);
+                red[sub - 1][1][t] = make_float4(O[4], O[5], O[6], O[7]);
             }
         }
         __syncthreads();
         if (sub == 0 && live) {
 #pragma unroll
             for (int q = 0; q < COMBINE_SPLIT - 1; q++) {
-                const float4 a = red[q][t][0], b = red[q][t][1];
+                const float4 a = red[q][0][t], b = red[q][1][t];
                 O[0] += a.x; O[1] += a.y; O[2] += a.z; O[3] += a.w;
                 O[4] += b.x; O[5] += b.y; O[6] += b.z; O[7] += b.w;
             }
