@@ -49,7 +49,11 @@ hipError_t take_launch_error() {
 // Output: plane r to out[(r*M + m)*N + n]; consumers add planes 0..P-1 in order
 // (gemm_planes: one plane when k_gemm_tm_sum has added them).
 constexpr int LX_WAVES = 8;
-constexpr int LX_R = 4;
+// The weight ring: one record in flight a wave ahead of the one computed.
+// Measured at configs[2]: two or three records ahead made the pass 4-6%
+// slower (more requests outstanding across the GPU's 2048 waves), none ahead
+// 13% slower.
+constexpr int LX_R = 2;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
