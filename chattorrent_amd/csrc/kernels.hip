@@ -324,7 +324,8 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm(const uint8_t* __rest
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int npairs = Nt / NT;
-    // Workgroup b runs on XCD b % 8 (dispatch is round-robin over the XCDs).
+    // Workgroups b and b + 8 run on one XCD (dispatch is round-robin over the
+    // XCDs, from an offset that varies by launch).
     // Each (plane, pair group) goes to one XCD, which runs its row blocks back
     // to back, so the row blocks after the first read its weight records from
     // that XCD's L2 instead of HBM. The order of workgroups changes no sums.
