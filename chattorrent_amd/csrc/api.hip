@@ -284,7 +284,9 @@ cc_status check_dims(cc_ctx* ctx, const cc_dims& d, const cc_opts& o) {
 }
 
 struct StepPlan {
-    int T = 0, S = 0, nitems = 0, ncwg = 0;
+    // nitems: attention partials (job, kv head, m-tile, chunk); nlaunch: the
+    // item list k_attn takes (blocks of m-tiles padded to 4)
+    int T = 0, S = 0, nitems = 0, ncwg = 0, nlaunch = 0;
     std::vector<JobDev> jobs;
     std::vector<AttnItem> items;
     std::vector<int32_t> row_job, plan, head_rows, cwg;
@@ -365,7 +367,9 @@ double qbytes(const QTensor& q) { return (double)q.N * q.K * (1.0 + 2.0 / 32.0);
 // Attention work items a pass can hold: every (kv head, m-tile) of every job
 // times the most chunks of `ppw` pages a frame has.
 size_t max_items_for(const cc_ctx* ctx) {
-    return max_cwg_for(ctx) * ceil_div(ctx->max_pages, ctx->ppw) + 16;
+    // a job of several m-tiles pads each (kv head, chunk) to whole blocks of 4
+    const size_t mtiles = (size_t)ctx->geom.nKV * (ceil_div(ctx->o.t_max * ctx->group, 16) + 4 * ctx->o.max_jobs);
+    return mtiles * ceil_div(ctx->max_pages, ctx->ppw) + 16;
 }
 
 }  // namespace
@@ -1009,7 +1013,7 @@ static void plan_jobs(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, b
     p.kv_bytes = 0;
     const int ng = ctx->geom.ng;
     size_t qp = 0;
-    int row = 0, items = 0, cwg = 0, S = 0;
+    int row = 0, items = 0, cwg = 0, S = 0, nlaunch = 0;
     for (int j = 0; j < njobs; j++) {
         JobDev& jd = p.jobs[j];
         jd.slot = jobs[j].slot;
@@ -1026,6 +1030,7 @@ static void plan_jobs(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, b
         jd.nchunk = ceil_div(ceil_div(T_act, ctx->geom.page), ctx->ppw);
         jd.item0 = items;
         items += ctx->geom.nKV * jd.mtq * jd.nchunk;
+        nlaunch += ctx->geom.nKV * jd.nchunk * (jd.mtq > 1 ? 4 * ceil_div(jd.mtq, 4) : 1);
         cwg += ctx->geom.nKV * jd.mtq;
         if (head) S += jobs[j].sampled;
         row += jd.n;
@@ -1033,6 +1038,7 @@ static void plan_jobs(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, b
     p.T = row;
     p.S = S;
     p.nitems = items;
+    p.nlaunch = nlaunch;
     p.ncwg = cwg;
     p.qp_units = qp;
     p.apart_floats = (size_t)items * 16 * (ctx->D + 4);
@@ -1045,17 +1051,33 @@ static void plan_tables(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p,
     p.row_job.clear();
     p.head_rows.clear();
     p.cwg.clear();
-    const int ng = ctx->geom.ng;
+    const int ng = ctx->geom.ng, part = 16 * (ctx->D + 4);
+    // k_pack's order: the jobs of several m-tiles as (kv head, chunk, block of
+    // 4 m-tiles) workgroups, then the jobs of one m-tile
+    for (int pass = 0; pass < 2; pass++)
+        for (int j = 0; j < njobs; j++) {
+            const JobDev& jd = p.jobs[j];
+            if ((jd.mtq > 1) != (pass == 0)) continue;
+            const int nb = jd.mtq > 1 ? ceil_div(jd.mtq, 4) : 1, per = jd.mtq > 1 ? 4 : 1;
+            for (int h = 0; h < ctx->geom.nKV; h++)
+                for (int c = 0; c < jd.nchunk; c++)
+                    for (int b = 0; b < nb; b++)
+                        for (int q = 0; q < per; q++) {
+                            const int mt = per * b + q;
+                            if (mt >= jd.mtq) {
+                                p.items.push_back(AttnItem{0, 0, 0, -1, 0, 0, 0, 0});
+                                continue;
+                            }
+                            const int hm = h * jd.mtq + mt;
+                            const int32_t idx = jd.item0 + hm * jd.nchunk + c;
+                            p.items.push_back(AttnItem{jd.slot, jd.past, jd.n, mt, jd.qp_off + hm * ng * 128,
+                                                       idx * part, h, c * ctx->ppw});
+                        }
+        }
     for (int j = 0; j < njobs; j++) {
         const JobDev& jd = p.jobs[j];
         for (int h = 0; h < ctx->geom.nKV; h++)
             for (int mt = 0; mt < jd.mtq; mt++) {
-                const int32_t qb = jd.qp_off + ((h * jd.mtq + mt) * ng) * 128;
-                for (int c = 0; c < jd.nchunk; c++) {
-                    const int32_t idx = (int32_t)p.items.size();
-                    p.items.push_back(AttnItem{jd.slot, jd.past, jd.n, mt, qb, idx * 16 * (ctx->D + 4), h,
-                                               c * ctx->ppw});
-                }
                 p.cwg.push_back(j);
                 p.cwg.push_back(h);
                 p.cwg.push_back(mt);
@@ -1100,7 +1122,7 @@ struct PassMeta {
     const AttnItem* items = nullptr;
     const int32_t* row_job = nullptr;
     const int32_t* cwg = nullptr;
-    int njobs = 0, nitems = 0, ncwg = 0;
+    int njobs = 0, nitems = 0, ncwg = 0, nlaunch = 0;
 };
 
 static RowScale row_scale_of(const cc_ctx* ctx) {
@@ -1132,7 +1154,7 @@ static void full_attn_half(cc_ctx* ctx, Layer& L, float* x, int T, int Mpad, con
     launch_gemm(st, L.qkv, ctx->xp_h, ctx->mt_alloc, ctx->part, T, ctx->ncu);
     launch_fin_qkv(st, ctx->part, gemm_planes(L.qkv, T, ctx->ncu), T, pm.row_job, pm.jobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
                    L.kpool, L.vpool, ctx->page_table, ctx->qp, rs, 1, 1, ex);
-    launch_attn(st, pm.items, pm.nitems, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
+    launch_attn(st, pm.items, pm.nlaunch, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
                 ctx->ppw, ctx->apart);
     launch_attn_combine(st, pm.jobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU, ctx->xp_o, nullptr, pm.cwg,
                         pm.ncwg, ctx->hybrid ? ctx->gbuf : nullptr);
@@ -1177,6 +1199,7 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
     pm.cwg = (const int32_t*)(ctx->d_meta + ml.cwg);
     pm.njobs = (int)p.jobs.size();
     pm.nitems = p.nitems;
+    pm.nlaunch = p.nlaunch;
     pm.ncwg = p.ncwg;
     const RowScale rs = row_scale_of(ctx);
     const int KUH = ceil_div(H, 64);   // every block's first matmul reads K = hidden
@@ -1290,7 +1313,7 @@ static void prof_replay(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, in
                 for (int b = b0; b < b1; b++) {
                     const Layer& L = ctx->layers[b - ctx->L0];
                     if (!L.kpool) continue;
-                    launch_attn(st, ditems, p.nitems, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom,
+                    launch_attn(st, ditems, p.nlaunch, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom,
                                 ctx->group, ctx->ppw, ctx->apart);
                 }
             });
@@ -1389,7 +1412,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
 
     StepPlan p;
     plan_jobs(ctx, jobs, njobs, p, head);
-    if (p.nitems > (int)ctx->items_cap || (size_t)p.ncwg > max_cwg_for(ctx))
+    if (std::max(p.nitems, p.nlaunch) > (int)ctx->items_cap || (size_t)p.ncwg > max_cwg_for(ctx))
         return bad(-1, "too many attention items");
     cc_status gs = grow(ctx, p);
     if (gs != CC_OK) return gs;
@@ -1569,7 +1592,7 @@ cc_status cc_decode_steps(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_
     for (auto& j : last) j.past += steps - 1;
     StepPlan pl;
     plan_jobs(ctx, last.data(), njobs, pl, true);
-    if (pl.nitems > (int)ctx->items_cap || (size_t)pl.ncwg > max_cwg_for(ctx))
+    if (std::max(pl.nitems, pl.nlaunch) > (int)ctx->items_cap || (size_t)pl.ncwg > max_cwg_for(ctx))
         return fail(ctx, CC_EARG, "too many attention items");
     cc_status gs = grow(ctx, pl);
     if (gs != CC_OK) return gs;
@@ -1724,6 +1747,7 @@ cc_status cc_mtp_draft(cc_ctx* ctx, int32_t slot, int32_t row, int32_t token, in
         pm.cwg = (const int32_t*)(b + o_cwg);
         pm.njobs = 1;
         pm.nitems = plans[k].nitems;
+        pm.nlaunch = plans[k].nlaunch;
         pm.ncwg = plans[k].ncwg;
         mtp_input(ctx, ids + k, ctx->mtp_in, 1);
         full_attn_half(ctx, ctx->mtpL, ctx->mx, 1, mpad_of(1), pm);
@@ -1949,7 +1973,7 @@ cc_status cc_op_attend(cc_ctx* ctx, int32_t layer, int32_t slot, const float* q,
     const AttnItem* di = (const AttnItem*)(ctx->d_meta + ml.items);
     launch_fin_qkv(st, dr, 1, n, (const int32_t*)(ctx->d_meta + ml.row_job), dj, d.n_heads, ctx->group, ctx->geom,
                    ctx->tbl, ctx->rot, L.kpool, L.vpool, ctx->page_table, ctx->qp, RowScale{}, 1, 0);
-    launch_attn(st, di, p.nitems, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->ppw,
+    launch_attn(st, di, p.nlaunch, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->ppw,
                  ctx->apart);
     launch_attn_combine(st, dj, ctx->apart, ctx->geom, d.n_heads, ctx->group, KU, dXp, dctx,
                          (const int32_t*)(ctx->d_meta + ml.cwg), p.ncwg);

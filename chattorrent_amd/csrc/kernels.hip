@@ -1773,6 +1773,7 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
     const int wid = blockIdx.x * 4 + wv;
     if (wid >= nitems) return;   // no barriers below: a finished wave may leave
     const AttnItem it = items[wid];
+    if (it.mt < 0) return;   // a slot that pads a workgroup of m-tiles
     const int T_act = it.past + it.n;
     const int R = it.n * group;
     const int npg = (T_act + 63) >> 6;
@@ -2429,7 +2430,12 @@ void launch_ids_col0(hipStream_t st, const uint32_t* ids, int rows, int stride, 
 // written by all threads. A job of n rows at past p needs ceil(n*group/16)
 // Q m-tiles, ceil(ceil((p+n)/64)/ppw) chunks of pages per (kv head, m-tile),
 // one combine triple per (kv head, m-tile), and nKV*mtq*ng*128 Q-operand
-// units; each work item's softmax partial takes 16*(D+4) floats.
+// units; each work item's softmax partial takes 16*(D+4) floats, at the
+// item's index in (job, kv head, m-tile, chunk) order. The item list itself
+// holds the jobs of several m-tiles first, each (kv head, chunk) as blocks of
+// four m-tiles (padded with mt = -1), so one workgroup's four waves read the
+// same pages together and the pages come from HBM once; then the jobs of
+// one m-tile, chunk by chunk.
 constexpr int PACK_THREADS = 256;
 
 __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict__ in, int njobs, int step,
@@ -2437,7 +2443,8 @@ __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict
                                                        AttnItem* __restrict__ items, int32_t* __restrict__ row_job,
                                                        int32_t* __restrict__ head_rows, int32_t* __restrict__ cwg) {
     __shared__ int32_t s_row0[PACK_MAX_JOBS], s_item0[PACK_MAX_JOBS], s_cwg0[PACK_MAX_JOBS],
-        s_qp0[PACK_MAX_JOBS], s_head0[PACK_MAX_JOBS], s_mtq[PACK_MAX_JOBS], s_nch[PACK_MAX_JOBS];
+        s_qp0[PACK_MAX_JOBS], s_head0[PACK_MAX_JOBS], s_mtq[PACK_MAX_JOBS], s_nch[PACK_MAX_JOBS],
+        s_pos0[PACK_MAX_JOBS];
     for (int j = threadIdx.x; j < njobs; j += blockDim.x) {
         const int n = in[j].n, tact = in[j].past + step + n;
         s_mtq[j] = (n * g.group + 15) / 16;
@@ -2445,19 +2452,28 @@ __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        int row = 0, item = 0, c = 0, qp = 0, head = 0;
+        int row = 0, item = 0, c = 0, qp = 0, head = 0, pos = 0;
         for (int j = 0; j < njobs; j++) {
             s_row0[j] = row;
             s_item0[j] = item;
             s_cwg0[j] = c;
             s_qp0[j] = qp;
             s_head0[j] = head;
+            if (s_mtq[j] > 1) {   // the jobs of several m-tiles first
+                s_pos0[j] = pos;
+                pos += g.nKV * s_nch[j] * 4 * ((s_mtq[j] + 3) / 4);
+            }
             row += in[j].n;
             item += g.nKV * s_mtq[j] * s_nch[j];
             c += g.nKV * s_mtq[j];
             qp += g.nKV * s_mtq[j] * g.ng * 128;
             head += g.head ? in[j].sampled : 0;
         }
+        for (int j = 0; j < njobs; j++)
+            if (s_mtq[j] == 1) {
+                s_pos0[j] = pos;
+                pos += g.nKV * s_nch[j];
+            }
     }
     __syncthreads();
     const int part = 16 * (g.D + 4);
@@ -2478,11 +2494,28 @@ __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict
             jd.keep = pj.keep;
             jobs[j] = jd;
         }
-        const int nit = g.nKV * mtq * nch;
-        for (int x = threadIdx.x; x < nit; x += blockDim.x) {
-            const int c = x % nch, hm = x / nch, mt = hm % mtq, h = hm / mtq;
-            const int idx = s_item0[j] + x;
-            items[idx] = AttnItem{pj.slot, past, pj.n, mt, s_qp0[j] + (hm * g.ng) * 128, idx * part, h, c * g.ppw};
+        if (mtq == 1) {
+            for (int x = threadIdx.x; x < g.nKV * nch; x += blockDim.x) {
+                const int c = x % nch, h = x / nch;
+                const int idx = s_item0[j] + x;   // (kv head, m-tile 0, chunk)
+                items[s_pos0[j] + x] = AttnItem{pj.slot, past, pj.n, 0, s_qp0[j] + (h * g.ng) * 128, idx * part, h,
+                                                c * g.ppw};
+            }
+        } else {
+            // (kv head, chunk, block of 4 m-tiles, m-tile): a block is one workgroup
+            const int nb = (mtq + 3) / 4, nit = g.nKV * nch * nb * 4;
+            for (int x = threadIdx.x; x < nit; x += blockDim.x) {
+                const int q = x % 4, b = (x / 4) % nb, c = (x / (4 * nb)) % nch, h = x / (4 * nb * nch);
+                const int mt = 4 * b + q;
+                if (mt >= mtq) {
+                    items[s_pos0[j] + x] = AttnItem{0, 0, 0, -1, 0, 0, 0, 0};
+                    continue;
+                }
+                const int hm = h * mtq + mt;
+                const int idx = s_item0[j] + hm * nch + c;
+                items[s_pos0[j] + x] =
+                    AttnItem{pj.slot, past, pj.n, mt, s_qp0[j] + (hm * g.ng) * 128, idx * part, h, c * g.ppw};
+            }
         }
         for (int x = threadIdx.x; x < g.nKV * mtq; x += blockDim.x) {
             const int at = 3 * (s_cwg0[j] + x);
