@@ -1808,6 +1808,15 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
     const int vk = l16 * D + (D / 4) * j4;   // K codes: token row l16 of a 16-token tile, lane's k-block
     const int vv = j4 * D * 16 + l16 * 16;   // V codes: lane's token block, channel l16 of a d-tile
     // Scale blocks sit at 64*D in both blocks: K [64 tokens][NG], V [4][NG][16] at vpos.
+    // The V scales go to LDS as [NG][4][16]: the four token blocks a wave reads
+    // at once then sit in different banks. Each lane loads the 16 bytes it
+    // stores at its own LDS offset, so the stores are contiguous as well.
+    int vso[SCL];
+#pragma unroll
+    for (int q = 0; q < SCL; q++) {
+        const int e = 256 * q + lane * 4, b = e >> 6, jb = (e >> 4) & 3;
+        vso[q] = 4 * ((jb * NG + b) * 16 + (e & 15));
+    }
 
     float mrow = -INFINITY, lsum = 0.0f;
     float4_t o[DT];
@@ -1821,7 +1830,7 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
 #pragma unroll
         for (int q = 0; q < SCL; q++) {
             kst[q] = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16, 64 * D + 1024 * q, 0);
-            vst[q] = __builtin_amdgcn_raw_buffer_load_b128(rv, lane * 16, 64 * D + 1024 * q, 0);
+            vst[q] = __builtin_amdgcn_raw_buffer_load_b128(rv, vso[q], 64 * D, 0);
         }
 #pragma unroll
         for (int tt = 0; tt < 4; tt++)
@@ -1903,7 +1912,7 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
                 float sv[16];   // the lane's 16 tokens of 32-block b
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const float4 f = *(const float4*)&vsl[wv][(j4 * NG + b) * 16 + 4 * q];
+                    const float4 f = *(const float4*)&vsl[wv][b * 64 + 16 * j4 + 4 * q];
                     sv[4 * q] = f.x; sv[4 * q + 1] = f.y; sv[4 * q + 2] = f.z; sv[4 * q + 3] = f.w;
                 }
 #pragma unroll
