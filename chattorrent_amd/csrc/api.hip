@@ -114,6 +114,7 @@ struct cc_ctx {
     float* apart = nullptr;
     size_t apart_floats = 0;
     int ppw = 8;                   // pages per attention work item
+    AttnSched attn;                // attention launches' block counters
     AttnItem* d_items = nullptr;
     size_t items_cap = 0;
     float* logits = nullptr;       // LM-head planes [P][rows][vocab]
@@ -425,6 +426,8 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
             HIPCHK(hipGetDeviceProperties(&prop, o.device));
             ctx->ncu = std::max(1, prop.multiProcessorCount);
         }
+        HIPCHK(dalloc(ctx, &ctx->attn.ctr, 2 * sizeof(uint32_t), &ctx->scratch_bytes));
+        ctx->attn.ncu = ctx->ncu;
         HIPCHK(hipEventCreate(&ctx->ev0));
         HIPCHK(hipEventCreate(&ctx->ev1));
         ctx->group = d.n_heads / d.n_kv_heads;
@@ -1155,7 +1158,7 @@ static void full_attn_half(cc_ctx* ctx, Layer& L, float* x, int T, int Mpad, con
     launch_fin_qkv(st, ctx->part, gemm_planes(L.qkv, T, ctx->ncu), T, pm.row_job, pm.jobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
                    L.kpool, L.vpool, ctx->page_table, ctx->qp, rs, 1, 1, ex);
     launch_attn(st, pm.items, pm.nlaunch, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
-                ctx->ppw, ctx->apart);
+                ctx->ppw, ctx->apart, ctx->attn);
     launch_attn_combine(st, pm.jobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU, ctx->xp_o, nullptr, pm.cwg,
                         pm.ncwg, ctx->hybrid ? ctx->gbuf : nullptr);
     launch_gemm(st, L.o, ctx->xp_o, ctx->mt_alloc, ctx->part, T, ctx->ncu);
@@ -1314,7 +1317,7 @@ static void prof_replay(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, in
                     const Layer& L = ctx->layers[b - ctx->L0];
                     if (!L.kpool) continue;
                     launch_attn(st, ditems, p.nlaunch, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom,
-                                ctx->group, ctx->ppw, ctx->apart);
+                                ctx->group, ctx->ppw, ctx->apart, ctx->attn);
                 }
             });
         blocks(CC_K_O, &Layer::o, ctx->xp_o);
@@ -1974,7 +1977,7 @@ cc_status cc_op_attend(cc_ctx* ctx, int32_t layer, int32_t slot, const float* q,
     launch_fin_qkv(st, dr, 1, n, (const int32_t*)(ctx->d_meta + ml.row_job), dj, d.n_heads, ctx->group, ctx->geom,
                    ctx->tbl, ctx->rot, L.kpool, L.vpool, ctx->page_table, ctx->qp, RowScale{}, 1, 0);
     launch_attn(st, di, p.nlaunch, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->ppw,
-                 ctx->apart);
+                 ctx->apart, ctx->attn);
     launch_attn_combine(st, dj, ctx->apart, ctx->geom, d.n_heads, ctx->group, KU, dXp, dctx,
                          (const int32_t*)(ctx->d_meta + ml.cwg), p.ncwg);
     HIPCHK(hipStreamSynchronize(st));

@@ -198,9 +198,16 @@ void launch_resid_w(hipStream_t st, float* x, const float* part, int splits, int
                     const float* w, int KU, uint4* Xp, float* ssp);
 void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const float* part, int splits, int M,
                        int Mpad, int H, int round, const float* w, float eps, int KU, uint4* Xp, float* y);
+// The attention launches of one stream: the CU count and a pair of device
+// counters (zero at the start) from which launches a little over one round
+// of workgroups hand out their last blocks; seq counts the launches.
+struct AttnSched {
+    uint32_t* ctr = nullptr;   // 2 counters
+    int seq = 0, ncu = 0;
+};
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const uint4* Qp,
                   const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
-                  int ppw, float* part);
+                  int ppw, float* part, AttnSched& sc);
 // `gate` (a hybrid checkpoint's, [rows][nH*D], or null): the output is
 // multiplied by sigmoid(gate) before it becomes the o_proj operand
 // (web/model/kernels.js:1822-1839 sigmoid_mul).

@@ -1756,24 +1756,17 @@ void launch_lin_norm(hipStream_t st, const float* core, const float* lraw, const
 // Every lane builds its fragments and rescales O on every page, with no
 // branch on row state: MFMA reads all lanes' operands whatever the execution
 // mask, and a still fully masked row (max -inf) just takes alpha = 0, p = 0.
+// One work item of a wave: its (job, kv head, m-tile) over the chunk's pages,
+// with the wave's LDS slices for the page's K and V scale blocks.
 template <int NG>
-__global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __restrict__ items, int nitems,
-                                                 const uint4* __restrict__ Qp,
-                                                 const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
-                                                 const uint32_t* __restrict__ page_table, KVGeom g, int group, int ppw,
-                                                 float* __restrict__ part) {
+__device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __restrict__ Qp,
+                                          const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
+                                          const uint32_t* __restrict__ page_table, const KVGeom& g, int group,
+                                          int ppw, float* __restrict__ part, float* ksl_w, float* vsl_w) {
     constexpr int D = 32 * NG;
     constexpr int DT = D / 16;
-    // per wave, the current page's K and V scale blocks (64 tokens x NG groups, f32)
     constexpr int SCL = NG > 4 ? NG / 4 : 1;   // 1 KiB loads per scale block (16 B a lane)
-    __shared__ __attribute__((aligned(16))) float ksl[4][256 * SCL];
-    __shared__ __attribute__((aligned(16))) float vsl[4][256 * SCL];
     const int lane = threadIdx.x & 63, j4 = lane >> 4, l16 = lane & 15;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wid = blockIdx.x * 4 + wv;
-    if (wid >= nitems) return;   // no barriers below: a finished wave may leave
-    const AttnItem it = items[wid];
-    if (it.mt < 0) return;   // a slot that pads a workgroup of m-tiles
     const int T_act = it.past + it.n;
     const int R = it.n * group;
     const int npg = (T_act + 63) >> 6;
@@ -1850,8 +1843,8 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
         const int pn = p + 1 < p1 ? p + 1 : p;
 #pragma unroll
         for (int q = 0; q < SCL; q++) {
-            *(u32x4*)&ksl[wv][256 * q + lane * 4] = kst[q];
-            *(u32x4*)&vsl[wv][256 * q + lane * 4] = vst[q];
+            *(u32x4*)&ksl_w[256 * q + lane * 4] = kst[q];
+            *(u32x4*)&vsl_w[256 * q + lane * 4] = vst[q];
         }
         {
             float pr[4][4];
@@ -1862,7 +1855,7 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
                 float ks[4 * NG];   // tokens 16tt + 4j4 + r, groups 0..NG-1
 #pragma unroll
                 for (int q = 0; q < NG; q++) {
-                    const float4 f = *(const float4*)&ksl[wv][(tt * 16 + 4 * j4) * NG + 4 * q];
+                    const float4 f = *(const float4*)&ksl_w[(tt * 16 + 4 * j4) * NG + 4 * q];
                     ks[4 * q] = f.x; ks[4 * q + 1] = f.y; ks[4 * q + 2] = f.z; ks[4 * q + 3] = f.w;
                 }
                 float4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -1912,7 +1905,7 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
                 float sv[16];   // the lane's 16 tokens of 32-block b
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const float4 f = *(const float4*)&vsl[wv][b * 64 + 16 * j4 + 4 * q];
+                    const float4 f = *(const float4*)&vsl_w[b * 64 + 16 * j4 + 4 * q];
                     sv[4 * q] = f.x; sv[4 * q + 1] = f.y; sv[4 * q + 2] = f.z; sv[4 * q + 3] = f.w;
                 }
 #pragma unroll
@@ -1964,20 +1957,68 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
     }
 }
 
+
+// Work items go to waves in workgroups of four (item 4b + w to wave w of
+// block b). Workgroup i takes block i; with `dyn` set, it then takes blocks
+// gridDim.x, gridDim.x + 1, ... from the counter ctr[seq & 1] as it finishes
+// each (launch_attn sets it for launches a little over one round of
+// resident workgroups: dispatch hands a pending workgroup to a fixed XCD, so
+// the few blocks past the first round would wait for that XCD's slowest
+// workgroups). Each launch clears the counter of the next launch on its
+// stream, ctr[(seq + 1) & 1]; the one it counts with was cleared by the
+// launch before it.
+template <int NG>
+__global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __restrict__ items, int nitems,
+                                                 const uint4* __restrict__ Qp,
+                                                 const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
+                                                 const uint32_t* __restrict__ page_table, KVGeom g, int group, int ppw,
+                                                 float* __restrict__ part, uint32_t* __restrict__ ctr, int seq,
+                                                 int dyn) {
+    // per wave, the current page's K and V scale blocks (64 tokens x NG groups, f32)
+    constexpr int SCL = NG > 4 ? NG / 4 : 1;
+    __shared__ __attribute__((aligned(16))) float ksl[4][256 * SCL];
+    __shared__ __attribute__((aligned(16))) float vsl[4][256 * SCL];
+    __shared__ int s_blk;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_store(&ctr[(seq + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int nblk = (nitems + 3) / 4;
+    for (int blk = blockIdx.x;;) {
+        const int wid = blk * 4 + wv;
+        if (wid < nitems) {
+            const AttnItem it = items[wid];
+            if (it.mt >= 0)   // mt < 0: a slot that pads a workgroup of m-tiles
+                attn_item<NG>(it, Qp, kpool, vpool, page_table, g, group, ppw, part, ksl[wv], vsl[wv]);
+        }
+        if (!dyn) break;   // no barriers then: a finished wave may leave
+        __syncthreads();
+        if (threadIdx.x == 0) s_blk = (int)gridDim.x + (int)atomicAdd(&ctr[seq & 1], 1u);
+        __syncthreads();
+        blk = s_blk;
+        if (blk >= nblk) break;
+    }
+}
+
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const uint4* Qp,
                  const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
-                 int ppw, float* part) {
+                 int ppw, float* part, AttnSched& sc) {
     if (nitems <= 0) return;
-    const int blocks = (nitems + 3) / 4;
+    const int nblk = (nitems + 3) / 4;
+    const int cap = sc.ncu * (g.ng == 8 ? 1 : 2);   // workgroups resident at once
+    // blocks past the first round go out from the counter while they are few;
+    // with more, dispatch's own rounds balance them
+    const int dyn = nblk > cap && 2 * nblk <= 3 * cap;
+    const int blocks = dyn ? cap : nblk;
+    const int seq = sc.seq++;
     if (g.ng == 8)
         hipLaunchKernelGGL(k_attn<8>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
-                     group, ppw, part);
+                     group, ppw, part, sc.ctr, seq, dyn);
     else if (g.ng == 4)
         hipLaunchKernelGGL(k_attn<4>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
-                     group, ppw, part);
+                     group, ppw, part, sc.ctr, seq, dyn);
     else
         hipLaunchKernelGGL(k_attn<2>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
-                     group, ppw, part);
+                     group, ppw, part, sc.ctr, seq, dyn);
     CHECK_LAUNCH();
 }
 
