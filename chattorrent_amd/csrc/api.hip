@@ -1056,14 +1056,17 @@ static void plan_tables(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p,
     p.cwg.clear();
     const int ng = ctx->geom.ng, part = 16 * (ctx->D + 4);
     // k_pack's order: the jobs of several m-tiles as (kv head, chunk, block of
-    // 4 m-tiles) workgroups, then the jobs of one m-tile
-    for (int pass = 0; pass < 2; pass++)
+    // 4 m-tiles) workgroups, then the jobs of one m-tile, their full chunks
+    // (pass 1) before their short last chunks (pass 2)
+    for (int pass = 0; pass < 3; pass++)
         for (int j = 0; j < njobs; j++) {
             const JobDev& jd = p.jobs[j];
             if ((jd.mtq > 1) != (pass == 0)) continue;
             const int nb = jd.mtq > 1 ? ceil_div(jd.mtq, 4) : 1, per = jd.mtq > 1 ? 4 : 1;
+            const int nfull = ceil_div(jd.past + jd.n, ctx->geom.page) / ctx->ppw;
+            const int c0 = pass == 2 ? nfull : 0, c1 = pass == 1 ? nfull : jd.nchunk;
             for (int h = 0; h < ctx->geom.nKV; h++)
-                for (int c = 0; c < jd.nchunk; c++)
+                for (int c = c0; c < c1; c++)
                     for (int b = 0; b < nb; b++)
                         for (int q = 0; q < per; q++) {
                             const int mt = per * b + q;

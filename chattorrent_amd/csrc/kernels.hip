@@ -2485,7 +2485,8 @@ void launch_ids_col0(hipStream_t st, const uint32_t* ids, int rows, int stride, 
 // holds the jobs of several m-tiles first, each (kv head, chunk) as blocks of
 // four m-tiles (padded with mt = -1), so one workgroup's four waves read the
 // same pages together and the pages come from HBM once; then the jobs of
-// one m-tile, chunk by chunk.
+// one m-tile: first every chunk of ppw pages, then the last, shorter chunks,
+// so the blocks a launch hands out last are the short ones (k_attn).
 constexpr int PACK_THREADS = 256;
 
 __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict__ in, int njobs, int step,
@@ -2494,7 +2495,7 @@ __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict
                                                        int32_t* __restrict__ head_rows, int32_t* __restrict__ cwg) {
     __shared__ int32_t s_row0[PACK_MAX_JOBS], s_item0[PACK_MAX_JOBS], s_cwg0[PACK_MAX_JOBS],
         s_qp0[PACK_MAX_JOBS], s_head0[PACK_MAX_JOBS], s_mtq[PACK_MAX_JOBS], s_nch[PACK_MAX_JOBS],
-        s_pos0[PACK_MAX_JOBS];
+        s_pos0[PACK_MAX_JOBS], s_posb[PACK_MAX_JOBS];
     for (int j = threadIdx.x; j < njobs; j += blockDim.x) {
         const int n = in[j].n, tact = in[j].past + step + n;
         s_mtq[j] = (n * g.group + 15) / 16;
@@ -2519,10 +2520,16 @@ __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict
             qp += g.nKV * s_mtq[j] * g.ng * 128;
             head += g.head ? in[j].sampled : 0;
         }
+        // one m-tile: the full chunks, then the short last ones
         for (int j = 0; j < njobs; j++)
             if (s_mtq[j] == 1) {
                 s_pos0[j] = pos;
-                pos += g.nKV * s_nch[j];
+                pos += g.nKV * (((in[j].past + step + in[j].n + g.page - 1) / g.page) / g.ppw);
+            }
+        for (int j = 0; j < njobs; j++)
+            if (s_mtq[j] == 1) {
+                s_posb[j] = pos;
+                pos += g.nKV * ((((in[j].past + step + in[j].n + g.page - 1) / g.page) % g.ppw) != 0);
             }
     }
     __syncthreads();
@@ -2545,11 +2552,12 @@ __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict
             jobs[j] = jd;
         }
         if (mtq == 1) {
+            const int nfull = ((past + pj.n + g.page - 1) / g.page) / g.ppw;
             for (int x = threadIdx.x; x < g.nKV * nch; x += blockDim.x) {
                 const int c = x % nch, h = x / nch;
                 const int idx = s_item0[j] + x;   // (kv head, m-tile 0, chunk)
-                items[s_pos0[j] + x] = AttnItem{pj.slot, past, pj.n, 0, s_qp0[j] + (h * g.ng) * 128, idx * part, h,
-                                                c * g.ppw};
+                items[c < nfull ? s_pos0[j] + h * nfull + c : s_posb[j] + h] =
+                    AttnItem{pj.slot, past, pj.n, 0, s_qp0[j] + (h * g.ng) * 128, idx * part, h, c * g.ppw};
             }
         } else {
             // (kv head, chunk, block of 4 m-tiles, m-tile): a block is one workgroup
