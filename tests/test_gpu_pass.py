@@ -6,6 +6,10 @@ Bars: greedy ids identical (with the top-1/top-2
 margin reported for the near-tie case); logits within 1e-2 abs; the f16
 residual within 2 f16 ulp; packing, page indices and batch invariance
 bit-exact."""
+import json
+import os
+import warnings
+
 import numpy as np
 import pytest
 
@@ -29,6 +33,23 @@ def _setup(gpu, d, contexts, n_max=1024, t_max=64, extra_slots=1):
             c.fill_random_kv(s, T, SEED, s + 1)
             om.fill_random_kv(s, T, SEED, s + 1)
     return c, om
+
+
+def _report(name, rec):
+    """A measured distribution, as a warning and, when gpurun_out/ exists,
+    in gpurun_out/pass_parity.json."""
+    warnings.warn(f"{name}: " + json.dumps(rec), stacklevel=2)
+    out = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "gpurun_out")
+    if os.path.isdir(out):
+        path = os.path.join(out, "pass_parity.json")
+        try:
+            with open(path) as f:
+                allr = json.load(f)
+        except (OSError, ValueError):
+            allr = {}
+        allr[name] = rec
+        with open(path, "w") as f:
+            json.dump(allr, f, indent=1)
 
 
 def _ids(n, vocab, salt):
@@ -103,6 +124,7 @@ def test_decode_step_matches_oracle(smol):
     # by an ulp and sit on a rounding boundary (then by one code).
     D, nKV = d["head_dim"], d["n_kv_heads"]
     same = total = 0
+    worst_scale = 0.0
     for layer in range(1):
         for which in (0, 1):
             for j in jobs:
@@ -114,8 +136,12 @@ def test_decode_step_matches_oracle(smol):
                     assert np.abs(gc - wc).max() <= 1
                     gs, ws = g[:, D // 4:].view(np.float32), w[:, D // 4:].view(np.float32)
                     assert np.allclose(gs, ws, rtol=1e-5, atol=0)
+                    worst_scale = max(worst_scale, float((np.abs(gs - ws) / np.abs(ws)).max()))
                     same += int((gc == wc).sum())
                     total += gc.size
+    _report("block-0 new K/V rows, SmolLM2 shape, 4 jobs", {
+        "codes": total, "codes_equal": same, "codes_off_by_one": total - same,
+        "frac_equal": same / total, "scale_max_rel_diff": worst_scale})
     assert same / total > 0.99
 
 
@@ -131,21 +157,34 @@ def test_hidden_rows_within_two_f16_ulp_per_block(smol):
     after = []
     om.pass_(jobs, head=False, capture=lambda layer, x: after.append(L.to_f16(x.copy())))
     entry = c.step(jobs, at=0, to=1)                       # the rounded embedding rows
+    per_block = []
     for b in range(d["n_layer"]):
         hj = [dict(j, ids=None, hidden=entry[i:i + 1]) for i, j in enumerate(jobs)]
         got = c.step(hj, at=b + 1, to=b + 2)
         steps = _ulps_at_scale(got, after[b], entry)
+        own = _f16_ulp_diff(got, after[b])
+        per_block.append((int(steps.max()), float((own == 0).mean()), float((own <= 1).mean()), int(own.max())))
         assert steps.max() <= 2, (b, steps.max())
-        assert (_f16_ulp_diff(got, after[b]) <= 1).mean() > 0.99   # and nearly all within one step of themselves
+        assert (own <= 1).mean() > 0.99   # and nearly all within one step of themselves
         entry = after[b]                                   # the next block gets the oracle's rows
     # and the whole pass end to end stays close (one-step flips compound through blocks):
     # nearly every element within 2 f16 steps of itself, and every element within
     # 16 f16 steps at its row's RMS (a wrong channel or row would be off by far more)
     full = c.step(jobs, at=0, to=d["n_layer"] + 1)
-    assert (_f16_ulp_diff(full, after[-1]) <= 2).mean() > 0.97
+    e2e = _f16_ulp_diff(full, after[-1])
     g, w = L.from_f16(full).astype(np.float64), L.from_f16(after[-1]).astype(np.float64)
     rms = np.sqrt((w * w).mean(axis=1, keepdims=True))
     worst = float((np.abs(g - w) / _f16_ulp(np.maximum(np.abs(w), rms))).max())
+    _report("hidden rows, SmolLM2 shape, 4 jobs", {
+        "blocks": len(per_block),
+        "per_block_max_steps_at_scale": max(x[0] for x in per_block),
+        "per_block_min_frac_equal": min(x[1] for x in per_block),
+        "per_block_min_frac_within_one_own_step": min(x[2] for x in per_block),
+        "per_block_max_own_steps": max(x[3] for x in per_block),
+        "end_to_end_frac_equal": float((e2e == 0).mean()),
+        "end_to_end_frac_within_two_own_steps": float((e2e <= 2).mean()),
+        "end_to_end_max_steps_at_row_rms": worst})
+    assert (e2e <= 2).mean() > 0.97
     assert worst <= 16, worst
 
 
