@@ -139,9 +139,12 @@ __device__ static inline void split_hilo(float x, _Float16& hi, _Float16& lo) {
 // v_cvt_pkrtz saves two instructions but biases every lo toward zero, and the
 // bias adds up over a long softmax sum.)
 __device__ static inline void split_hilo2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    typedef float f2_t __attribute__((ext_vector_type(2)));
     asm("" : "+v"(x0), "+v"(x1));
-    const half2_t h = {(_Float16)x0, (_Float16)x1};
-    const half2_t l = {(_Float16)(x0 - (float)h[0]), (_Float16)(x1 - (float)h[1])};
+    const f2_t x = {x0, x1};
+    const half2_t h = __builtin_convertvector(x, half2_t);   // one packed conversion
+    const f2_t hb = __builtin_convertvector(h, f2_t);        // back from the packed halves
+    const half2_t l = __builtin_convertvector(x - hb, half2_t);
     hi = __builtin_bit_cast(uint32_t, h);
     lo = __builtin_bit_cast(uint32_t, l);
 }

@@ -203,7 +203,8 @@ void launch_resid_norm(hipStream_t st, float* x, const int32_t* rows, const floa
 // of workgroups hand out their last blocks; seq counts the launches.
 struct AttnSched {
     uint32_t* ctr = nullptr;   // 2 counters
-    int seq = 0, ncu = 0;
+    uint32_t seq = 0;
+    int ncu = 0;
 };
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const uint4* Qp,
                   const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,

@@ -1960,19 +1960,19 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
 
 // Work items go to waves in workgroups of four (item 4b + w to wave w of
 // block b). Workgroup i takes block i; with `dyn` set, it then takes blocks
-// gridDim.x, gridDim.x + 1, ... from the counter ctr[seq & 1] as it finishes
+// gridDim.x, gridDim.x + 1, ... from the counter ctr[par] as it finishes
 // each (launch_attn sets it for launches a little over one round of
 // resident workgroups: dispatch hands a pending workgroup to a fixed XCD, so
 // the few blocks past the first round would wait for that XCD's slowest
 // workgroups). Each launch clears the counter of the next launch on its
-// stream, ctr[(seq + 1) & 1]; the one it counts with was cleared by the
+// stream, ctr[par ^ 1]; the one it counts with was cleared by the
 // launch before it.
 template <int NG>
 __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __restrict__ items, int nitems,
                                                  const uint4* __restrict__ Qp,
                                                  const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
                                                  const uint32_t* __restrict__ page_table, KVGeom g, int group, int ppw,
-                                                 float* __restrict__ part, uint32_t* __restrict__ ctr, int seq,
+                                                 float* __restrict__ part, uint32_t* __restrict__ ctr, int par,
                                                  int dyn) {
     // per wave, the current page's K and V scale blocks (64 tokens x NG groups, f32)
     constexpr int SCL = NG > 4 ? NG / 4 : 1;
@@ -1981,7 +1981,7 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
     __shared__ int s_blk;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (blockIdx.x == 0 && threadIdx.x == 0)
-        __hip_atomic_store(&ctr[(seq + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&ctr[par ^ 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int nblk = (nitems + 3) / 4;
     for (int blk = blockIdx.x;;) {
         const int wid = blk * 4 + wv;
@@ -1992,7 +1992,7 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
         }
         if (!dyn) break;   // no barriers then: a finished wave may leave
         __syncthreads();
-        if (threadIdx.x == 0) s_blk = (int)gridDim.x + (int)atomicAdd(&ctr[seq & 1], 1u);
+        if (threadIdx.x == 0) s_blk = (int)gridDim.x + (int)atomicAdd(&ctr[par], 1u);
         __syncthreads();
         blk = s_blk;
         if (blk >= nblk) break;
@@ -2009,16 +2009,16 @@ void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const uint4*
     // with more, dispatch's own rounds balance them
     const int dyn = nblk > cap && 2 * nblk <= 3 * cap;
     const int blocks = dyn ? cap : nblk;
-    const int seq = sc.seq++;
+    const int par = (int)(sc.seq++ & 1u);
     if (g.ng == 8)
         hipLaunchKernelGGL(k_attn<8>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
-                     group, ppw, part, sc.ctr, seq, dyn);
+                     group, ppw, part, sc.ctr, par, dyn);
     else if (g.ng == 4)
         hipLaunchKernelGGL(k_attn<4>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
-                     group, ppw, part, sc.ctr, seq, dyn);
+                     group, ppw, part, sc.ctr, par, dyn);
     else
         hipLaunchKernelGGL(k_attn<2>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
-                     group, ppw, part, sc.ctr, seq, dyn);
+                     group, ppw, part, sc.ctr, par, dyn);
     CHECK_LAUNCH();
 }
 
