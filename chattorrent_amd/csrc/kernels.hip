@@ -1837,18 +1837,30 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
     };
     // One page. Its scale blocks arrived in kst/vst during the previous page;
     // they go to this wave's LDS slice first (a wave's LDS accesses run in
-    // order, so the previous page's reads of the slice are done).
+    // order, so the previous page's reads of the slice are done). The V
+    // scales of tokens past the job's are another session's stale values
+    // (even NaN): they go in as zero, so p * s is zero for every token whose
+    // p is (a masked token's p is exp2(-inf) = +0, every scale of a visible
+    // token is finite and positive).
     auto page = [&](int p) {
         // the last page reloads itself instead of branching (an L2 hit)
         const int pn = p + 1 < p1 ? p + 1 : p;
 #pragma unroll
         for (int q = 0; q < SCL; q++) {
             *(u32x4*)&ksl_w[256 * q + lane * 4] = kst[q];
-            *(u32x4*)&vsl_w[256 * q + lane * 4] = vst[q];
+            u32x4 v = vst[q];
+            if (p * 64 + 64 > T_act) {
+                // LDS element 256q + 4 lane + e holds V position v = 16 jj + 4 (lane & 3) + e,
+                // jj = ((256q + 4 lane) >> 4) & 3: the page's token vpos(v) = 16 (lane & 3) + 4 jj + e
+                const int t0 = p * 64 + 16 * (lane & 3) + 4 * (((256 * q + lane * 4) >> 4) & 3);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (t0 + e >= T_act) v[e] = 0u;
+            }
+            *(u32x4*)&vsl_w[256 * q + lane * 4] = v;
         }
         {
             float pr[4][4];
-            uint32_t keep[4][4];   // all ones for a visible token, zero for a masked one
             float pm = -INFINITY;
 #pragma unroll
             for (int tt = 0; tt < 4; tt++) {
@@ -1873,7 +1885,6 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
                 for (int r = 0; r < 4; r++) {
                     const int tok = p * 64 + tt * 16 + 4 * j4 + r;
                     const bool ok = tok < T_act && tok <= lim;
-                    keep[tt][r] = ok ? 0xffffffffu : 0u;
                     pr[tt][r] = ok ? acc[r] * score_scale : -INFINITY;
                     pm = fmaxf(pm, pr[tt][r]);
                 }
@@ -1914,11 +1925,8 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
 #pragma unroll
                     for (int ii = 0; ii < 8; ii += 2) {
                         const int tt = 2 * ks + (ii >> 2), r = ii & 3;
-                        // a masked token's scale may be another session's stale value (even
-                        // NaN): its product is cleared by bits, with no branch
-                        const float p0 = __uint_as_float(__float_as_uint(pr[tt][r] * sv[4 * tt + r]) & keep[tt][r]);
-                        const float p1 =
-                            __uint_as_float(__float_as_uint(pr[tt][r + 1] * sv[4 * tt + r + 1]) & keep[tt][r + 1]);
+                        const float p0 = pr[tt][r] * sv[4 * tt + r];
+                        const float p1 = pr[tt][r + 1] * sv[4 * tt + r + 1];
                         uint32_t h, l;
                         split_hilo2(p0, p1, h, l);
                         phw[ii >> 1] = h;

@@ -235,3 +235,32 @@ def test_attend_vs_oracle(gpu):
             assert err <= 2e-5 * max(1.0, np.abs(want).max()), (base["hidden"], tokens, n, err)
         finally:
             c.close()
+
+
+def test_attend_ignores_stale_rows_past_the_context(gpu):
+    """The pool rows past a job's tokens hold whatever an earlier session left
+    there, NaN and inf included (web/model/kernels.js:1140-1310 never reads
+    them: its loops stop at the context length). Poisoning every K and V
+    row after the attended tokens, codes and scales, leaves the output
+    bitwise unchanged: decode rows and a causal verify run whose last page
+    is partly filled."""
+    for base, tokens, n in [(configs.M27B, 700, 1), (configs.M27B, 300, 8), (D256, 520, 6)]:
+        d = configs.with_layers(base, 1)
+        c = _ctx(gpu, d, n_max=1024, t_max=64, slots=2)
+        try:
+            end = (tokens + n + 63) // 64 * 64 + 40          # rows into the next page too
+            c.fill_random_kv(1, end, 11, 3)
+            D, nH, nKV = d["head_dim"], d["n_heads"], d["n_kv_heads"]
+            q = np.random.default_rng(tokens + n).standard_normal((n, nH * D)).astype(np.float32)
+            clean = c.op_attend(0, 1, q, tokens)
+            bad = np.empty((end - tokens - n, D // 4 + D // 32), np.uint32)
+            bad[:, :D // 4] = 0x7f7f7f7f                    # codes at their largest
+            bad[:, D // 4:] = np.array([0x7fc00000, 0x7f800000, 0xff800000, 0x7f7fffff] * D, np.uint32)[:D // 32]
+            for which in (0, 1):
+                for h in range(nKV):
+                    c.write_kv(0, which, 1, h, tokens + n, bad)
+            poisoned = c.op_attend(0, 1, q, tokens)
+            assert np.isfinite(poisoned).all()
+            assert np.array_equal(clean.view(np.uint32), poisoned.view(np.uint32)), (tokens, n)
+        finally:
+            c.close()
