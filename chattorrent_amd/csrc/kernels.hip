@@ -2484,8 +2484,7 @@ void launch_ids_col0(hipStream_t st, const uint32_t* ids, int rows, int stride, 
 
 // ================================================================ packing ===
 // One workgroup: per-job counts in parallel, their prefix sums in job order
-// (one thread; a pass holds at most a few hundred jobs), then every table
-// written by all threads. A job of n rows at past p needs ceil(n*group/16)
+// (pack_exscan), then every table written by all threads. A job of n rows at past p needs ceil(n*group/16)
 // Q m-tiles, ceil(ceil((p+n)/64)/ppw) chunks of pages per (kv head, m-tile),
 // one combine triple per (kv head, m-tile), and nKV*mtq*ng*128 Q-operand
 // units; each work item's softmax partial takes 16*(D+4) floats, at the
@@ -2497,49 +2496,82 @@ void launch_ids_col0(hipStream_t st, const uint32_t* ids, int rows, int stride, 
 // so the blocks a launch hands out last are the short ones (k_attn).
 constexpr int PACK_THREADS = 256;
 
+static_assert(PACK_MAX_JOBS <= 4 * PACK_THREADS, "pack_exscan takes four jobs a thread");
+// Exclusive prefix sums of v[0 .. n) in place, n <= 4 * PACK_THREADS, over the
+// whole workgroup (four consecutive values a thread, a wave scan, the waves'
+// totals in order); `total` = the sum of all n. part: PACK_THREADS / 64 ints.
+__device__ static void pack_exscan(int32_t* v, int n, int32_t* part, int& total) {
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    int a[4], s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        a[i] = 4 * t + i < n ? v[4 * t + i] : 0;
+        s += a[i];
+    }
+    int x = s;   // inclusive scan of the threads' sums across the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) part[w] = x;
+    __syncthreads();
+    int off = 0;
+    total = 0;
+#pragma unroll
+    for (int k = 0; k < PACK_THREADS / 64; k++) {
+        off += k < w ? part[k] : 0;
+        total += part[k];
+    }
+    int run = off + x - s;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (4 * t + i < n) v[4 * t + i] = run;
+        run += a[i];
+    }
+    __syncthreads();   // part is reused by the next scan
+}
+
 __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict__ in, int njobs, int step,
                                                        PackGeom g, JobDev* __restrict__ jobs,
                                                        AttnItem* __restrict__ items, int32_t* __restrict__ row_job,
                                                        int32_t* __restrict__ head_rows, int32_t* __restrict__ cwg) {
     __shared__ int32_t s_row0[PACK_MAX_JOBS], s_item0[PACK_MAX_JOBS], s_cwg0[PACK_MAX_JOBS],
         s_qp0[PACK_MAX_JOBS], s_head0[PACK_MAX_JOBS], s_mtq[PACK_MAX_JOBS], s_nch[PACK_MAX_JOBS],
-        s_pos0[PACK_MAX_JOBS], s_posb[PACK_MAX_JOBS];
+        s_pos0[PACK_MAX_JOBS], s_posf[PACK_MAX_JOBS], s_posb[PACK_MAX_JOBS], s_part[PACK_THREADS / 64];
+    // each job's counts, then their exclusive prefix sums in job order
     for (int j = threadIdx.x; j < njobs; j += blockDim.x) {
         const int n = in[j].n, tact = in[j].past + step + n;
-        s_mtq[j] = (n * g.group + 15) / 16;
-        s_nch[j] = ((tact + g.page - 1) / g.page + g.ppw - 1) / g.ppw;
+        const int mtq = (n * g.group + 15) / 16, pages = (tact + g.page - 1) / g.page;
+        const int nch = (pages + g.ppw - 1) / g.ppw;
+        s_mtq[j] = mtq;
+        s_nch[j] = nch;
+        s_row0[j] = n;
+        s_item0[j] = g.nKV * mtq * nch;
+        s_cwg0[j] = g.nKV * mtq;
+        s_qp0[j] = g.nKV * mtq * g.ng * 128;
+        s_head0[j] = g.head ? in[j].sampled : 0;
+        // the item list: jobs of several m-tiles first, then the one-m-tile jobs'
+        // full chunks, then their short last chunks
+        s_pos0[j] = mtq > 1 ? g.nKV * nch * 4 * ((mtq + 3) / 4) : 0;
+        s_posf[j] = mtq > 1 ? 0 : g.nKV * (pages / g.ppw);
+        s_posb[j] = mtq > 1 ? 0 : g.nKV * (pages % g.ppw != 0);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int row = 0, item = 0, c = 0, qp = 0, head = 0, pos = 0;
-        for (int j = 0; j < njobs; j++) {
-            s_row0[j] = row;
-            s_item0[j] = item;
-            s_cwg0[j] = c;
-            s_qp0[j] = qp;
-            s_head0[j] = head;
-            if (s_mtq[j] > 1) {   // the jobs of several m-tiles first
-                s_pos0[j] = pos;
-                pos += g.nKV * s_nch[j] * 4 * ((s_mtq[j] + 3) / 4);
-            }
-            row += in[j].n;
-            item += g.nKV * s_mtq[j] * s_nch[j];
-            c += g.nKV * s_mtq[j];
-            qp += g.nKV * s_mtq[j] * g.ng * 128;
-            head += g.head ? in[j].sampled : 0;
+    int tot_multi, tot_full, unused;
+    pack_exscan(s_row0, njobs, s_part, unused);
+    pack_exscan(s_item0, njobs, s_part, unused);
+    pack_exscan(s_cwg0, njobs, s_part, unused);
+    pack_exscan(s_qp0, njobs, s_part, unused);
+    pack_exscan(s_head0, njobs, s_part, unused);
+    pack_exscan(s_pos0, njobs, s_part, tot_multi);
+    pack_exscan(s_posf, njobs, s_part, tot_full);
+    pack_exscan(s_posb, njobs, s_part, unused);
+    for (int j = threadIdx.x; j < njobs; j += blockDim.x)
+        if (s_mtq[j] == 1) {
+            s_pos0[j] = tot_multi + s_posf[j];
+            s_posb[j] += tot_multi + tot_full;
         }
-        // one m-tile: the full chunks, then the short last ones
-        for (int j = 0; j < njobs; j++)
-            if (s_mtq[j] == 1) {
-                s_pos0[j] = pos;
-                pos += g.nKV * (((in[j].past + step + in[j].n + g.page - 1) / g.page) / g.ppw);
-            }
-        for (int j = 0; j < njobs; j++)
-            if (s_mtq[j] == 1) {
-                s_posb[j] = pos;
-                pos += g.nKV * ((((in[j].past + step + in[j].n + g.page - 1) / g.page) % g.ppw) != 0);
-            }
-    }
     __syncthreads();
     const int part = 16 * (g.D + 4);
     for (int j = 0; j < njobs; j++) {
