@@ -188,7 +188,7 @@ hipError_t alloc_q(cc_ctx* ctx, QTensor& q, int N, int K) {
     q.K = K;
     q.Nt = ceil_div(ceil_div(N, 16), 2) * 2;   // tile pairs
     q.KU = ceil_div(K, 64);
-    q.P = lx_planes(q.KU);
+    q.P = lx_planes_for(N, K, ctx->ncu);
     return dalloc(ctx, &q.codes, (size_t)q.Nt * q.KU * (LX_REC / 2), &ctx->weight_bytes);
 }
 
@@ -621,7 +621,7 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
             HIPCHK(hipHostMalloc((void**)&ctx->h_chain, cb, hipHostMallocDefault));
         }
         if (ctx->head) {
-            ctx->head_planes = lx_planes(ceil_div(H, 64));
+            ctx->head_planes = lx_planes_for(d.vocab, H, ctx->ncu);   // the head tensor's own planes
             HIPCHK(dalloc(ctx, &ctx->logits, (size_t)ctx->head_planes * T * d.vocab * 4, &ctx->scratch_bytes));
             const size_t keys = (size_t)T * ceil_div(d.vocab, 4096) * TOPK_MAX;
             HIPCHK(dalloc(ctx, &ctx->tk_a, keys * 8, &ctx->scratch_bytes));
@@ -1781,7 +1781,7 @@ cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K, con
     q.K = K;
     q.Nt = ceil_div(ceil_div(N, 16), 2) * 2;
     q.KU = ceil_div(K, 64);
-    q.P = lx_planes(q.KU);
+    q.P = lx_planes_for(N, K, ctx->ncu);
     const int ng = ceil_div(K, 32);
     const int Mt = 2 * ceil_div(M, 32);
     const int sp = q.P;

@@ -6,7 +6,8 @@
 
 // q8 weight in matmul stream order. A tile is 16 rows x 64 columns of K (a
 // "unit"); tiles pair up (t, t^1). K units split into P planes, plane r
-// covering units [r*KU/P, (r+1)*KU/P) (at most LX_UNITS each). For each
+// covering units [r*KU/P, (r+1)*KU/P) (at most LX_UNITS each; P from
+// lx_planes_for when the tensor is allocated). For each
 // plane, then each tile pair, then each unit of the plane, one record of
 // LX_REC bytes:
 //   [nt*1024 + lane*16 + b]  code of W[16t + lane%16][64u + 32(b/8) + 8(lane/16) + b%8]
@@ -91,6 +92,7 @@ void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtile
 // add in plane order: w.P, or 1 when the matmul adds them itself.
 int gemm_planes(const QTensor& w, int M, int ncu);
 int lx_groups(const QTensor& w, int ncu);
+int lx_planes_for(int N, int K, int ncu);
 void launch_prep_rows(hipStream_t st, const float* x, int ldx, int M, int Mpad, int K, int KU,
                       uint4* Xp);
 void launch_fin_swiglu(hipStream_t st, const float* part, int splits, int M, int Mpad, int F,

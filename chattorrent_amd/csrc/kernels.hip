@@ -260,6 +260,19 @@ int lx_groups(const QTensor& w, int ncu) {
     return w.P * per;
 }
 
+// K planes of an N x K q8 tensor: the fewest the LDS allows (lx_planes),
+// doubled (up to 16, and to one unit a plane) while the workgroups the
+// matmul launches (planes x column groups, lx_groups) would fill fewer than
+// half the CUs. A small model's narrow matrices (30 tile pairs at
+// SmolLM2's q|k|v) otherwise leave most CUs idle; a 27B or 8B layer fills
+// them at the fewest planes and keeps those.
+int lx_planes_for(int N, int K, int ncu) {
+    const int KU = (K + 63) / 64, npairs = (N + 31) / 32;
+    int P = lx_planes(KU);
+    while (2 * P <= std::min(KU, 16) && 2LL * P * std::max(1, std::min(ncu / P, npairs)) <= ncu) P *= 2;
+    return P;
+}
+
 template <int MT>
 static void launch_lx(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, int ncu) {
     static bool attr = false;
