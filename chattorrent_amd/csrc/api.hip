@@ -288,6 +288,7 @@ struct StepPlan {
     // nitems: attention partials (job, kv head, m-tile, chunk); nlaunch: the
     // item list k_attn takes (blocks of m-tiles padded to 4)
     int T = 0, S = 0, nitems = 0, ncwg = 0, nlaunch = 0;
+    int multi = 0;   // a job of several Q m-tiles (attention's shared-page blocks)
     std::vector<JobDev> jobs;
     std::vector<AttnItem> items;
     std::vector<int32_t> row_job, plan, head_rows, cwg;
@@ -1017,6 +1018,7 @@ static void plan_jobs(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, b
     const int ng = ctx->geom.ng;
     size_t qp = 0;
     int row = 0, items = 0, cwg = 0, S = 0, nlaunch = 0;
+    p.multi = 0;
     for (int j = 0; j < njobs; j++) {
         JobDev& jd = p.jobs[j];
         jd.slot = jobs[j].slot;
@@ -1035,6 +1037,7 @@ static void plan_jobs(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, b
         items += ctx->geom.nKV * jd.mtq * jd.nchunk;
         nlaunch += ctx->geom.nKV * jd.nchunk * (jd.mtq > 1 ? 4 * ceil_div(jd.mtq, 4) : 1);
         cwg += ctx->geom.nKV * jd.mtq;
+        if (jd.mtq > 1) p.multi = 1;
         if (head) S += jobs[j].sampled;
         row += jd.n;
     }
@@ -1128,7 +1131,7 @@ struct PassMeta {
     const AttnItem* items = nullptr;
     const int32_t* row_job = nullptr;
     const int32_t* cwg = nullptr;
-    int njobs = 0, nitems = 0, ncwg = 0, nlaunch = 0;
+    int njobs = 0, nitems = 0, ncwg = 0, nlaunch = 0, multi = 0;
 };
 
 static RowScale row_scale_of(const cc_ctx* ctx) {
@@ -1161,7 +1164,7 @@ static void full_attn_half(cc_ctx* ctx, Layer& L, float* x, int T, int Mpad, con
     launch_fin_qkv(st, ctx->part, gemm_planes(L.qkv, T, ctx->ncu), T, pm.row_job, pm.jobs, nH, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
                    L.kpool, L.vpool, ctx->page_table, ctx->qp, rs, 1, 1, ex);
     launch_attn(st, pm.items, pm.nlaunch, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group,
-                ctx->ppw, ctx->apart, ctx->attn);
+                ctx->ppw, ctx->apart, pm.multi, ctx->attn);
     launch_attn_combine(st, pm.jobs, ctx->apart, ctx->geom, nH, ctx->group, L.o.KU, ctx->xp_o, nullptr, pm.cwg,
                         pm.ncwg, ctx->hybrid ? ctx->gbuf : nullptr);
     launch_gemm(st, L.o, ctx->xp_o, ctx->mt_alloc, ctx->part, T, ctx->ncu);
@@ -1206,6 +1209,7 @@ static void run_blocks(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, int
     pm.njobs = (int)p.jobs.size();
     pm.nitems = p.nitems;
     pm.nlaunch = p.nlaunch;
+    pm.multi = p.multi;
     pm.ncwg = p.ncwg;
     const RowScale rs = row_scale_of(ctx);
     const int KUH = ceil_div(H, 64);   // every block's first matmul reads K = hidden
@@ -1320,7 +1324,7 @@ static void prof_replay(cc_ctx* ctx, const StepPlan& p, const MetaLayout& ml, in
                     const Layer& L = ctx->layers[b - ctx->L0];
                     if (!L.kpool) continue;
                     launch_attn(st, ditems, p.nlaunch, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom,
-                                ctx->group, ctx->ppw, ctx->apart, ctx->attn);
+                                ctx->group, ctx->ppw, ctx->apart, p.multi, ctx->attn);
                 }
             });
         blocks(CC_K_O, &Layer::o, ctx->xp_o);
@@ -1754,6 +1758,7 @@ cc_status cc_mtp_draft(cc_ctx* ctx, int32_t slot, int32_t row, int32_t token, in
         pm.njobs = 1;
         pm.nitems = plans[k].nitems;
         pm.nlaunch = plans[k].nlaunch;
+        pm.multi = plans[k].multi;
         pm.ncwg = plans[k].ncwg;
         mtp_input(ctx, ids + k, ctx->mtp_in, 1);
         full_attn_half(ctx, ctx->mtpL, ctx->mx, 1, mpad_of(1), pm);
@@ -1980,7 +1985,7 @@ cc_status cc_op_attend(cc_ctx* ctx, int32_t layer, int32_t slot, const float* q,
     launch_fin_qkv(st, dr, 1, n, (const int32_t*)(ctx->d_meta + ml.row_job), dj, d.n_heads, ctx->group, ctx->geom,
                    ctx->tbl, ctx->rot, L.kpool, L.vpool, ctx->page_table, ctx->qp, RowScale{}, 1, 0);
     launch_attn(st, di, p.nlaunch, ctx->qp, L.kpool, L.vpool, ctx->page_table, ctx->geom, ctx->group, ctx->ppw,
-                 ctx->apart, ctx->attn);
+                 ctx->apart, p.multi, ctx->attn);
     launch_attn_combine(st, dj, ctx->apart, ctx->geom, d.n_heads, ctx->group, KU, dXp, dctx,
                          (const int32_t*)(ctx->d_meta + ml.cwg), p.ncwg);
     HIPCHK(hipStreamSynchronize(st));

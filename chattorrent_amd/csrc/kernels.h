@@ -210,7 +210,7 @@ struct AttnSched {
 };
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const uint4* Qp,
                   const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
-                  int ppw, float* part, AttnSched& sc);
+                  int ppw, float* part, int multi, AttnSched& sc);
 // `gate` (a hybrid checkpoint's, [rows][nH*D], or null): the output is
 // multiplied by sigmoid(gate) before it becomes the o_proj operand
 // (web/model/kernels.js:1822-1839 sigmoid_mul).

@@ -1979,6 +1979,224 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
 }
 
 
+// One block of a job of several m-tiles: its four waves hold m-tiles
+// 4b .. 4b+3 of one (job, kv head, chunk) (an m-tile past the job's is an
+// empty slot, mt < 0) and read the same pages. Each wave loads a quarter of
+// a page (K token tile w, V d-tiles w*DT/4 ..), dequantises it once into the
+// workgroup's LDS, and every wave's MFMAs read the fragments from there, so a
+// page is dequantised once instead of once per m-tile. One barrier a page;
+// the fragments are double-buffered (a wave past page p's barrier has
+// finished page p - 1, so page p + 1 may reuse that buffer). Every value and
+// every operation of a row is the one attn_item computes for it.
+template <int NG>
+__device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& it0, int wv,
+                                            const uint4* __restrict__ Qp, const uint8_t* __restrict__ kpool,
+                                            const uint8_t* __restrict__ vpool,
+                                            const uint32_t* __restrict__ page_table, const KVGeom& g, int group,
+                                            int ppw, float* __restrict__ part, u32x4* lds) {
+    constexpr int D = 32 * NG;
+    constexpr int DT = D / 16, DQ = DT / 4;
+    constexpr int SCL = NG > 4 ? NG / 4 : 1;
+    // LDS: K fragments [2][4 tt][NG gg][64], V fragments [2][DT][2 ks][64], then the
+    // K and V scale blocks [2][256 * SCL] floats each
+    u32x4* kf_s = lds;
+    u32x4* vf_s = kf_s + 2 * 4 * NG * 64;
+    float* ks_s = (float*)(vf_s + 2 * DT * 2 * 64);
+    float* vs_s = ks_s + 2 * 256 * SCL;
+    const int lane = threadIdx.x & 63, j4 = lane >> 4, l16 = lane & 15;
+    const int T_act = it0.past + it0.n;
+    const int R = it0.n * group;
+    const int npg = (T_act + 63) >> 6;
+    const int p0 = it0.p0;
+    const int p1 = min(npg, p0 + ppw);
+    const bool mine = it.mt >= 0;
+    const float score_scale = 1.4426950408889634f / sqrtf((float)D);
+
+    uint4 qh[NG], ql[NG];
+    if (mine) {
+        const size_t qb = (size_t)it.qb + lane;
+#pragma unroll
+        for (int gg = 0; gg < NG; gg++) {
+            qh[gg] = Qp[qb + (size_t)gg * 128];
+            ql[gg] = Qp[qb + (size_t)gg * 128 + 64];
+        }
+    }
+    const int rho = (mine ? it.mt : 0) * 16 + l16;
+    const int lim = mine && rho < R ? it0.past + rho / group : -1;
+    const uint32_t* pt = page_table + (size_t)it0.slot * g.max_pages;
+    const size_t hoff = (size_t)it0.kvh * g.blk;
+    const size_t pstride = (size_t)g.nKV * g.blk;
+    const uint32_t pgv = lane < p1 - p0 ? pt[p0 + lane] : 0u;
+    auto page_rsrc = [&](const uint8_t* pool, int p) {
+        const uint32_t pg = __builtin_amdgcn_readlane(pgv, p - p0);
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(pool + (size_t)pg * pstride + hoff), 0, g.blk, 0x00020000);
+    };
+    const int vk = l16 * D + (D / 4) * j4;
+    const int vv = j4 * D * 16 + l16 * 16;
+    int vso[SCL];
+#pragma unroll
+    for (int q = 0; q < SCL; q++) {
+        const int e = 256 * q + lane * 4, b = e >> 6, jb = (e >> 4) & 3;
+        vso[q] = 4 * ((jb * NG + b) * 16 + (e & 15));
+    }
+
+    float mrow = -INFINITY, lsum = 0.0f;
+    float4_t o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // this wave's quarter of the next page: K token tile wv, V d-tiles wv*DQ .. +DQ-1,
+    // and (waves 0 and 1) the K or V scale block
+    u32x4 kc[NG / 2], vc[DQ], sc[SCL];
+    auto load = [&](int p) {
+        const auto rk = page_rsrc(kpool, p), rv = page_rsrc(vpool, p);
+#pragma unroll
+        for (int q = 0; q < NG / 2; q++) kc[q] = __builtin_amdgcn_raw_buffer_load_b128(rk, vk, wv * 16 * D + 16 * q, 0);
+#pragma unroll
+        for (int i = 0; i < DQ; i++) vc[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, (wv * DQ + i) * 256, 0);
+        if (wv == 0) {
+#pragma unroll
+            for (int q = 0; q < SCL; q++) sc[q] = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16, 64 * D + 1024 * q, 0);
+        } else if (wv == 1) {
+#pragma unroll
+            for (int q = 0; q < SCL; q++) sc[q] = __builtin_amdgcn_raw_buffer_load_b128(rv, vso[q], 64 * D, 0);
+        }
+    };
+    if (p0 < p1) load(p0);
+    for (int p = p0; p < p1; p++) {
+        const int B = (p - p0) & 1;
+        u32x4* kf = kf_s + B * 4 * NG * 64;
+        u32x4* vf = vf_s + B * DT * 2 * 64;
+        float* ksl = ks_s + B * 256 * SCL;
+        float* vsl = vs_s + B * 256 * SCL;
+#pragma unroll
+        for (int q = 0; q < NG / 2; q++) {
+            kf[(wv * NG + 2 * q) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(kc[q][0], kc[q][1]));
+            kf[(wv * NG + 2 * q + 1) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(kc[q][2], kc[q][3]));
+        }
+#pragma unroll
+        for (int i = 0; i < DQ; i++) {
+            vf[((wv * DQ + i) * 2) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(vc[i][0], vc[i][1]));
+            vf[((wv * DQ + i) * 2 + 1) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(vc[i][2], vc[i][3]));
+        }
+        if (wv == 0) {
+#pragma unroll
+            for (int q = 0; q < SCL; q++) *(u32x4*)&ksl[256 * q + lane * 4] = sc[q];
+        } else if (wv == 1) {
+#pragma unroll
+            for (int q = 0; q < SCL; q++) {
+                u32x4 v = sc[q];
+                if (p * 64 + 64 > T_act) {   // stale scales past the job's tokens go in as zero
+                    const int t0 = p * 64 + 16 * (lane & 3) + 4 * (((256 * q + lane * 4) >> 4) & 3);
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (t0 + e >= T_act) v[e] = 0u;
+                }
+                *(u32x4*)&vsl[256 * q + lane * 4] = v;
+            }
+        }
+        __syncthreads();
+        if (p + 1 < p1) load(p + 1);   // the registers are free: the next page is on its way
+        if (!mine) continue;
+        float pr[4][4];
+        float pm = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++) {
+            float ks[4 * NG];
+#pragma unroll
+            for (int q = 0; q < NG; q++) {
+                const float4 f = *(const float4*)&ksl[(tt * 16 + 4 * j4) * NG + 4 * q];
+                ks[4 * q] = f.x; ks[4 * q + 1] = f.y; ks[4 * q + 2] = f.z; ks[4 * q + 3] = f.w;
+            }
+            float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int gg = 0; gg < NG; gg++) {
+                const half8_t kfr = __builtin_bit_cast(half8_t, kf[(tt * NG + gg) * 64 + lane]);
+                float4_t pp = {0.f, 0.f, 0.f, 0.f};
+                pp = mfma16x16x32(kfr, __builtin_bit_cast(half8_t, qh[gg]), pp);
+                pp = mfma16x16x32(kfr, __builtin_bit_cast(half8_t, ql[gg]), pp);
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(ks[r * NG + gg], pp[r], acc[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int tok = p * 64 + tt * 16 + 4 * j4 + r;
+                const bool ok = tok < T_act && tok <= lim;
+                pr[tt][r] = ok ? acc[r] * score_scale : -INFINITY;
+                pm = fmaxf(pm, pr[tt][r]);
+            }
+        }
+        pm = fmaxf(pm, __shfl_xor(pm, 16));
+        pm = fmaxf(pm, __shfl_xor(pm, 32));
+        const float mnew = fmaxf(mrow, pm);
+        const float alpha = mrow == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrow - mnew);
+        lsum *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[dt][r] *= alpha;
+        const float msub = mnew == -INFINITY ? 0.0f : mnew;
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float e = __builtin_amdgcn_exp2f(pr[tt][r] - msub);
+                pr[tt][r] = e;
+                lsum += e;
+            }
+#pragma unroll
+        for (int b = 0; b < NG; b++) {
+            float sv[16];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 f = *(const float4*)&vsl[b * 64 + 16 * j4 + 4 * q];
+                sv[4 * q] = f.x; sv[4 * q + 1] = f.y; sv[4 * q + 2] = f.z; sv[4 * q + 3] = f.w;
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                u32x4 phw, plw;
+#pragma unroll
+                for (int ii = 0; ii < 8; ii += 2) {
+                    const int tt = 2 * ks + (ii >> 2), r = ii & 3;
+                    uint32_t h, l;
+                    split_hilo2(pr[tt][r] * sv[4 * tt + r], pr[tt][r + 1] * sv[4 * tt + r + 1], h, l);
+                    phw[ii >> 1] = h;
+                    plw[ii >> 1] = l;
+                }
+                const half8_t ph = __builtin_bit_cast(half8_t, phw), pl = __builtin_bit_cast(half8_t, plw);
+#pragma unroll
+                for (int dd = 0; dd < 2; dd++) {
+                    const int dt = 2 * b + dd;
+                    const half8_t vfr = __builtin_bit_cast(half8_t, vf[(dt * 2 + ks) * 64 + lane]);
+                    o[dt] = mfma16x16x32(vfr, ph, o[dt]);
+                    o[dt] = mfma16x16x32(vfr, pl, o[dt]);
+                }
+            }
+        }
+        mrow = mnew;
+    }
+    if (!mine) return;
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if (rho < R) {
+        float* dst = part + it.part + (size_t)l16 * (D + 4);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) *(float4_t*)(dst + 4 + dt * 16 + 4 * j4) = o[dt];
+        if (j4 == 0) *(float2*)dst = make_float2(mrow, lsum);
+    }
+}
+
+// LDS of a k_attn workgroup: the four waves' scale slices for one-m-tile
+// items (8 KiB per 4 groups), or a block's shared fragments and scales
+// (attn_block4) when the launch holds jobs of several m-tiles (`multi`).
+template <int NG>
+constexpr size_t attn_lds_bytes() {
+    constexpr size_t SCL = NG > 4 ? NG / 4 : 1, DT = 2 * NG;
+    constexpr size_t single = 8 * 256 * SCL * 4;
+    constexpr size_t block = (2 * 4 * NG * 64 + 2 * DT * 2 * 64) * 16 + 2 * 2 * 256 * SCL * 4;
+    return single > block ? single : block;
+}
+
 // Work items go to waves in workgroups of four (item 4b + w to wave w of
 // block b). Workgroup i takes block i; with `dyn` set, it then takes blocks
 // gridDim.x, gridDim.x + 1, ... from the counter ctr[par] as it finishes
@@ -1994,11 +2212,11 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
                                                  const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
                                                  const uint32_t* __restrict__ page_table, KVGeom g, int group, int ppw,
                                                  float* __restrict__ part, uint32_t* __restrict__ ctr, int par,
-                                                 int dyn) {
-    // per wave, the current page's K and V scale blocks (64 tokens x NG groups, f32)
+                                                 int dyn, int multi) {
+    // per wave, the current page's K and V scale blocks (64 tokens x NG groups,
+    // f32), or a block's shared fragments: attn_lds_bytes<NG>() of dynamic LDS
     constexpr int SCL = NG > 4 ? NG / 4 : 1;
-    __shared__ __attribute__((aligned(16))) float ksl[4][256 * SCL];
-    __shared__ __attribute__((aligned(16))) float vsl[4][256 * SCL];
+    extern __shared__ __attribute__((aligned(1024))) u32x4 lds[];
     __shared__ int s_blk;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (blockIdx.x == 0 && threadIdx.x == 0)
@@ -2006,10 +2224,15 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
     const int nblk = (nitems + 3) / 4;
     for (int blk = blockIdx.x;;) {
         const int wid = blk * 4 + wv;
-        if (wid < nitems) {
+        const AttnItem it0 = items[blk * 4];
+        if (multi && it0.n * group > 16) {
+            // a job of several m-tiles: the block is one chunk's m-tiles (mt < 0 pads it)
+            attn_block4<NG>(items[wid], it0, wv, Qp, kpool, vpool, page_table, g, group, ppw, part, lds);
+        } else if (wid < nitems) {
             const AttnItem it = items[wid];
-            if (it.mt >= 0)   // mt < 0: a slot that pads a workgroup of m-tiles
-                attn_item<NG>(it, Qp, kpool, vpool, page_table, g, group, ppw, part, ksl[wv], vsl[wv]);
+            if (it.mt >= 0)
+                attn_item<NG>(it, Qp, kpool, vpool, page_table, g, group, ppw, part, (float*)lds + wv * 256 * SCL,
+                              (float*)lds + (4 + wv) * 256 * SCL);
         }
         if (!dyn) break;   // no barriers then: a finished wave may leave
         __syncthreads();
@@ -2022,7 +2245,7 @@ __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __
 
 void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const uint4* Qp,
                  const uint8_t* kpool, const uint8_t* vpool, const uint32_t* page_table, const KVGeom& g, int group,
-                 int ppw, float* part, AttnSched& sc) {
+                 int ppw, float* part, int multi, AttnSched& sc) {
     if (nitems <= 0) return;
     const int nblk = (nitems + 3) / 4;
     const int cap = sc.ncu * (g.ng == 8 ? 1 : 2);   // workgroups resident at once
@@ -2031,15 +2254,22 @@ void launch_attn(hipStream_t st, const AttnItem* items, int nitems, const uint4*
     const int dyn = nblk > cap && 2 * nblk <= 3 * cap;
     const int blocks = dyn ? cap : nblk;
     const int par = (int)(sc.seq++ & 1u);
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute((const void*)k_attn<8>, hipFuncAttributeMaxDynamicSharedMemorySize, attn_lds_bytes<8>());
+        (void)hipFuncSetAttribute((const void*)k_attn<4>, hipFuncAttributeMaxDynamicSharedMemorySize, attn_lds_bytes<4>());
+        (void)hipFuncSetAttribute((const void*)k_attn<2>, hipFuncAttributeMaxDynamicSharedMemorySize, attn_lds_bytes<2>());
+    }
     if (g.ng == 8)
-        hipLaunchKernelGGL(k_attn<8>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
-                     group, ppw, part, sc.ctr, par, dyn);
+        hipLaunchKernelGGL(k_attn<8>, dim3(blocks), dim3(256), multi ? attn_lds_bytes<8>() : 8 * 256 * 2 * 4, st, items, nitems, Qp, kpool, vpool, page_table, g,
+                     group, ppw, part, sc.ctr, par, dyn, multi);
     else if (g.ng == 4)
-        hipLaunchKernelGGL(k_attn<4>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
-                     group, ppw, part, sc.ctr, par, dyn);
+        hipLaunchKernelGGL(k_attn<4>, dim3(blocks), dim3(256), multi ? attn_lds_bytes<4>() : 8 * 256 * 1 * 4, st, items, nitems, Qp, kpool, vpool, page_table, g,
+                     group, ppw, part, sc.ctr, par, dyn, multi);
     else
-        hipLaunchKernelGGL(k_attn<2>, dim3(blocks), dim3(256), 0, st, items, nitems, Qp, kpool, vpool, page_table, g,
-                     group, ppw, part, sc.ctr, par, dyn);
+        hipLaunchKernelGGL(k_attn<2>, dim3(blocks), dim3(256), multi ? attn_lds_bytes<2>() : 8 * 256 * 1 * 4, st, items, nitems, Qp, kpool, vpool, page_table, g,
+                     group, ppw, part, sc.ctr, par, dyn, multi);
     CHECK_LAUNCH();
 }
 
