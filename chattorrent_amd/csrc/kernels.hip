@@ -2727,7 +2727,8 @@ void launch_ids_col0(hipStream_t st, const uint32_t* ids, int rows, int stride, 
 
 // ================================================================ packing ===
 // One workgroup: per-job counts in parallel, their prefix sums in job order
-// (pack_exscan), then every table written by all threads. A job of n rows at past p needs ceil(n*group/16)
+// (pack_exscan), then every job's tables written by one wave, four jobs at a
+// time. A job of n rows at past p needs ceil(n*group/16)
 // Q m-tiles, ceil(ceil((p+n)/64)/ppw) chunks of pages per (kv head, m-tile),
 // one combine triple per (kv head, m-tile), and nKV*mtq*ng*128 Q-operand
 // units; each work item's softmax partial takes 16*(D+4) floats, at the
@@ -2817,10 +2818,12 @@ __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict
         }
     __syncthreads();
     const int part = 16 * (g.D + 4);
-    for (int j = 0; j < njobs; j++) {
+    // one wave a job: the four waves write four jobs' tables at a time
+    const int wv = threadIdx.x >> 6, ln = threadIdx.x & 63;
+    for (int j = wv; j < njobs; j += PACK_THREADS / 64) {
         const PackJob pj = in[j];
         const int past = pj.past + step, mtq = s_mtq[j], nch = s_nch[j];
-        if (threadIdx.x == 0) {
+        if (ln == 0) {
             JobDev jd;
             jd.slot = pj.slot;
             jd.past = past;
@@ -2836,7 +2839,7 @@ __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict
         }
         if (mtq == 1) {
             const int nfull = ((past + pj.n + g.page - 1) / g.page) / g.ppw;
-            for (int x = threadIdx.x; x < g.nKV * nch; x += blockDim.x) {
+            for (int x = ln; x < g.nKV * nch; x += 64) {
                 const int c = x % nch, h = x / nch;
                 const int idx = s_item0[j] + x;   // (kv head, m-tile 0, chunk)
                 items[c < nfull ? s_pos0[j] + h * nfull + c : s_posb[j] + h] =
@@ -2845,7 +2848,7 @@ __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict
         } else {
             // (kv head, chunk, block of 4 m-tiles, m-tile): a block is one workgroup
             const int nb = (mtq + 3) / 4, nit = g.nKV * nch * nb * 4;
-            for (int x = threadIdx.x; x < nit; x += blockDim.x) {
+            for (int x = ln; x < nit; x += 64) {
                 const int q = x % 4, b = (x / 4) % nb, c = (x / (4 * nb)) % nch, h = x / (4 * nb * nch);
                 const int mt = 4 * b + q;
                 if (mt >= mtq) {
@@ -2858,15 +2861,15 @@ __global__ __launch_bounds__(PACK_THREADS) void k_pack(const PackJob* __restrict
                     AttnItem{pj.slot, past, pj.n, mt, s_qp0[j] + (hm * g.ng) * 128, idx * part, h, c * g.ppw};
             }
         }
-        for (int x = threadIdx.x; x < g.nKV * mtq; x += blockDim.x) {
+        for (int x = ln; x < g.nKV * mtq; x += 64) {
             const int at = 3 * (s_cwg0[j] + x);
             cwg[at] = j;
             cwg[at + 1] = x / mtq;
             cwg[at + 2] = x % mtq;
         }
-        for (int i = threadIdx.x; i < pj.n; i += blockDim.x) row_job[s_row0[j] + i] = j;
+        for (int i = ln; i < pj.n; i += 64) row_job[s_row0[j] + i] = j;
         if (g.head)
-            for (int i = threadIdx.x; i < pj.sampled; i += blockDim.x)
+            for (int i = ln; i < pj.sampled; i += 64)
                 head_rows[s_head0[j] + i] = s_row0[j] + pj.n - pj.sampled + i;
     }
 }
