@@ -306,7 +306,7 @@ static void launch_lx(hipStream_t st, const QTensor& w, const uint4* Xp, float* 
 // order; the cut points depend only on N, K and the CU count (lx_cuts), and
 // k_gemm_tm folds its running sum at the same units. Each MFMA pair, scale
 // FMA and addition is the same operation on the same operands.
-constexpr int TM_MT = 4, TM_WAVES = 8, TM_PAIRS = 8, TM_R = 4;
+constexpr int TM_MT = 4, TM_WAVES = 8, TM_PAIRS = 8, TM_R = 2;
 
 // Unit offsets inside pair p (of a plane of `len` <= 32 units) where
 // k_gemm_lx starts a new partial sum, as a bit mask: the wave boundaries of
