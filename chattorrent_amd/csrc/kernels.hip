@@ -2205,7 +2205,10 @@ constexpr size_t attn_lds_bytes() {
 // the few blocks past the first round would wait for that XCD's slowest
 // workgroups). Each launch clears the counter of the next launch on its
 // stream, ctr[par ^ 1]; the one it counts with was cleared by the
-// launch before it.
+// launch before it. A block of one chunk's m-tiles (a job of several
+// m-tiles, in a launch with `multi` set) runs attn_block4, its four waves
+// sharing each page's dequantised fragments; other blocks' waves run their
+// items on their own (attn_item).
 template <int NG>
 __global__ __launch_bounds__(256, NG > 4 ? 1 : 2) void k_attn(const AttnItem* __restrict__ items, int nitems,
                                                  const uint4* __restrict__ Qp,
