@@ -237,6 +237,27 @@ def test_attend_vs_oracle(gpu):
             c.close()
 
 
+@pytest.mark.parametrize("shape", ["27b", "d256"])
+def test_attend_verify_rows_equal_one_row_bitwise(gpu, shape):
+    """A verify job's rows (several Q m-tiles: the workgroup's four waves share
+    each page's dequantised fragments) give the bits of the same rows attended
+    one at a time (one m-tile: each wave dequantises for itself), across a
+    page and chunk boundary (positions 505..512)."""
+    base = configs.M27B if shape == "27b" else D256
+    d = configs.with_layers(base, 1)
+    c = _ctx(gpu, d, n_max=1024, t_max=64, slots=2)
+    try:
+        P, n = 505, 8
+        c.fill_random_kv(1, P + n, 5, 9)
+        D, nH = d["head_dim"], d["n_heads"]
+        q = np.random.default_rng(P).standard_normal((n, nH * D)).astype(np.float32)
+        many = c.op_attend(0, 1, q, P)
+        for i in range(n):
+            one = c.op_attend(0, 1, q[i:i + 1], P + i)
+            assert np.array_equal(one.view(np.uint32), many[i:i + 1].view(np.uint32)), (shape, i)
+    finally:
+        c.close()
+
 def test_attend_ignores_stale_rows_past_the_context(gpu):
     """The pool rows past a job's tokens hold whatever an earlier session left
     there, NaN and inf included (web/model/kernels.js:1140-1310 never reads
