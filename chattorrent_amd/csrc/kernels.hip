@@ -2309,7 +2309,7 @@ __global__ __launch_bounds__(1024) void k_attn_combine(const JobDev* __restrict_
     // 16 rows x D columns, 8 a thread, in chunks of at most 128 columns (one
     // chunk up to D = 128, two at D = 256); every thread reaches every barrier
     const int sub = threadIdx.x >> 8, t = threadIdx.x & 255;
-    constexpr int CW = D < 128 ? D : 128, PRE = 8;
+    constexpr int CW = D < 128 ? D : 128, PRE = D > 128 ? 4 : 8;   // 8 at D = 256 spills at 128 VGPRs
     const int rl2 = t / (CW / 8);
     const bool live = rl2 < 16 && mt * 16 + rl2 < R;
     const int ca = (sub * nc) / COMBINE_SPLIT, c1 = ((sub + 1) * nc) / COMBINE_SPLIT;
