@@ -46,6 +46,7 @@ struct Layer {
 int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 constexpr int MTP_STEPS_MAX = 7;   // SPEC_COLS - 1 drafts (stage.js:303-304)
+constexpr int PPW_NARROW = 2;   // pages per attention item for narrow K/V rows (nKV * D <= 512)
 
 }  // namespace
 
@@ -570,8 +571,12 @@ cc_status cc_create(const cc_dims* dims, const cc_opts* opts, cc_ctx** out) {
         ctx->qp_units = (size_t)(ceil_div(T * ctx->group, 16) + o.max_jobs) * nKV * (D / 32) * 128;
         HIPCHK(dalloc(ctx, &ctx->qp, ctx->qp_units * 16, &ctx->scratch_bytes));
         // Attention work items: `ppw` pages each, at most COMBINE_CMAX chunks a
-        // frame (the combine kernel's LDS).
-        ctx->ppw = std::max(8, ceil_div(ctx->max_pages, 512));   // <= 64 (check_dims)
+        // frame (the combine kernel's LDS). Fixed for the context, so a row's
+        // sums depend on its own chunks only. Narrow K/V rows (nKV * D <= 512,
+        // SmolLM2's 3 x 64) make short items, and such a model's passes hold
+        // few of them: PPW_NARROW pages an item gives more waves at the same
+        // share of partial traffic.
+        ctx->ppw = std::max(nKV * D <= 512 ? PPW_NARROW : 8, ceil_div(ctx->max_pages, 512));   // <= 64 (check_dims)
         ctx->items_cap = max_items_for(ctx);
         // Attention partials: 16 rows of (D + 4) floats per item.
         ctx->apart_floats = ctx->items_cap * 16 * (size_t)(D + 4);
