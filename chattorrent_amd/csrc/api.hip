@@ -184,6 +184,23 @@ hipError_t dalloc(cc_ctx* ctx, T** p, size_t bytes, uint64_t* acct) {
     return hipSuccess;
 }
 
+// Frees a buffer dalloc made (nullptr: nothing) once the context's stream
+// has finished with it, and drops it from the context's list and account.
+template <class T>
+hipError_t dfree(cc_ctx* ctx, T* p, size_t bytes, uint64_t* acct) {
+    if (!p) return hipSuccess;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return e;
+    for (size_t i = 0; i < ctx->allocs.size(); i++)
+        if (ctx->allocs[i] == (void*)p) {
+            ctx->allocs[i] = ctx->allocs.back();
+            ctx->allocs.pop_back();
+            if (acct) *acct -= bytes;
+            return hipFree((void*)p);
+        }
+    return hipSuccess;
+}
+
 hipError_t alloc_q(cc_ctx* ctx, QTensor& q, int N, int K) {
     q.N = N;
     q.K = K;
@@ -1110,12 +1127,18 @@ static void build_plan(cc_ctx* ctx, const cc_job* jobs, int njobs, StepPlan& p, 
 static cc_status grow(cc_ctx* ctx, const StepPlan& p) {
     if (p.qp_units > ctx->qp_units) {
         uint4* q = nullptr;
+        HIPCHK(dfree(ctx, ctx->qp, ctx->qp_units * 16, &ctx->scratch_bytes));
+        ctx->qp = nullptr;
+        ctx->qp_units = 0;
         HIPCHK(dalloc(ctx, &q, p.qp_units * 16, &ctx->scratch_bytes));
         ctx->qp = q;
         ctx->qp_units = p.qp_units;
     }
     if (p.apart_floats > ctx->apart_floats) {
         float* a = nullptr;
+        HIPCHK(dfree(ctx, ctx->apart, ctx->apart_floats * 4, &ctx->scratch_bytes));
+        ctx->apart = nullptr;
+        ctx->apart_floats = 0;
         HIPCHK(dalloc(ctx, &a, p.apart_floats * 4, &ctx->scratch_bytes));
         ctx->apart = a;
         ctx->apart_floats = p.apart_floats;
@@ -1616,6 +1639,11 @@ cc_status cc_decode_steps(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_
     if (per * steps > ctx->dec_cap) {
         float* v = nullptr;
         uint32_t* i = nullptr;
+        HIPCHK(dfree(ctx, ctx->dec_vals, ctx->dec_cap * 4, &ctx->scratch_bytes));
+        HIPCHK(dfree(ctx, ctx->dec_ids, ctx->dec_cap * 4, &ctx->scratch_bytes));
+        ctx->dec_vals = nullptr;
+        ctx->dec_ids = nullptr;
+        ctx->dec_cap = 0;
         HIPCHK(dalloc(ctx, &v, per * steps * 4, &ctx->scratch_bytes));
         HIPCHK(dalloc(ctx, &i, per * steps * 4, &ctx->scratch_bytes));
         ctx->dec_vals = v;

@@ -110,7 +110,9 @@ function planBatch(lead, queue, rows) {
 //     or a closed-loop job (`exact`), must continue exactly (past == fed);
 //   * otherwise a closed-loop job behind the block is a duplicate (stale),
 //     and anything else is a cache the session no longer has (cold).
-// Returns {keep} (null: nothing rolled back) or {stale | cold: message}.
+// Returns {keep} (null: nothing rolled back), {stale: message}, or
+// {cold: message, behind}: behind is true only when the block holds fewer
+// rows than the job continues from.
 function continuation(q) {
     let keep = null;
     for (let p = Math.max(q.at, 1); p < q.last; p++) {
@@ -128,8 +130,11 @@ function continuation(q) {
         } else if (q.exact && q.past < fed && !q.specLost) {
             return { stale: `a duplicate of session ${q.session}'s job at ${q.past} (block ${b} is already at ${fed})` };
         } else {
+            // behind: the block lost rows the job needs (an eviction, which a
+            // capacity refusal may explain); otherwise the block is ahead of
+            // a job that cannot rewind it, which no retry can fix
             return { cold: `session ${q.session} is no longer cached here (block ${b} holds ${fed} rows, the job ` +
-                           `continues from ${q.past})` };
+                           `continues from ${q.past})`, behind: q.past > fed };
         }
         if (keep !== null && keep !== k) {
             return { cold: `session ${q.session}'s blocks disagree on a rollback (${keep} and ${k} rows)` };

@@ -475,7 +475,11 @@ class Runner {
                 err.stale = true;
                 throw err;
             }
-            if (c.cold) throw this.cold(h.s, c.cold);
+            if (c.cold && c.behind) throw this.cold(h.s, c.cold);
+            if (c.cold) {
+                this.counts.cold++;
+                throw new Error(c.cold);
+            }
             keep = c.keep;
         }
         let linear = false;

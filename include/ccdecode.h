@@ -278,9 +278,11 @@ cc_status cc_op_topk(cc_ctx* ctx, const float* logits, int32_t rows, int32_t V, 
  * serving loops, harnesses that forbid hipMalloc). `logits` [rows, V] f32,
  * `vals` and `ids` [rows, M] are DEVICE pointers the caller owns; the stages'
  * keys go to a static 4 MiB scratch array per GPU (TOPK_SCRATCH_KEYS keys),
- * and calls needing more are refused with CC_EARG (it holds, for example,
- * 256 rows of 2^20 logits at M = 1, or 30 rows of 262144 at M = 256). Runs
- * asynchronously on
+ * and calls needing more are refused with CC_EARG. The first stage keeps
+ * rows * ceil(V/4096) * M keys and the next one far fewer: at M = 1 and
+ * V = 2^20 a call needs rows * 257 keys, so up to 2040 rows fit; at M = 256
+ * and V = 262144, 30 rows.
+ * Runs asynchronously on
  * `stream` (a hipStream_t; NULL: the context's stream): the caller
  * synchronises before reading `vals`/`ids`. Calls no hipMalloc, hipFree or
  * allocating routine. Every call on one GPU shares that GPU's scratch, so

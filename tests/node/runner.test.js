@@ -337,6 +337,19 @@ test('hybrid: a recurrent block cannot be rewound (cold), a restart at 0 is fine
     await r.run(job('a', { past: 0, n: 2, ids: [1, 2] }));
 });
 
+test('hybrid: after a capacity refusal, a rewound recurrent block is still cold, not busy', async () => {
+    const { r } = makeHybrid();
+    await r.run(job('a', { n: 5, ids: [1, 2, 3, 4, 5] }));
+    r.refused.set('a', Number(process.hrtime.bigint()) / 1e6);
+    const cold0 = r.counts.cold;
+    const e = await rejects(r.run(job('a', { past: 3, n: 1, ids: [1] })), /session a is no longer cached here/);
+    assert.ok(!e.busy);
+    assert.strictEqual(r.counts.cold, cold0 + 1);
+    // behind the block (rows lost), the refusal still reads as busy
+    const e2 = await rejects(r.run(job('a', { past: 9, n: 1, ids: [1] })), /refused here for capacity/);
+    assert.strictEqual(e2.busy, true);
+});
+
 test('hybrid: replay leases beyond specSlots are refused nospec; an idle session\'s is taken', async () => {
     const { r } = makeHybrid({ specSlots: 1, idleMs: 30 });
     await r.run(job('a', { n: 2, ids: [1, 2] }));

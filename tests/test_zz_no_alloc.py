@@ -23,6 +23,16 @@ class _Hip:
         self.h.hipFree.argtypes = [C.c_void_p]
         self.h.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
         self.h.hipDeviceSynchronize.argtypes = []
+        self.h.hipStreamCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.h.hipStreamSynchronize.argtypes = [C.c_void_p]
+        self.h.hipStreamDestroy.argtypes = [C.c_void_p]
+        self.h.hipStreamBeginCapture.argtypes = [C.c_void_p, C.c_int]
+        self.h.hipStreamEndCapture.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
+        self.h.hipGraphInstantiate.argtypes = [C.POINTER(C.c_void_p), C.c_void_p, C.c_void_p, C.c_char_p,
+                                               C.c_size_t]
+        self.h.hipGraphLaunch.argtypes = [C.c_void_p, C.c_void_p]
+        self.h.hipGraphExecDestroy.argtypes = [C.c_void_p]
+        self.h.hipGraphDestroy.argtypes = [C.c_void_p]
         self.bufs = []
 
     def check(self, e):
@@ -59,18 +69,25 @@ def ctx(gpu):
     c.close()
 
 
-def _noalloc(c, hip, logits, M):
-    lib = c.lib
+def _bind(lib):
     lib.cc_topk_noalloc.restype = C.c_int32
     lib.cc_topk_noalloc.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
                                     C.c_void_p, C.c_void_p]
+
+
+def _noalloc(c, hip, logits, M, stream=None):
+    lib = c.lib
+    _bind(lib)
     rows, V = logits.shape
     dl = hip.upload(logits.astype(np.float32))
     dv = hip.alloc(rows * M * 4)
     di = hip.alloc(rows * M * 4)
-    st = lib.cc_topk_noalloc(c.h, dl, rows, V, M, dv, di, None)
+    st = lib.cc_topk_noalloc(c.h, dl, rows, V, M, dv, di, stream)
     assert st == 0, lib.cc_last_error(c.h).decode()
-    hip.check(hip.h.hipDeviceSynchronize())
+    if stream is None:
+        hip.check(hip.h.hipDeviceSynchronize())
+    else:
+        hip.check(hip.h.hipStreamSynchronize(stream))
     return hip.download(dv, (rows, M), np.float32), hip.download(di, (rows, M), np.uint32)
 
 
@@ -101,13 +118,73 @@ def test_noalloc_topk_refuses_past_its_scratch(ctx):
     hip = _Hip()
     try:
         lib = ctx.lib
-        lib.cc_topk_noalloc.restype = C.c_int32
-        lib.cc_topk_noalloc.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_void_p,
-                                        C.c_void_p, C.c_void_p]
+        _bind(lib)
         rows, V, M = 64, 262144, 256            # 64 * 64 * 256 keys in the first stage alone
         dl, dv, di = hip.alloc(4), hip.alloc(4), hip.alloc(4)
         st = lib.cc_topk_noalloc(ctx.h, dl, rows, V, M, dv, di, None)
         assert st == 5, st                      # CC_EARG
         assert "scratch" in lib.cc_last_error(ctx.h).decode()
     finally:
+        hip.free()
+
+
+def test_noalloc_topk_on_the_callers_stream(ctx):
+    """The call runs on a stream the caller created and synchronises, not the
+    context's: twice, the second smaller, each equal to cc_op_topk bitwise."""
+    hip = _Hip()
+    st = C.c_void_p()
+    hip.check(hip.h.hipStreamCreate(C.byref(st)))
+    try:
+        rng = np.random.default_rng(77)
+        for rows, V, M in ((9, 151936, 4), (2, 49152, 1)):
+            logits = rng.standard_normal((rows, V)).astype(np.float32)
+            vals, ids = _noalloc(ctx, hip, logits, M, stream=st)
+            want_v, want_i = ctx.op_topk(logits, M)
+            assert np.array_equal(ids, want_i), (rows, V, M)
+            assert np.array_equal(vals.view(np.uint32), want_v.view(np.uint32)), (rows, V, M)
+    finally:
+        hip.check(hip.h.hipStreamDestroy(st))
+        hip.free()
+
+
+def test_noalloc_topk_under_graph_capture(ctx):
+    """Captured once into a HIP graph on the caller's stream (relaxed capture
+    mode) and replayed four times over fresh logits copied in eagerly between
+    the replays: every replay equals cc_op_topk on that replay's logits. The
+    call records kernels only, no memset nodes, and allocates nothing, so it
+    can sit inside a caller's graph."""
+    hip = _Hip()
+    lib = ctx.lib
+    _bind(lib)
+    st = C.c_void_p()
+    hip.check(hip.h.hipStreamCreate(C.byref(st)))
+    graph, exe = C.c_void_p(), C.c_void_p()
+    try:
+        rows, V, M = 5, 151936, 3
+        rng = np.random.default_rng(91)
+        dl = hip.alloc(rows * V * 4)
+        dv = hip.alloc(rows * M * 4)
+        di = hip.alloc(rows * M * 4)
+        hip.check(hip.h.hipStreamBeginCapture(st, 2))          # hipStreamCaptureModeRelaxed
+        code = lib.cc_topk_noalloc(ctx.h, dl, rows, V, M, dv, di, st)
+        hip.check(hip.h.hipStreamEndCapture(st, C.byref(graph)))
+        assert code == 0, lib.cc_last_error(ctx.h).decode()
+        hip.check(hip.h.hipGraphInstantiate(C.byref(exe), graph, None, None, 0))
+        for rep in range(4):
+            logits = rng.standard_normal((rows, V)).astype(np.float32)
+            logits[rep % rows, 7 + rep] = logits[rep % rows, 3 * rep + 11] = 12.0   # a tie at the top
+            hip.check(hip.h.hipMemcpy(dl, logits.ctypes.data_as(C.c_void_p), logits.nbytes, 1))
+            hip.check(hip.h.hipGraphLaunch(exe, st))
+            hip.check(hip.h.hipStreamSynchronize(st))
+            vals = hip.download(dv, (rows, M), np.float32)
+            ids = hip.download(di, (rows, M), np.uint32)
+            want_v, want_i = ctx.op_topk(logits, M)          # eager work between the replays
+            assert np.array_equal(ids, want_i), rep
+            assert np.array_equal(vals.view(np.uint32), want_v.view(np.uint32)), rep
+    finally:
+        if exe.value:
+            hip.h.hipGraphExecDestroy(exe)
+        if graph.value:
+            hip.h.hipGraphDestroy(graph)
+        hip.check(hip.h.hipStreamDestroy(st))
         hip.free()
