@@ -223,44 +223,69 @@ void orc_matmul_q8(const float* X, int M, int K, const int8_t* W, const float* S
                 for (int j = 0; j < 4; j++)
                     xt[m * per + (g * 4 + j) * L + l] = X[(int64_t)m * K + 4 * w + j];
             }
+    /* Columns go in blocks of NB, each block's dequantised weights held while
+     * every row streams past them (a row's activations are read once per
+     * block, not per column); within a block, CB columns advance together as
+     * independent chains. Each output keeps the sequence above. */
+    enum { NB = 16, CB = 4 };
+    const int nblk = (N + NB - 1) / NB;
     #pragma omp parallel
     {
-        float* wt = (float*)malloc((size_t)per * sizeof(float));
-        float* acc = (float*)malloc((size_t)L * sizeof(float));
-        #pragma omp for schedule(static)
-        for (int n = 0; n < N; n++) {
-            for (int g = 0; g < ng; g++)
-                for (int l = 0; l < L; l++) {
-                    int w = g * L + l;
-                    for (int j = 0; j < 4; j++)
-                        wt[(g * 4 + j) * L + l] = w < K4 ? (float)W[(int64_t)n * K + 4 * w + j] : 0.0f;
-                }
-            const float* sn = S + (int64_t)n * ng;
+        float* wt = (float*)malloc((size_t)NB * per * sizeof(float));
+        float* acc = (float*)malloc((size_t)CB * L * sizeof(float));
+        #pragma omp for schedule(dynamic, 1)
+        for (int blk = 0; blk < nblk; blk++) {
+            const int n0 = blk * NB, nn = N - n0 < NB ? N - n0 : NB;
+            for (int c = 0; c < nn; c++)
+                for (int g = 0; g < ng; g++)
+                    for (int l = 0; l < L; l++) {
+                        int w = g * L + l;
+                        for (int j = 0; j < 4; j++)
+                            wt[c * per + (g * 4 + j) * L + l] =
+                                w < K4 ? (float)W[(int64_t)(n0 + c) * K + 4 * w + j] : 0.0f;
+                    }
             for (int m = 0; m < M; m++) {
                 const float* xm = xt + m * per;
-                for (int l = 0; l < L; l++) acc[l] = 0.0f;
-                for (int g = 0; g < ng; g++) {
-                    const float s = sn[g];
-                    const float* x0 = xm + (g * 4 + 0) * L; const float* w0 = wt + (g * 4 + 0) * L;
-                    const float* x1 = xm + (g * 4 + 1) * L; const float* w1 = wt + (g * 4 + 1) * L;
-                    const float* x2 = xm + (g * 4 + 2) * L; const float* w2 = wt + (g * 4 + 2) * L;
-                    const float* x3 = xm + (g * 4 + 3) * L; const float* w3 = wt + (g * 4 + 3) * L;
-                    if ((g + 1) * L <= K4) {
-                        for (int l = 0; l < L; l++) {
-                            float d = ((x0[l] * w0[l] + x1[l] * w1[l]) + x2[l] * w2[l]) + x3[l] * w3[l];
-                            acc[l] += s * d;
-                        }
-                    } else {
-                        for (int l = 0; l < L; l++) {
-                            if (g * L + l >= K4) continue;      /* partial last group */
-                            float d = ((x0[l] * w0[l] + x1[l] * w1[l]) + x2[l] * w2[l]) + x3[l] * w3[l];
-                            acc[l] += s * d;
+                for (int c0 = 0; c0 < nn; c0 += CB) {
+                    const int cn = nn - c0 < CB ? nn - c0 : CB;
+                    for (int i = 0; i < CB * L; i++) acc[i] = 0.0f;
+                    for (int g = 0; g < ng; g++) {
+                        const float* x0 = xm + (g * 4 + 0) * L;
+                        const float* x1 = xm + (g * 4 + 1) * L;
+                        const float* x2 = xm + (g * 4 + 2) * L;
+                        const float* x3 = xm + (g * 4 + 3) * L;
+                        const int full = (g + 1) * L <= K4;
+                        for (int c = 0; c < cn; c++) {
+                            const float s = S[(int64_t)(n0 + c0 + c) * ng + g];
+                            const float* wc = wt + (int64_t)(c0 + c) * per + (g * 4) * L;
+                            const float *w0 = wc, *w1 = wc + L, *w2 = wc + 2 * L, *w3 = wc + 3 * L;
+                            float* a = acc + c * L;
+                            if (full && L == 8) {       /* group 32: one 8-lane vector */
+                                for (int l = 0; l < 8; l++) {
+                                    float d = ((x0[l] * w0[l] + x1[l] * w1[l]) + x2[l] * w2[l]) + x3[l] * w3[l];
+                                    a[l] += s * d;
+                                }
+                            } else if (full) {
+                                for (int l = 0; l < L; l++) {
+                                    float d = ((x0[l] * w0[l] + x1[l] * w1[l]) + x2[l] * w2[l]) + x3[l] * w3[l];
+                                    a[l] += s * d;
+                                }
+                            } else {
+                                for (int l = 0; l < L; l++) {
+                                    if (g * L + l >= K4) continue;      /* partial last group */
+                                    float d = ((x0[l] * w0[l] + x1[l] * w1[l]) + x2[l] * w2[l]) + x3[l] * w3[l];
+                                    a[l] += s * d;
+                                }
+                            }
                         }
                     }
+                    for (int c = 0; c < cn; c++) {
+                        float* a = acc + c * L;
+                        for (int st = L / 2; st > 0; st >>= 1)
+                            for (int l = 0; l < st; l++) a[l] += a[l + st];
+                        Y[(int64_t)m * N + n0 + c0 + c] = a[0];
+                    }
                 }
-                for (int st = L / 2; st > 0; st >>= 1)
-                    for (int l = 0; l < st; l++) acc[l] += acc[l + st];
-                Y[(int64_t)m * N + n] = acc[0];
             }
         }
         free(wt);
@@ -393,33 +418,63 @@ void orc_store_kv(const float* src, uint32_t* cache, int T_new, int T_past, int 
 
 /* web/model/kernels.js:1140-1178 qk_scores_gqa: per block,
  * s = sum_w dot(q4, k4) (dot order as in orc_matmul_q8); sum += s * scale_b;
- * score = sum * (1/sqrt(D)). Q is [nH, T_q, D]; rows r0 .. r0+T_new-1. */
+ * score = sum * (1/sqrt(D)). Q is [nH, T_q, D]; rows r0 .. r0+T_new-1.
+ * Every score is that sequence of f32 operations; the loops only visit them
+ * by kv head and token, so each K row is read once for the group x T_new
+ * query rows that share it (one lane each). */
 void orc_qk_scores(const float* Q, const uint32_t* K, float* scores, int T_new, int T_act,
                    int page, int D, int nH, int group, const uint32_t* pages, int r0, int T_q) {
     const int QB = D < 32 ? D : 32, nb = D / QB, RW = D / 4 + nb, nKV = nH / group;
+    const int G = group * T_new, TB = 64;
+    const int nblk = (T_act + TB - 1) / TB;
     const float sc = 1.0f / sqrtf((float)D);
-    #pragma omp parallel for collapse(2) schedule(static)
+    /* qt[kvh][i][g]: lane g = (h - kvh*group) * T_new + tn */
+    float* qt = (float*)malloc((size_t)nKV * D * G * sizeof(float));
     for (int h = 0; h < nH; h++)
         for (int tn = 0; tn < T_new; tn++) {
-            const int kvh = h / group;
+            const int kvh = h / group, g = (h - kvh * group) * T_new + tn;
             const float* q = Q + ((int64_t)h * T_q + r0 + tn) * D;
-            for (int ta = 0; ta < T_act; ta++) {
-                int64_t at = (((int64_t)pages[ta / page] * nKV + kvh) * page + ta % page) * RW;
-                const int8_t* k8 = (const int8_t*)(K + at);
-                float sum = 0.0f;
-                for (int b = 0; b < nb; b++) {
-                    float s = 0.0f;
-                    for (int w = 0; w < QB / 4; w++) {
-                        int i = b * QB + 4 * w;
-                        float d = (((q[i] * (float)k8[i]) + q[i + 1] * (float)k8[i + 1])
-                                   + q[i + 2] * (float)k8[i + 2]) + q[i + 3] * (float)k8[i + 3];
-                        s += d;
-                    }
-                    sum += s * u2f(K[at + D / 4 + b]);
-                }
-                scores[((int64_t)h * T_new + tn) * T_act + ta] = sum * sc;
-            }
+            for (int i = 0; i < D; i++) qt[((int64_t)kvh * D + i) * G + g] = q[i];
         }
+    #pragma omp parallel
+    {
+        float* sum = (float*)malloc((size_t)G * sizeof(float));
+        float* s = (float*)malloc((size_t)G * sizeof(float));
+        float kf[512];
+        #pragma omp for collapse(2) schedule(dynamic, 1)
+        for (int kvh = 0; kvh < nKV; kvh++)
+            for (int blk = 0; blk < nblk; blk++) {
+                const float* qk = qt + (int64_t)kvh * D * G;
+                const int t1 = blk * TB + TB < T_act ? blk * TB + TB : T_act;
+                for (int ta = blk * TB; ta < t1; ta++) {
+                    int64_t at = (((int64_t)pages[ta / page] * nKV + kvh) * page + ta % page) * RW;
+                    const int8_t* k8 = (const int8_t*)(K + at);
+                    for (int i = 0; i < D; i++) kf[i] = (float)k8[i];
+                    for (int g = 0; g < G; g++) sum[g] = 0.0f;
+                    for (int b = 0; b < nb; b++) {
+                        for (int g = 0; g < G; g++) s[g] = 0.0f;
+                        for (int w = 0; w < QB / 4; w++) {
+                            const int i = b * QB + 4 * w;
+                            const float k0 = kf[i], k1 = kf[i + 1], k2 = kf[i + 2], k3 = kf[i + 3];
+                            const float *q0 = qk + (int64_t)i * G, *q1 = q0 + G, *q2 = q1 + G, *q3 = q2 + G;
+                            for (int g = 0; g < G; g++) {
+                                float d = (((q0[g] * k0) + q1[g] * k1) + q2[g] * k2) + q3[g] * k3;
+                                s[g] += d;
+                            }
+                        }
+                        const float scale = u2f(K[at + D / 4 + b]);
+                        for (int g = 0; g < G; g++) sum[g] += s[g] * scale;
+                    }
+                    for (int g = 0; g < G; g++) {
+                        const int h = kvh * group + g / T_new, tn = g % T_new;
+                        scores[((int64_t)h * T_new + tn) * T_act + ta] = sum[g] * sc;
+                    }
+                }
+            }
+        free(sum);
+        free(s);
+    }
+    free(qt);
 }
 
 /* web/model/kernels.js:1188-1253 causal_softmax: exact three passes over a
@@ -455,27 +510,40 @@ void orc_causal_softmax(float* scores, int T_new, int T_act, int T_past, int nH)
 }
 
 /* web/model/kernels.js:1264-1310 attn_av_gqa: out[h, r0+tn, d] =
- * sum_i p_i * (q_i,d * scale_i,d/QB), tokens in order. */
+ * sum_i p_i * (q_i,d * scale_i,d/QB), tokens in order. Each channel's sum is
+ * that sequence; the loops walk (kv head, 32 channels) and then the tokens,
+ * so each V row is dequantised once for all the query rows of its group. */
 void orc_attn_av(const float* scores, const uint32_t* V, float* out, int T_new, int T_act,
                  int page, int D, int nH, int group, const uint32_t* pages, int r0, int T_q) {
     const int QB = D < 32 ? D : 32, RW = D / 4 + D / QB, nKV = nH / group;
-    #pragma omp parallel for collapse(2) schedule(static)
-    for (int h = 0; h < nH; h++)
-        for (int tn = 0; tn < T_new; tn++) {
-            const int kvh = h / group;
-            const float* p = scores + ((int64_t)h * T_new + tn) * T_act;
-            float sum[256];
-            for (int d = 0; d < D; d++) sum[d] = 0.0f;
-            /* every channel's sum runs over the tokens in order; walking the
-             * tokens outermost reads each V row once */
-            for (int i = 0; i < T_act; i++) {
-                int64_t r = (((int64_t)pages[i / page] * nKV + kvh) * page + i % page) * RW;
-                const int8_t* q8 = (const int8_t*)(V + r);
-                const float pi = p[i];
-                for (int d = 0; d < D; d++) sum[d] += pi * ((float)q8[d] * u2f(V[r + D / 4 + d / QB]));
+    const int G = group * T_new, DC = D < 32 ? D : 32, nch = D / DC;
+    #pragma omp parallel
+    {
+        float* sum = (float*)malloc((size_t)G * DC * sizeof(float));
+        float vq[32];
+        #pragma omp for collapse(2) schedule(dynamic, 1)
+        for (int kvh = 0; kvh < nKV; kvh++)
+            for (int c = 0; c < nch; c++) {
+                const int d0 = c * DC;
+                for (int j = 0; j < G * DC; j++) sum[j] = 0.0f;
+                for (int i = 0; i < T_act; i++) {
+                    int64_t r = (((int64_t)pages[i / page] * nKV + kvh) * page + i % page) * RW;
+                    const int8_t* q8 = (const int8_t*)(V + r);
+                    for (int d = 0; d < DC; d++) vq[d] = (float)q8[d0 + d] * u2f(V[r + D / 4 + (d0 + d) / QB]);
+                    for (int g = 0; g < G; g++) {
+                        const int h = kvh * group + g / T_new, tn = g % T_new;
+                        const float pi = scores[((int64_t)h * T_new + tn) * T_act + i];
+                        float* sg = sum + (int64_t)g * DC;
+                        for (int d = 0; d < DC; d++) sg[d] += pi * vq[d];
+                    }
+                }
+                for (int g = 0; g < G; g++) {
+                    const int h = kvh * group + g / T_new, tn = g % T_new;
+                    for (int d = 0; d < DC; d++) out[((int64_t)h * T_q + r0 + tn) * D + d0 + d] = sum[g * DC + d];
+                }
             }
-            for (int d = 0; d < D; d++) out[((int64_t)h * T_q + r0 + tn) * D + d] = sum[d];
-        }
+        free(sum);
+    }
 }
 
 /* web/model/kernels.js:1513-1529 silu_mul: scale = 1/(1 + exp(-g));

@@ -263,6 +263,86 @@ def test_softmax_rows_sum_to_one_and_mask():
         assert np.all(p[:, i, 2 + i + 1:] == 0)
 
 
+def _softmax64(s, T_past, exp=np.exp, shift=0):
+    """Masked softmax in f64: row i sees keys 0..T_past+i (+ shift)."""
+    s = np.asarray(s, np.float64)
+    _, T_new, T_act = s.shape
+    keep = np.arange(T_act)[None, :] <= (T_past + shift + np.arange(T_new))[:, None]
+    m = np.where(keep, s, -np.inf).max(-1, keepdims=True)
+    e = np.where(keep, exp(s - m), 0.0)
+    return e / e.sum(-1, keepdims=True)
+
+
+def test_softmax_values_vs_f64():
+    """causal_softmax (kernels.js:1180-1253) against an f64 softmax with the
+    same mask, over scores spread wide enough that exp's base matters. The
+    same bar rejects an exp2 in place of exp and a causal limit one off."""
+    rng = np.random.default_rng(123)
+    T_past, T_new = 9, 4
+    s = (rng.random((3, T_new, T_past + T_new)) * 16 - 8).astype(np.float32)
+    p = L.causal_softmax(s, T_past)
+    want = _softmax64(s, T_past)
+    tol = 2e-6
+    assert np.abs(p - want).max() < tol
+    assert np.all(p[want == 0] == 0)
+    # planted mistakes in the f64 statement: each must exceed the bar
+    assert np.abs(p - _softmax64(s, T_past, exp=np.exp2)).max() > 100 * tol
+    assert np.abs(p - _softmax64(s, T_past, shift=1)).max() > 100 * tol
+    assert np.abs(p - _softmax64(s, T_past, shift=-1)).max() > 100 * tol
+
+
+def _attend64(Qr, Kd, Vd, past, group, kv_of=None, shift=0):
+    """f64 attention of Qr [nH, n, D] over dequantised rows Kd/Vd [nKV, T, D]:
+    scores / sqrt(D), causal (row i sees 0..past+i), softmax, P.V."""
+    nH, n, D = Qr.shape
+    kv_of = kv_of or (lambda h: h // group)
+    out = np.empty((nH, n, D))
+    for h in range(nH):
+        k, v = Kd[kv_of(h)], Vd[kv_of(h)]
+        s = (Qr[h].astype(np.float64) @ k.T) / np.sqrt(D)
+        out[h] = _softmax64(s[None], past, shift=shift)[0] @ v
+    return out
+
+
+def test_model_attend_vs_f64_paged_ragged_verify():
+    """Model.attend (model.js:321-351: store K/V into the paged int8 cache,
+    RoPE on Q, qk, exact causal softmax, P.V) for a verify job of 5 rows that
+    crosses a page boundary through a non-monotone page table, against f64
+    attention over the dequantised rows read back from the pool. The same bar
+    rejects a wrong GQA head mapping and a causal limit one off."""
+    d = dict(hidden=64, n_layer=1, n_heads=6, n_kv_heads=2, head_dim=64, ffn=64, vocab=64,
+             rms_eps=1e-5, rope_theta=1e4, tied=True, group_q8=32)
+    nH, nKV, D = 6, 2, 64
+    group = nH // nKV
+    om = Mo.Model(d, n_slots=3, max_pages=4)
+    om.fill_random_kv(0, 64, 5, 1)
+    om.fill_random_kv(1, 62, 5, 2)
+    om.fill_random_kv(2, 64, 5, 3)
+    past, n = 62, 5
+    assert om.pool.ensure(om.frames[1], past + n)
+    assert list(om.frames[1]["pages"][:2]) == [1, 3]          # non-monotone
+    rng = np.random.default_rng(8)
+    q = (rng.standard_normal((n, nH * D))).astype(np.float32)
+    k = (rng.standard_normal((n, nKV * D))).astype(np.float32)
+    v = (rng.standard_normal((n, nKV * D))).astype(np.float32)
+    got = om.attend(0, 1, q, k, v, past).reshape(n, nH, D).transpose(1, 0, 2)
+    Qr = L.rope(np.ascontiguousarray(q.reshape(n, nH, D).transpose(1, 0, 2)), D, past, om.tbl)
+    RW = om.rw
+    Kd = np.stack([_dequant(om.kv_rows(0, 0, 1, 0, past + n, h), D, RW)[0] for h in range(nKV)])
+    Vd = np.stack([_dequant(om.kv_rows(0, 1, 1, 0, past + n, h), D, RW)[0] for h in range(nKV)])
+    want = _attend64(Qr, Kd, Vd, past, group)
+    scale = np.abs(want).max()
+    tol = 2e-6 * scale
+    assert np.abs(got - want).max() < tol
+    assert np.abs(got - _attend64(Qr, Kd, Vd, past, group, kv_of=lambda h: h % nKV)).max() > 100 * tol
+    assert np.abs(got - _attend64(Qr, Kd, Vd, past, group, shift=1)).max() > 100 * tol
+    assert np.abs(got - _attend64(Qr, Kd, Vd, past, group, shift=-1)).max() > 100 * tol
+    # the new rows are the job's own K (after RoPE) and V, quantised
+    Kn = L.rope(np.ascontiguousarray(k.reshape(n, nKV, D).transpose(1, 0, 2)), D, past, om.tbl)
+    assert np.abs(Kd[:, past:] - Kn).max() <= 0.5 * np.abs(Kn).max(-1, keepdims=True).max() / 127 + 1e-6
+    assert np.abs(Vd[:, past:] - v.reshape(n, nKV, D).transpose(1, 0, 2)).max() <= np.abs(v).max() / 254 + 1e-6
+
+
 def _contiguous_cache(vals, D, page_words=None):
     """Rows [n_kv][N_max][D] -> quantised words via the oracle's store (V)."""
     nKV, N, _ = vals.shape
