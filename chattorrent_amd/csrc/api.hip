@@ -779,24 +779,45 @@ cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data
     QTensor* q = tensor_of(ctx, layer, tensor, &row_tile0, &N, &K);
     if (!q) return fail(ctx, CC_EARG, "tensor not held here");
     if (group < 32 || group % 32) return fail(ctx, CC_EARG, "q8 group must be a multiple of 32");
-    const int ng = ceil_div(K, 32), ngi = ceil_div(K, group), rep = group / 32;
+    const int ngi = ceil_div(K, group);
     if (n != (size_t)N * K || ns != (size_t)N * ngi || !scales)
         return fail(ctx, CC_EARG, "q8 tensor needs N*K codes and N*ceil(K/group) scales");
-    // one scale per 32 values along K: a wider group's scale repeats, exactly
-    std::vector<uint16_t> s16((size_t)N * ng);
-    for (size_t row = 0; row < (size_t)N; row++)
-        for (int g = 0; g < ng; g++) {
-            const size_t i = row * ngi + g / rep;
-            s16[row * ng + g] = scale_dtype == CC_SCALES_F16 ? ((const uint16_t*)scales)[i]
-                                                             : half_bits(((const float*)scales)[i]);
-        }
+    // f32 scales of a group of 64 or a multiple (the converter's, loaded by
+    // uploadQ8, web/model/kernels.js:116-126) stay f32: one per row and
+    // 64-wide unit, in the same bytes f16 scales per 32 take. Other groups
+    // keep one f16 scale per 32 values (f32 ones rounded to it). A wider
+    // group's scale repeats over its units or groups, exactly.
+    const bool f32u = scale_dtype == CC_SCALES_F32 && group % 64 == 0;
+    if (f32u ? q->up_f16 : q->up_f32)
+        return fail(ctx, CC_EARG, "the parts of a fused q8 tensor need one scale format: f32 scales with a group "
+                                  "of 64 (or a multiple) for every part, or none");
+    std::vector<uint8_t> sv;
+    if (f32u) {
+        const int rep = group / 64;
+        sv.resize((size_t)N * q->KU * 4);
+        float* s32 = (float*)sv.data();
+        for (size_t row = 0; row < (size_t)N; row++)
+            for (int u = 0; u < q->KU; u++) s32[row * q->KU + u] = ((const float*)scales)[row * ngi + u / rep];
+    } else {
+        const int ng = ceil_div(K, 32), rep = group / 32;
+        sv.resize((size_t)N * ng * 2);
+        uint16_t* s16 = (uint16_t*)sv.data();
+        for (size_t row = 0; row < (size_t)N; row++)
+            for (int g = 0; g < ng; g++) {
+                const size_t i = row * ngi + g / rep;
+                s16[row * ng + g] = scale_dtype == CC_SCALES_F16 ? ((const uint16_t*)scales)[i]
+                                                                 : half_bits(((const float*)scales)[i]);
+            }
+    }
+    q->f32s = f32u ? 1 : 0;
+    (f32u ? q->up_f32 : q->up_f16)++;
     int8_t* dc = nullptr;
-    uint16_t* ds = nullptr;
+    uint8_t* ds = nullptr;
     HIPCHK(hipMalloc(&dc, n));
-    HIPCHK(hipMalloc(&ds, s16.size() * 2));
+    HIPCHK(hipMalloc(&ds, sv.size()));
     HIPCHK(hipMemcpy(dc, data, n, hipMemcpyHostToDevice));
-    HIPCHK(hipMemcpy(ds, s16.data(), s16.size() * 2, hipMemcpyHostToDevice));
-    launch_tile_q8(ctx->stream, dc, ds, N, K, 32, *q, row_tile0);
+    HIPCHK(hipMemcpy(ds, sv.data(), sv.size(), hipMemcpyHostToDevice));
+    launch_tile_q8(ctx->stream, dc, ds, N, K, *q, row_tile0);
     HIPCHK(hipStreamSynchronize(ctx->stream));
     hipFree(dc);
     hipFree(ds);
@@ -805,10 +826,22 @@ cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data
 
 // Generator streams shared with the test oracle: wte 1, lm_head 2, block
 // tensor t of layer l: (l+1)*16 + t (q, k, v, o, gate, up, down).
+// Every q8 tensor of the context back to f16 scales per 32 with no parts
+// uploaded (the synthetic fill writes that format everywhere).
+static void reset_scale_formats(cc_ctx* ctx) {
+    auto reset = [](QTensor& q) { q.f32s = q.up_f16 = q.up_f32 = 0; };
+    for (Layer& L : ctx->layers)
+        for (QTensor* q : {&L.qkv, &L.o, &L.gu, &L.down, &L.lin, &L.out}) reset(*q);
+    for (QTensor* q : {&ctx->mtpL.qkv, &ctx->mtpL.o, &ctx->mtpL.gu, &ctx->mtpL.down, &ctx->fc_e, &ctx->fc_h,
+                       &ctx->embed_draft, &ctx->head_draft, &ctx->wte, &ctx->lm_head})
+        reset(*q);
+}
+
 cc_status cc_fill_random(cc_ctx* ctx, uint64_t seed) {
     if (!ctx) return CC_EARG;
     const cc_dims& d = ctx->d;
     hipStream_t st = ctx->stream;
+    reset_scale_formats(ctx);
     for (int li = 0; li < (int)ctx->layers.size(); li++) {
         const int layer = ctx->L0 + li;
         Layer& L = ctx->layers[li];
@@ -1837,7 +1870,7 @@ cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K, con
     HIPCHK(hipMemcpy(dS, scales_f16, (size_t)N * ng * 2, hipMemcpyHostToDevice));
     HIPCHK(hipMemcpy(dX, X, (size_t)M * K * 4, hipMemcpyHostToDevice));
     hipStream_t st = ctx->stream;
-    launch_tile_q8(st, dW, dS, N, K, 32, q, 0);
+    launch_tile_q8(st, dW, dS, N, K, q, 0);
     launch_prep_rows(st, dX, K, M, Mt * 16, K, q.KU, dXp);
     launch_gemm(st, q, dXp, Mt, dP, M, ctx->ncu);
     launch_sum_splits(st, dP, gemm_planes(q, M, ctx->ncu), M, N, dY);

@@ -20,6 +20,11 @@ constexpr int LX_REC = 2176;     // bytes per (tile pair, unit) record
 struct QTensor {
     uint8_t* codes = nullptr;    // records, Nt*KU*1088 bytes
     int N = 0, K = 0, Nt = 0, KU = 0, P = 1;
+    // Scale format of the records' 128-byte scale block: 0 = one f16 per
+    // row and 32-wide group (two per unit), 1 = one f32 per row and 64-wide
+    // unit (a converter checkpoint's group-64 f32 scales, kept exactly).
+    int f32s = 0;
+    int up_f16 = 0, up_f32 = 0;  // parts uploaded in each format since the last fill
 };
 
 __host__ __device__ inline int lx_plane_start(int r, int KU, int P) { return (r * KU) / P; }
@@ -188,8 +193,9 @@ void launch_kv_to_ref(hipStream_t st, const uint8_t* pool, const uint32_t* page_
                       int head, int t0, int t1, const KVGeom& g, int which, uint32_t* out);
 void launch_kv_from_ref(hipStream_t st, uint8_t* pool, const uint32_t* page_table, int slot,
                         int head, int t0, int t1, const KVGeom& g, int which, const uint32_t* in);
-void launch_tile_q8(hipStream_t st, const int8_t* codes, const uint16_t* scales, int N, int K,
-                    int group, const QTensor& w, int row_tile0);
+// scales: f16 [N, ceil(K/32)] when w.f32s == 0, f32 [N, ceil(K/64)] when 1.
+void launch_tile_q8(hipStream_t st, const int8_t* codes, const void* scales, int N, int K, const QTensor& w,
+                    int row_tile0);
 hipError_t take_launch_error();
 // Residual step (planes added in order, optional f16 round) and rmsnorm into
 // the operand Xp or rows y, one workgroup per row; H % 8 == 0, H <= 8192.

@@ -57,7 +57,22 @@ constexpr int LX_R = 2;
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-template <int MT>
+// The scale of half-group h (K columns 32h .. 32h+31 of the unit) of one
+// tile row, from the row's 32-bit word in the record's scale block: an f16
+// per 32-wide group (h = 0 in the low half), or one f32 per 64-wide unit
+// that both halves share (QTensor::f32s).
+template <bool F32S>
+__device__ static inline float rec_scale(uint32_t word, int h) {
+    if constexpr (F32S) {
+        (void)h;
+        return __builtin_bit_cast(float, word);
+    } else {
+        const uint16_t s16 = h ? (uint16_t)(word >> 16) : (uint16_t)(word & 0xffffu);
+        return (float)__builtin_bit_cast(_Float16, s16);
+    }
+}
+
+template <int MT, bool F32S>
 __global__ __launch_bounds__(64 * LX_WAVES) void k_gemm_lx(const uint8_t* __restrict__ Wr,
                                                            const uint4* __restrict__ Xp, float* __restrict__ out,
                                                            int KU, int M, int N, int Nt, int P, int Gm) {
@@ -128,8 +143,7 @@ __global__ __launch_bounds__(64 * LX_WAVES) void k_gemm_lx(const uint8_t* __rest
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 b[nt] = h ? dequant8_biased(wc[nt][2], wc[nt][3]) : dequant8_biased(wc[nt][0], wc[nt][1]);
-                const uint16_t s16 = h ? (uint16_t)(sc[nt] >> 16) : (uint16_t)(sc[nt] & 0xffffu);
-                scale[nt] = (float)__builtin_bit_cast(_Float16, s16);
+                scale[nt] = rec_scale<F32S>(sc[nt], h);
             }
             // hi then lo into one partial per output, then one scale FMA
             float4_t pp[MT][NT];
@@ -273,12 +287,12 @@ int lx_planes_for(int N, int K, int ncu) {
     return P;
 }
 
-template <int MT>
+template <int MT, bool F32S>
 static void launch_lx(hipStream_t st, const QTensor& w, const uint4* Xp, float* out, int M, int ncu) {
     static bool attr = false;
     if (!attr) {
         attr = true;
-        (void)hipFuncSetAttribute((const void*)k_gemm_lx<MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        (void)hipFuncSetAttribute((const void*)k_gemm_lx<MT, F32S>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   LX_UNITS * MT * 4096);
     }
     const int G = lx_groups(w, ncu), Gm = G / w.P;
@@ -286,8 +300,8 @@ static void launch_lx(hipStream_t st, const QTensor& w, const uint4* Xp, float* 
     // the plane's activations, and afterwards the cut parts (1 KiB per wave, m-tile and tile)
     const size_t lds = std::max((size_t)lenmax * MT * 4096, (size_t)LX_WAVES * MT * 2 * 1024);
     dim3 grid(G, (M + 16 * MT - 1) / (16 * MT));
-    hipLaunchKernelGGL(k_gemm_lx<MT>, grid, dim3(64 * LX_WAVES), lds, st, (const uint8_t*)w.codes, Xp, out, w.KU, M, w.N,
-                 w.Nt, w.P, Gm);
+    hipLaunchKernelGGL((k_gemm_lx<MT, F32S>), grid, dim3(64 * LX_WAVES), lds, st, (const uint8_t*)w.codes, Xp, out,
+                       w.KU, M, w.N, w.Nt, w.P, Gm);
 }
 
 // ------------------------------------------------- many rows (M > 32) ---
@@ -327,6 +341,7 @@ __device__ static inline uint32_t lx_cuts(int p, int npairs, int Gm, int len) {
     return m;
 }
 
+template <bool F32S>
 __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm(const uint8_t* __restrict__ Wr,
                                                               const uint4* __restrict__ Xp, int xp_mtiles,
                                                               float* __restrict__ out, int KU, int M, int N, int Nt,
@@ -427,8 +442,7 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm(const uint8_t* __rest
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 b[h][nt] = h ? dequant8_biased(wc[nt][2], wc[nt][3]) : dequant8_biased(wc[nt][0], wc[nt][1]);
-                const uint16_t s16 = h ? (uint16_t)(sv[nt] >> 16) : (uint16_t)(sv[nt] & 0xffffu);
-                scale[h][nt] = (float)__builtin_bit_cast(_Float16, s16);
+                scale[h][nt] = rec_scale<F32S>(sv[nt], h);
             }
 #pragma unroll
         for (int mt = 0; mt < MTW; mt++) {
@@ -507,6 +521,7 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm(const uint8_t* __rest
 // loads pad this sum the same way when P < 16), so the bits are the same,
 // and the P-plane write and read are spared. For rows enough to fill the
 // GPU without the K split (gemm_planes).
+template <bool F32S>
 __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm_sum(const uint8_t* __restrict__ Wr,
                                                               const uint4* __restrict__ Xp, int xp_mtiles,
                                                               float* __restrict__ out, int KU, int M, int N, int Nt,
@@ -616,8 +631,7 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm_sum(const uint8_t* __
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 b[h][nt] = h ? dequant8_biased(wc[nt][2], wc[nt][3]) : dequant8_biased(wc[nt][0], wc[nt][1]);
-                const uint16_t s16 = h ? (uint16_t)(sv[nt] >> 16) : (uint16_t)(sv[nt] & 0xffffu);
-                scale[h][nt] = (float)__builtin_bit_cast(_Float16, s16);
+                scale[h][nt] = rec_scale<F32S>(sv[nt], h);
             }
 #pragma unroll
         for (int mt = 0; mt < MTW; mt++) {
@@ -711,9 +725,11 @@ int gemm_planes(const QTensor& w, int M, int ncu) {
     return work >= 2LL * ncu ? 1 : w.P;
 }
 
-void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtiles, float* out, int M, int ncu) {
-    if (M <= 16) launch_lx<1>(st, w, Xp, out, M, ncu);
-    else if (M <= 32) launch_lx<2>(st, w, Xp, out, M, ncu);
+template <bool F32S>
+static void launch_gemm_fmt(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtiles, float* out, int M,
+                            int ncu) {
+    if (M <= 16) launch_lx<1, F32S>(st, w, Xp, out, M, ncu);
+    else if (M <= 32) launch_lx<2, F32S>(st, w, Xp, out, M, ncu);
     else {
         // the same planes and cut points as k_gemm_lx (lx_groups)
         const int Gm = lx_groups(w, ncu) / w.P;
@@ -722,13 +738,18 @@ void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtile
         const int units = (sum ? 1 : w.P) * ((npairs + TM_PAIRS - 1) / TM_PAIRS), nrb = (M + 16 * TM_MT - 1) / (16 * TM_MT);
         dim3 grid(8 * ((units + 7) / 8) * nrb);
         if (sum)
-            hipLaunchKernelGGL(k_gemm_tm_sum, grid, dim3(64 * TM_WAVES), 0, st, (const uint8_t*)w.codes, Xp, xp_mtiles,
-                               out, w.KU, M, w.N, w.Nt, w.P, Gm);
+            hipLaunchKernelGGL(k_gemm_tm_sum<F32S>, grid, dim3(64 * TM_WAVES), 0, st, (const uint8_t*)w.codes, Xp,
+                               xp_mtiles, out, w.KU, M, w.N, w.Nt, w.P, Gm);
         else
-            hipLaunchKernelGGL(k_gemm_tm, grid, dim3(64 * TM_WAVES), 0, st, (const uint8_t*)w.codes, Xp, xp_mtiles, out,
-                               w.KU, M, w.N, w.Nt, w.P, Gm);
+            hipLaunchKernelGGL(k_gemm_tm<F32S>, grid, dim3(64 * TM_WAVES), 0, st, (const uint8_t*)w.codes, Xp,
+                               xp_mtiles, out, w.KU, M, w.N, w.Nt, w.P, Gm);
     }
     CHECK_LAUNCH();
+}
+
+void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtiles, float* out, int M, int ncu) {
+    if (w.f32s) launch_gemm_fmt<true>(st, w, Xp, xp_mtiles, out, M, ncu);
+    else launch_gemm_fmt<false>(st, w, Xp, xp_mtiles, out, M, ncu);
 }
 
 // =========================================================== operand prep ===
@@ -2437,8 +2458,8 @@ void launch_attn_combine(hipStream_t st, const JobDev* jobs, const float* part, 
 // embedding rows are rounded like a block's output, stage.js:1365-1370);
 // or, for a pass entering past position 0, the f16 rows handed in.
 __global__ void k_embed(const int32_t* __restrict__ ids, const uint16_t* __restrict__ hidden, int T, int H,
-                        const uint8_t* __restrict__ rec, int Nt, int KU, int P, float* __restrict__ x, int round,
-                        int nrows) {
+                        const uint8_t* __restrict__ rec, int Nt, int KU, int P, int f32s, float* __restrict__ x,
+                        int round, int nrows) {
     const int t = blockIdx.y;
     const int h = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= T || h >= H) return;
@@ -2455,16 +2476,17 @@ __global__ void k_embed(const int32_t* __restrict__ ids, const uint16_t* __restr
     const int byte = 8 * ((h & 63) >> 5) + (h & 7);
     const uint8_t* r = rec + lx_record(tile, u, KU, P, Nt);
     const int8_t q = (int8_t)(r[(tile & 1) * 1024 + lane * 16 + byte] ^ 0x80);
-    const uint16_t sb = *(const uint16_t*)(r + 2048 + (v & 15) * 8 + (tile & 1) * 4 + ((h >> 5) & 1) * 2);
-    const float e = (float)q * half_value(sb);
+    const uint8_t* sp = r + 2048 + (v & 15) * 8 + (tile & 1) * 4;
+    const float sc = f32s ? *(const float*)sp : half_value(*(const uint16_t*)(sp + ((h >> 5) & 1) * 2));
+    const float e = (float)q * sc;
     x[(size_t)t * H + h] = round ? round_f16_value(e) : e;
 }
 
 void launch_embed(hipStream_t st, const int32_t* ids, const uint16_t* hidden, int T, const QTensor& wte,
                   float* x, int round) {
     dim3 grid((wte.K + 255) / 256, T);
-    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, st, ids, hidden, T, wte.K, wte.codes, wte.Nt, wte.KU, wte.P, x,
-                       round, ids ? wte.N : 0);
+    hipLaunchKernelGGL(k_embed, grid, dim3(256), 0, st, ids, hidden, T, wte.K, wte.codes, wte.Nt, wte.KU, wte.P,
+                       wte.f32s, x, round, ids ? wte.N : 0);
     CHECK_LAUNCH();
 }
 
@@ -2951,9 +2973,10 @@ void launch_gen_q8(hipStream_t st, const QTensor& w, int row_tile0, int N, int K
     CHECK_LAUNCH();
 }
 
-// Host int8 [N, K] codes + f16 scales [N, ceil(K/group)] (group 32) -> records.
-__global__ void k_tile_q8(const int8_t* __restrict__ src, const uint16_t* __restrict__ sc, int N, int K,
-                          uint8_t* __restrict__ rec, int Nt, int KU, int P, int row_tile0) {
+// Host int8 [N, K] codes + scales -> records: f16 scales [N, ceil(K/32)]
+// (f32s = 0), or f32 scales [N, KU], one per 64-wide unit (f32s = 1).
+__global__ void k_tile_q8(const int8_t* __restrict__ src, const void* __restrict__ scv, int N, int K,
+                          uint8_t* __restrict__ rec, int Nt, int KU, int P, int row_tile0, int f32s) {
     const int tiles = (N + 15) / 16;
     const int64_t total = (int64_t)tiles * KU * 64;
     const int ng = (K + 31) / 32;
@@ -2971,23 +2994,27 @@ __global__ void k_tile_q8(const int8_t* __restrict__ src, const uint16_t* __rest
             const int q = (n < N && k < K) ? src[(size_t)n * K + k] : 0;
             dst[j] = (uint8_t)((q & 0xff) ^ 0x80);
         }
-        if (lane < 16)
+        if (lane < 16 && f32s) {
+            const float* sc = (const float*)scv;
+            *(float*)(r + 2048 + lane * 8 + (tg & 1) * 4) = n < N ? sc[(size_t)n * KU + u] : 0.0f;
+        } else if (lane < 16) {
+            const uint16_t* sc = (const uint16_t*)scv;
             for (int h = 0; h < 2; h++) {
                 const int gg = 2 * u + h;
                 *(uint16_t*)(r + 2048 + lane * 8 + (tg & 1) * 4 + h * 2) =
                     (n < N && gg < ng) ? sc[(size_t)n * ng + gg] : (uint16_t)0;
             }
+        }
     }
 }
 
-void launch_tile_q8(hipStream_t st, const int8_t* codes, const uint16_t* scales, int N, int K, int group,
-                    const QTensor& w, int row_tile0) {
-    (void)group;
+void launch_tile_q8(hipStream_t st, const int8_t* codes, const void* scales, int N, int K, const QTensor& w,
+                    int row_tile0) {
     const int64_t total = (int64_t)((N + 15) / 16) * w.KU * 64;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     hipLaunchKernelGGL(k_tile_q8, dim3((unsigned)blocks), dim3(256), 0, st, codes, scales, N, K, w.codes, w.Nt,
-                       w.KU, w.P, row_tile0);
+                       w.KU, w.P, row_tile0, w.f32s);
     CHECK_LAUNCH();
 }
 
