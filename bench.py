@@ -188,7 +188,13 @@ def cpu_line(value, unit, sample, kind="port"):
     return out
 
 
-def base_line(args, metric, value, unit, ms, dtype="int8xf32"):
+# The arithmetic: int8 weights (f16 or f32 scales) times f32 activations, the
+# activations carried into the MFMAs as two f16 halves, hi + 2^-11 lo (about 22
+# significant bits), with f32 products and accumulation.
+DTYPE = "int8 x f32 (activations as f16 hi + 2^-11 lo, 22-bit; f32 accumulate)"
+
+
+def base_line(args, metric, value, unit, ms, dtype=DTYPE):
     return {"metric": metric, "value": round(value, 2), "unit": unit, "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": dtype,
@@ -464,7 +470,46 @@ def bench_c5(args, ceil):
                                 "(f16 hi and lo halves of the f32 activations)"}
     line["ceilings"] = ceil
     line["cpu_baseline"] = None
+    if not args.no_cpu:
+        log("c5: timing the CPU oracle sample")
+        ms_cpu, rows, secs = cpu_churn_sample(d, slots, chunk, t_max, args.seed, passes=3)
+        line["cpu_baseline"] = cpu_line(
+            round(rows / (ms_cpu / 1000.0), 3), "tok/s",
+            f"oracle (C restatement, OpenMP): the churn's first 3 passes ({rows} rows, prompt chunks and decode "
+            f"rows) through one 8B block ({secs:.1f} s) plus the LM head for their sampled rows, scaled to 32 "
+            f"blocks ({ms_cpu:.0f} ms for the 3 passes)")
     return line
+
+
+def cpu_churn_sample(d, slots, chunk, t_max, seed, passes):
+    """The CPU oracle on configs[4]'s first `passes` passes (the same Churn
+    workload, seeded alike): every pass's rows through one block with its own
+    weights, and the LM head for the pass's sampled rows, scaled to d's depth.
+    Returns (ms for the passes at full depth, rows, seconds spent)."""
+    from chattorrent_amd import configs
+    from oracle import lib as L
+    from oracle import model as Mo
+    ds = dict(d, n_layer=1)
+    n_max = 4096 + 512 + 64
+    om = Mo.Model(ds, n_slots=slots, max_pages=-(-n_max // 64))
+    om.gen_weights(seed)
+    churn = configs.Churn(d["vocab"], slots, chunk, t_max, seed + 5)
+    t_blocks = t_head = 0.0
+    rows = 0
+    for _ in range(passes):
+        jobs = churn.jobs()
+        t0 = time.perf_counter()
+        om.pass_(jobs, head=False)
+        t_blocks += time.perf_counter() - t0
+        sampled = sum(j["sampled"] for j in jobs)
+        if sampled:
+            hs = np.ones((sampled, d["hidden"]), np.float32)
+            t0 = time.perf_counter()
+            L.matmul_q8(hs, *om.head_weight(), group=32)
+            t_head += time.perf_counter() - t0
+        rows += sum(j["n"] for j in jobs)
+        churn.advance(jobs, np.zeros(sampled, np.int64))
+    return (t_blocks * d["n_layer"] + t_head) * 1000.0, rows, t_blocks + t_head
 
 
 def js_sample(d, lens, prompts, seed, steps=3):

@@ -134,6 +134,29 @@ __device__ static inline void split_hilo(float x, _Float16& hi, _Float16& lo) {
     lo = (_Float16)(x - (float)hi);
 }
 
+// The scaled split the matmul operands and attention's P.V use: hi = f16(x)
+// and lo = f16((x - hi) * 2^11). The remainder is below half an f16 step of
+// hi, so lo scaled by 2^11 is of x's own magnitude and stays a normal f16 for
+// every |x| >= 2^-14 (an unscaled lo is subnormal below |x| = 2^-3 and keeps
+// fewer bits). The consumer multiplies lo's products by 2^-11, exactly: the
+// matmuls with the weight fragment scaled by HILO_LO_WEIGHT, attention with
+// its lo accumulator. |x - hi| * 2^11 <= 2^15 for every finite f16 hi.
+constexpr float HILO_LO_SHIFT = 2048.0f;
+constexpr float HILO_LO_WEIGHT = 1.0f / 2048.0f;
+__device__ static inline void split_hilo_x(float x, _Float16& hi, _Float16& lo) {
+    asm("" : "+v"(x));
+    hi = (_Float16)x;
+    lo = (_Float16)((x - (float)hi) * HILO_LO_SHIFT);
+}
+
+// Eight dequantised weights scaled by 2^-11 (exact: |q| <= 127 integers), the
+// fragment the scaled lo half multiplies.
+__device__ static inline half8_t lo_weight8(half8_t b) {
+    const _Float16 w = (_Float16)HILO_LO_WEIGHT;
+    const half8_t s = {w, w, w, w, w, w, w, w};
+    return b * s;
+}
+
 // Two values at once, as split_hilo (nearest-even hi, lo = f16 of the exact
 // remainder), returned packed as two f16 pairs. (Truncating the pair with
 // v_cvt_pkrtz saves two instructions but biases every lo toward zero, and the
@@ -145,6 +168,20 @@ __device__ static inline void split_hilo2(float x0, float x1, uint32_t& hi, uint
     const half2_t h = __builtin_convertvector(x, half2_t);   // one packed conversion
     const f2_t hb = __builtin_convertvector(h, f2_t);        // back from the packed halves
     const half2_t l = __builtin_convertvector(x - hb, half2_t);
+    hi = __builtin_bit_cast(uint32_t, h);
+    lo = __builtin_bit_cast(uint32_t, l);
+}
+
+// split_hilo2 with the scaled lo of split_hilo_x.
+__device__ static inline void split_hilo2_x(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    asm("" : "+v"(x0), "+v"(x1));
+    const f2_t x = {x0, x1};
+    const half2_t h = __builtin_convertvector(x, half2_t);
+    const f2_t hb = __builtin_convertvector(h, f2_t);
+    const f2_t r = x - hb;
+    const f2_t rs = {r[0] * HILO_LO_SHIFT, r[1] * HILO_LO_SHIFT};
+    const half2_t l = __builtin_convertvector(rs, half2_t);
     hi = __builtin_bit_cast(uint32_t, h);
     lo = __builtin_bit_cast(uint32_t, l);
 }

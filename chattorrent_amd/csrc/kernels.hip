@@ -32,7 +32,8 @@ hipError_t take_launch_error() {
 // Y[M, N] = X[M, K] . W[N, K]^T for a q8 W in record order (kernels.h) and an
 // activation operand Xp prepared by the prep/finish kernels:
 //   Xp[((mt*G2 + g)*2 + hl)*64 + lane] = 8 f16 of X[16mt + lane%16][32g + 8(lane/16) ..]
-// (hl = 0: hi part, 1: lo part; G2 = 2*KU groups, zero beyond K).
+// (hl = 0: hi part, 1: lo part scaled by 2^11 (split_hilo_x), which meets the
+// weights scaled by 2^-11; G2 = 2*KU groups, zero beyond K).
 // Reference: matmul_gemv_q8 / matmul_gemv_rows_q8 / matmul_rows_q8 /
 // matmul_tiled_q8 (web/model/kernels.js:449-804): per group, acc += scale * dot(x, q).
 //
@@ -153,11 +154,14 @@ __global__ __launch_bounds__(64 * LX_WAVES) void k_gemm_lx(const uint8_t* __rest
                 for (int nt = 0; nt < NT; nt++)
                     pp[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[mt][2 * h]), b[nt],
                                               float4_t{0.f, 0.f, 0.f, 0.f});
+            half8_t bl[NT];   // the lo half carries 2^11 x its remainder
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) bl[nt] = lo_weight8(b[nt]);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
-                    pp[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[mt][2 * h + 1]), b[nt], pp[mt][nt]);
+                    pp[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[mt][2 * h + 1]), bl[nt], pp[mt][nt]);
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
@@ -435,13 +439,14 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm(const uint8_t* __rest
                 }
             started = true;
         }
-        half8_t b[2][NT];
+        half8_t b[2][NT], bl[2][NT];   // bl: the lo half's fragment, 2^-11 b
         float scale[2][NT];
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 b[h][nt] = h ? dequant8_biased(wc[nt][2], wc[nt][3]) : dequant8_biased(wc[nt][0], wc[nt][1]);
+                bl[h][nt] = lo_weight8(b[h][nt]);
                 scale[h][nt] = rec_scale<F32S>(sv[nt], h);
             }
 #pragma unroll
@@ -457,7 +462,7 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm(const uint8_t* __rest
                     pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h]), b[h][nt], float4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
-                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h + 1]), b[h][nt], pp[nt]);
+                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h + 1]), bl[h][nt], pp[nt]);
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
 #pragma unroll
@@ -624,13 +629,14 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm_sum(const uint8_t* __
                 }
             started = true;
         }
-        half8_t b[2][NT];
+        half8_t b[2][NT], bl[2][NT];   // bl: the lo half's fragment, 2^-11 b
         float scale[2][NT];
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 b[h][nt] = h ? dequant8_biased(wc[nt][2], wc[nt][3]) : dequant8_biased(wc[nt][0], wc[nt][1]);
+                bl[h][nt] = lo_weight8(b[h][nt]);
                 scale[h][nt] = rec_scale<F32S>(sv[nt], h);
             }
 #pragma unroll
@@ -646,7 +652,7 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm_sum(const uint8_t* __
                     pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h]), b[h][nt], float4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
-                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h + 1]), b[h][nt], pp[nt]);
+                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h + 1]), bl[h][nt], pp[nt]);
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
 #pragma unroll
@@ -754,7 +760,7 @@ void launch_gemm(hipStream_t st, const QTensor& w, const uint4* Xp, int xp_mtile
 
 // =========================================================== operand prep ===
 // Writes 8 consecutive values of row m (columns 8c .. 8c+7) as the f16 hi/lo
-// operand fragments of the GEMM (layout above).
+// operand fragments of the GEMM (layout above; lo scaled by 2^11).
 __device__ static inline void write_hilo(uint4* Xp, int m, int c, int KU, const float* v) {
     const int g = c >> 2, kb = c & 3;
     const int mt = m >> 4, lane = (m & 15) + 16 * kb;
@@ -762,7 +768,7 @@ __device__ static inline void write_hilo(uint4* Xp, int m, int c, int KU, const 
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         _Float16 a, b;
-        split_hilo(v[j], a, b);
+        split_hilo_x(v[j], a, b);
         hi[j] = a;
         lo[j] = b;
     }
@@ -1945,6 +1951,9 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
                     lsum += e;
                 }
             __builtin_amdgcn_sched_barrier(0);
+            // p * s as hi + 2^-11 lo (split_hilo2_x): the lo products gather in
+            // ol over the page and join O once, times 2^-11
+            float4_t ol[DT];
 #pragma unroll
             for (int b = 0; b < NG; b++) {
                 float sv[16];   // the lane's 16 tokens of 32-block b
@@ -1962,7 +1971,7 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
                         const float p0 = pr[tt][r] * sv[4 * tt + r];
                         const float p1 = pr[tt][r + 1] * sv[4 * tt + r + 1];
                         uint32_t h, l;
-                        split_hilo2(p0, p1, h, l);
+                        split_hilo2_x(p0, p1, h, l);
                         phw[ii >> 1] = h;
                         plw[ii >> 1] = l;
                     }
@@ -1973,10 +1982,14 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
                         const u32x4 c = vc[dt];
                         const half8_t vf = ks ? dequant8_biased(c[2], c[3]) : dequant8_biased(c[0], c[1]);
                         o[dt] = mfma16x16x32(vf, ph, o[dt]);
-                        o[dt] = mfma16x16x32(vf, pl, o[dt]);
+                        ol[dt] = mfma16x16x32(vf, pl, ks ? ol[dt] : float4_t{0.f, 0.f, 0.f, 0.f});
                     }
                 }
             }
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) o[dt][r] = __builtin_fmaf(HILO_LO_WEIGHT, ol[dt][r], o[dt][r]);
             mrow = mnew;
             load_v(rvn);
         }
@@ -2165,6 +2178,7 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
                 pr[tt][r] = e;
                 lsum += e;
             }
+        float4_t ol[DT];   // the page's lo-half products (split_hilo2_x), 2^11 x
 #pragma unroll
         for (int b = 0; b < NG; b++) {
             float sv[16];
@@ -2180,7 +2194,7 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
                 for (int ii = 0; ii < 8; ii += 2) {
                     const int tt = 2 * ks + (ii >> 2), r = ii & 3;
                     uint32_t h, l;
-                    split_hilo2(pr[tt][r] * sv[4 * tt + r], pr[tt][r + 1] * sv[4 * tt + r + 1], h, l);
+                    split_hilo2_x(pr[tt][r] * sv[4 * tt + r], pr[tt][r + 1] * sv[4 * tt + r + 1], h, l);
                     phw[ii >> 1] = h;
                     plw[ii >> 1] = l;
                 }
@@ -2190,10 +2204,14 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
                     const int dt = 2 * b + dd;
                     const half8_t vfr = __builtin_bit_cast(half8_t, vf[(dt * 2 + ks) * 64 + lane]);
                     o[dt] = mfma16x16x32(vfr, ph, o[dt]);
-                    o[dt] = mfma16x16x32(vfr, pl, o[dt]);
+                    ol[dt] = mfma16x16x32(vfr, pl, ks ? ol[dt] : float4_t{0.f, 0.f, 0.f, 0.f});
                 }
             }
         }
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[dt][r] = __builtin_fmaf(HILO_LO_WEIGHT, ol[dt][r], o[dt][r]);
         mrow = mnew;
     }
     if (!mine) return;

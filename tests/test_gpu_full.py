@@ -28,6 +28,7 @@ import warnings
 import numpy as np
 import pytest
 
+import f64_block as F
 from chattorrent_amd import configs
 
 pytestmark = pytest.mark.gpu
@@ -139,6 +140,7 @@ def test_config0_smollm2_full_depth_32_greedy_steps(gpu):
 SEED27 = 1234          # bench.py's default seed: weights, KV keys s+1, first ids
 CHATS = 32
 CHECK_STEPS = 3
+F64_BLOCKS = (0, 1, 31, 63)   # blocks also computed in f64 (tests/f64_block.py)
 
 
 @pytest.fixture(scope="module")
@@ -188,6 +190,12 @@ def test_config2_27b_full_depth_greedy_steps(model27b):
       rows against the oracle's (one oracle pass of 3 rows per chat fed the
       same ids: row i has the bits of its i-th one-row pass, which
       tests/test_oracle.py pins), and the greedy ids.
+
+    * the f32 floor: blocks 0, 1, 31 and 63 also run in f64 from the same
+      inputs and stored values (tests/f64_block.py); rounded once to f16 that
+      is the exact block, and the GPU's elements more than 2 f16 steps from it
+      may exceed the f32 oracle's by at most 0.01% of the block's elements
+      (both distributions are reported).
 
     The random 64-block model amplifies a one-step f16 difference anywhere in
     the residual stream into about 1e-2 at the logits, so no implementation
@@ -243,6 +251,8 @@ def test_config2_27b_full_depth_greedy_steps(model27b):
         assert np.array_equal(entry, emb)                       # gather + round is exact
         worst_scaled = worst_own = 0.0
         within1, within2 = [], []
+        floor64 = {}
+        segs = [(s, int(T), CHECK_STEPS, CHECK_STEPS * s) for s, T in enumerate(pasts)]
         rows_in = emb
         for b in range(L_):
             hj = [dict(slot=s, past=int(T), n=CHECK_STEPS, hidden=rows_in[CHECK_STEPS * s:CHECK_STEPS * (s + 1)])
@@ -253,6 +263,18 @@ def test_config2_27b_full_depth_greedy_steps(model27b):
             worst_scaled, worst_own = max(worst_scaled, float(scaled.max())), max(worst_own, float(own.max()))
             within1.append(float((own <= 1).mean()))
             within2.append(float((own <= 2).mean()))
+            if b in F64_BLOCKS:
+                # the exact block for the same inputs: the oracle's f32 floor and the GPU beside it
+                sm._load(b)
+                exact = F.f16_bits(F.block_f64(sm, b, L.from_f16(rows_in).astype(np.float64), segs))
+                sm.w["layers"][b] = None
+                sm.K[b] = sm.V[b] = None
+                floor64[b] = {"oracle": F.summary(F.steps_from_exact(after[b], exact)),
+                              "gpu": F.summary(F.steps_from_exact(got, exact))}
+                # the GPU's tail beyond 2 steps of the exact block is the f32
+                # oracle's own, to within 0.01% of the elements
+                assert floor64[b]["gpu"]["within_2"] >= floor64[b]["oracle"]["within_2"] - 1e-4, (b, floor64[b])
+                _progress(f"configs[2] f64 block {b} done")
             rows_in = after[b]
         _progress("configs[2] per-block checks done")
 
@@ -280,6 +302,7 @@ def test_config2_27b_full_depth_greedy_steps(model27b):
                     "per_block_max_steps_at_scale": worst_scaled, "per_block_max_steps_own": worst_own,
                     "per_block_min_frac_within_one_own_step": min(within1),
                     "per_block_min_frac_within_two_own_steps": min(within2),
+                    "f64_blocks_own_steps_from_exact": floor64,
                     "ids_equal": sum(int(toks[k + 1][s]) == _top2(want[s]["logits"][k])[0]
                                      for k in range(CHECK_STEPS) for s in range(CHATS)),
                     "rows_inside_noise": near})
