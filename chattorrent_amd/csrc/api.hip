@@ -129,6 +129,8 @@ struct cc_ctx {
     float* dec_vals = nullptr;
     uint32_t* dec_ids = nullptr;
     size_t dec_cap = 0;
+    int32_t* dec_plan = nullptr;   // cc_decode_steps: every pass's page pops
+    size_t dec_plan_cap = 0;       // (int32 entries)
     uint16_t* d_hbits = nullptr;
     // per-step metadata (device) and its pinned host staging
     uint8_t* d_meta = nullptr;
@@ -1683,33 +1685,57 @@ cc_status cc_decode_steps(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_
         ctx->dec_ids = i;
         ctx->dec_cap = per * steps;
     }
+    // Pages as a host loop of cc_step calls takes them (take_pages, after
+    // ensurePages, web/model/model.js:185-202): pass k pops, job by job in
+    // order, the pages its past + k + 1 tokens need beyond those it owns.
+    // Every pass's pops are planned here, (slot, owned, new pages, prefix in
+    // the pass) for each job that takes one, and an allocating pass runs its
+    // plan first, so the frames end with the page tables the Runner's passes
+    // give them.
+    std::vector<int32_t> pplan;
+    std::vector<int> pass_off(steps + 1, 0), pass_top(steps, 0);
+    std::vector<int> own(ctx->owned);
+    int top = ctx->top;
+    for (int k = 0; k < steps; k++) {
+        pass_off[k] = (int)(pplan.size() / 4);
+        pass_top[k] = top;
+        int pre = 0;
+        for (int j = 0; j < njobs; j++) {
+            const int slot = jobs[j].slot;
+            const int nw = ceil_div(jobs[j].past + k + 1, ctx->geom.page) - own[slot];
+            if (nw <= 0) continue;
+            pplan.insert(pplan.end(), {slot, own[slot], nw, pre});
+            pre += nw;
+            own[slot] += nw;
+        }
+        if (pre > top)
+            return fail(ctx, CC_BUSY, "no KV page free for pass " + std::to_string(k) + " of the loop (" +
+                                          std::to_string(pre) + " needed, " + std::to_string(top) + " free)");
+        top -= pre;
+    }
+    pass_off[steps] = (int)(pplan.size() / 4);
+    if (pplan.size() > ctx->dec_plan_cap) {
+        int32_t* dp = nullptr;
+        HIPCHK(dfree(ctx, ctx->dec_plan, ctx->dec_plan_cap * 4, &ctx->scratch_bytes));
+        ctx->dec_plan = nullptr;
+        ctx->dec_plan_cap = 0;
+        HIPCHK(dalloc(ctx, &dp, pplan.size() * 4, &ctx->scratch_bytes));
+        ctx->dec_plan = dp;
+        ctx->dec_plan_cap = pplan.size();
+    }
     MetaLayout ml = meta_layout(ctx);
     uint8_t* hm = ctx->h_meta;
     PackJob* pk = (PackJob*)(hm + ml.pack);
     int32_t* ids0 = (int32_t*)(hm + ml.ids);
-    std::vector<std::pair<int, int>> want;
-    int32_t* plan = (int32_t*)(hm + ml.plan);
-    int total = 0;
     for (int j = 0; j < njobs; j++) {
         pk[j] = PackJob{jobs[j].slot, jobs[j].past, 1, 1, 0, -1};
         ids0[j] = jobs[j].ids[0];
-        want.push_back({jobs[j].slot, jobs[j].past + steps});
-        const int need = ceil_div(jobs[j].past + steps, ctx->geom.page);
-        const int nw = std::max(0, need - ctx->owned[jobs[j].slot]);
-        plan[4 * j] = jobs[j].slot;
-        plan[4 * j + 1] = ctx->owned[jobs[j].slot];
-        plan[4 * j + 2] = nw;
-        plan[4 * j + 3] = total;
-        total += nw;
     }
     hipStream_t st = ctx->stream;
     HIPCHK(hipEventRecord(ctx->ev0, st));
     HIPCHK(hipMemcpyAsync(ctx->d_meta, hm, ml.hidden, hipMemcpyHostToDevice, st));
-    cc_status ps = take_pages(ctx, want, (int32_t*)(ctx->d_meta + ml.plan), plan, nullptr);
-    if (ps != CC_OK) {
-        hipStreamSynchronize(st);
-        return ps;
-    }
+    if (!pplan.empty())
+        HIPCHK(hipMemcpyAsync(ctx->dec_plan, pplan.data(), pplan.size() * 4, hipMemcpyHostToDevice, st));
     const QTensor& hw = d.tied ? ctx->wte : ctx->lm_head;
     QTensor emb = ctx->wte;
     emb.K = d.hidden;
@@ -1718,6 +1744,8 @@ cc_status cc_decode_steps(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_
     std::vector<cc_job> cur(jobs, jobs + njobs);
     for (int k = 0; k < steps; k++) {
         // step k: every job one row further, fed the token step k-1 sampled
+        launch_alloc_pages(st, ctx->dec_plan + 4 * (size_t)pass_off[k], pass_off[k + 1] - pass_off[k],
+                           ctx->free_stack, pass_top[k], ctx->page_table, ctx->max_pages);
         StepPlan p;
         plan_jobs(ctx, cur.data(), njobs, p, true);
         pack_on_device(ctx, ml, njobs, k, true);
@@ -1732,6 +1760,8 @@ cc_status cc_decode_steps(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_
         for (auto& j : cur) j.past++;
     }
     ctx->head_rows = S;
+    ctx->owned = own;
+    ctx->top = top;
     HIPCHK(hipMemcpyAsync(top_vals, ctx->dec_vals, per * steps * 4, hipMemcpyDeviceToHost, st));
     HIPCHK(hipMemcpyAsync(top_ids, ctx->dec_ids, per * steps * 4, hipMemcpyDeviceToHost, st));
     HIPCHK(hipEventRecord(ctx->ev1, st));

@@ -187,10 +187,12 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
  * (web/route.js:865-952) without a host round trip between passes: every
  * job is one row, sampled; pass k runs each job at past + k with the token
  * pass k-1 sampled (column 0 of its candidates; pass 0 takes jobs[j].ids[0]),
- * and packs its rows and attention work on the device. The pages for
- * past + steps tokens are taken first. Outputs: top_vals / top_ids
- * [steps][njobs][topk], best first. Each pass's results equal cc_step's for
- * the same jobs. A context holding every position of a full-attention model
+ * and packs its rows and attention work on the device. Each pass takes the
+ * pages its jobs newly need, job by job, as a cc_step of that pass would, so
+ * the frames' page tables and the pool end as after `steps` cc_step calls
+ * (CC_BUSY, before anything runs, when the pool cannot supply them).
+ * Outputs: top_vals / top_ids [steps][njobs][topk], best first. Each pass's
+ * results equal cc_step's for the same jobs. A context holding every position of a full-attention model
  * without an MTP head. */
 cc_status cc_decode_steps(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t steps, int32_t topk,
                           float* top_vals, uint32_t* top_ids);

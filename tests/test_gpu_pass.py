@@ -376,3 +376,48 @@ def test_decode_steps_equal_step_by_step(smol):
         assert np.array_equal(i, ids[k]), k
         assert np.array_equal(v.view(np.uint32), vals[k].view(np.uint32)), k
         toks = [int(x) for x in i[:, 0]]
+
+
+def test_decode_steps_take_pages_as_step_by_step(gpu):
+    """cc_decode_steps takes each pass's pages job by job as that pass's
+    cc_step would (ensurePages in job order, web/model/model.js:185-202), so
+    after a loop whose jobs cross page boundaries at different passes the
+    device page tables and the free count equal the oracle pool's replay of
+    the passes one by one; the tokens equal a cc_step loop's."""
+    from chattorrent_amd.ccdecode import Context
+    from oracle.model import PagePool
+    d = configs.with_layers(configs.SMOLLM2, 2)
+    max_pages, frames_n = 8, 5
+    pasts = [60, 127, 5, 190]            # cross a page at passes 4, 1, 59 and 2
+    steps = 70
+    slots = [3, 0, 4, 1]                 # job order differs from slot order
+    c = Context(d, n_max=max_pages * 64, t_max=8, slots=4, sessions=frames_n, max_jobs=4)
+    pool = PagePool(4 * max_pages)
+    frames = [{"pages": np.zeros(max_pages, np.uint32), "owned": [], "max_pages": max_pages}
+              for _ in range(frames_n)]
+    try:
+        c.fill_random(SEED)
+        for s, T in zip(slots, pasts):
+            c.fill_random_kv(s, T, SEED, s + 1)
+            assert pool.ensure(frames[s], T)
+        first = [int(x) for x in _ids(4, d["vocab"], 95)]
+        _, ids = c.decode_steps(slots, pasts, first, steps, topk=1)
+        for k in range(steps):
+            for s, T in zip(slots, pasts):
+                assert pool.ensure(frames[s], T + k + 1)
+        for s in range(frames_n):
+            assert list(c.pages(s)) == frames[s]["owned"], s
+        assert c.free_pages() == len(pool.free)
+        # the same passes one cc_step at a time give the same tokens
+        for s in slots:
+            c.release(s)
+        for s, T in zip(slots, pasts):
+            c.fill_random_kv(s, T, SEED, s + 1)
+        toks = first
+        for k in range(steps):
+            _, i = c.step([dict(slot=s, past=T + k, n=1, ids=[toks[j]], sampled=1)
+                           for j, (s, T) in enumerate(zip(slots, pasts))], topk=1)
+            assert np.array_equal(i[:, 0], ids[k][:, 0]), k
+            toks = [int(x) for x in i[:, 0]]
+    finally:
+        c.close()
