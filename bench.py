@@ -132,7 +132,7 @@ def step_roofline(bytes_per_step, ms):
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_step": bytes_per_step}
 
 
-def gemm_roofline(prof, steps):
+def gemm_roofline(prof, steps, kernel="k_gemm_lx (all q8 projections + LM head)"):
     """The dominant kernel: the q8 matmul (every projection and the LM head),
     its launches timed back-to-back between HIP events on the library's
     stream (cc_profile); achieved = algorithmic bytes / summed launch time."""
@@ -145,7 +145,7 @@ def gemm_roofline(prof, steps):
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "traffic_source": "profiles/k_gemm_lx_c3_traffic.md: FETCH_SIZE + WRITE_SIZE counter runs of configs[2] "
                               "(each scaled by a plain copy), HBM bytes per launch in that step's mix",
-            "kernel": "k_gemm_lx (all q8 projections + LM head)",
+            "kernel": kernel,
             "avg_launch_us": round(g_ms * 1000.0 / max(g_n, 1), 2),
             "bytes_per_launch": round(g_b / max(g_n, 1)),
             "per_kind": {k: {"ms_per_step": round(v[0] / steps, 4), "launches": v[1],
@@ -390,7 +390,8 @@ def bench_c4(args, ceil):
         timed.append(state["pasts"].copy())
         step()
     ms = (time.perf_counter() - t0) * 1000.0 / args.steps
-    roof = gemm_roofline(profiled(ctx, step, args.prof_steps), args.prof_steps)
+    roof = gemm_roofline(profiled(ctx, step, args.prof_steps), args.prof_steps,
+                         kernel="k_gemm_tm (all q8 projections at 128 rows; the LM head too)")
     ctx.close()
     b = float(np.mean([step_bytes(d, [(int(p), n) for p in ps]) for ps in timed]))
     line = base_line(args, "speculative verify rows/s, 16 chats x 8 rows, 27B q8; % of HBM roofline",
