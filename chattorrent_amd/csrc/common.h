@@ -123,7 +123,11 @@ __device__ static inline half8_t dequant8_biased(uint32_t lo, uint32_t hi) {
 }
 
 // x ≈ hi + lo with hi = f16(x) (nearest-even) and lo = f16(x - hi); the
-// difference x - hi is exact in f32, so hi + lo carries ~22 significant bits.
+// difference x - hi is exact in f32, so hi + lo carries ~22 significant bits
+// while lo stays a normal f16 (|x| >= 2^-3; below that lo's absolute step is
+// 2^-24). Attention's Q operand uses it: its values are of order 1 and its
+// scores are sums of such products, where that step is below f32 rounding.
+// The matmul operands and P.V use split_hilo_x.
 // x is made opaque first: when x is a product, the compiler may otherwise fold
 // the multiply into the f16 conversion (v_fma_mix, one rounding) for one use
 // of hi and convert the f32 product (two roundings) for another, and the two
@@ -157,22 +161,10 @@ __device__ static inline half8_t lo_weight8(half8_t b) {
     return b * s;
 }
 
-// Two values at once, as split_hilo (nearest-even hi, lo = f16 of the exact
-// remainder), returned packed as two f16 pairs. (Truncating the pair with
-// v_cvt_pkrtz saves two instructions but biases every lo toward zero, and the
-// bias adds up over a long softmax sum.)
-__device__ static inline void split_hilo2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
-    typedef float f2_t __attribute__((ext_vector_type(2)));
-    asm("" : "+v"(x0), "+v"(x1));
-    const f2_t x = {x0, x1};
-    const half2_t h = __builtin_convertvector(x, half2_t);   // one packed conversion
-    const f2_t hb = __builtin_convertvector(h, f2_t);        // back from the packed halves
-    const half2_t l = __builtin_convertvector(x - hb, half2_t);
-    hi = __builtin_bit_cast(uint32_t, h);
-    lo = __builtin_bit_cast(uint32_t, l);
-}
-
-// split_hilo2 with the scaled lo of split_hilo_x.
+// Two values at once, as split_hilo_x (nearest-even hi, lo = f16 of the
+// exact remainder times 2^11), returned packed as two f16 pairs. (Truncating
+// the pair with v_cvt_pkrtz saves two instructions but biases every lo toward
+// zero, and the bias adds up over a long softmax sum.)
 __device__ static inline void split_hilo2_x(float x0, float x1, uint32_t& hi, uint32_t& lo) {
     typedef float f2_t __attribute__((ext_vector_type(2)));
     asm("" : "+v"(x0), "+v"(x1));
