@@ -448,7 +448,7 @@ def bench_c5(args, ceil):
     t0 = time.perf_counter()
     for k in range(args.steps):
         one_step()
-        if k % 50 == 49:
+        if k % 250 == 249:
             log(f"c5: {k + 1} steps, {len(churn.chats)} chats")
     secs = time.perf_counter() - t0
     prof = profiled(ctx, one_step, args.prof_steps)
@@ -649,7 +649,7 @@ def bench_hybrid(args, ceil):
 
 
 CONFIGS = {"c1": bench_c1, "c2": bench_c2, "c3": bench_c3, "c4": bench_c4, "c5": bench_c5}
-DEFAULT_STEPS = {"c1": 32, "c2": 50, "c3": 128, "c4": 10, "c5": 200}
+DEFAULT_STEPS = {"c1": 32, "c2": 50, "c3": 128, "c4": 10, "c5": 2000}   # c5: configs[4]'s 2000 steps
 
 
 def main():
