@@ -366,10 +366,11 @@ void prof_mark(cc_ctx* ctx, int kind, int n, double bytes, F&& launches) {
         if (hipEventCreateWithFlags(&ev, hipEventDisableSystemFence) != hipSuccess) return;
         ctx->pev.push_back(ev);
     }
-    hipEventRecord(ctx->pev[e], ctx->stream);
+    // a mark whose events cannot be recorded is left out of the profile
+    const bool a = hipEventRecord(ctx->pev[e], ctx->stream) == hipSuccess;
     launches();
-    hipEventRecord(ctx->pev[e + 1], ctx->stream);
-    ctx->marks.push_back(cc_ctx::Mark{kind, e, e + 1, n, bytes});
+    const bool b = hipEventRecord(ctx->pev[e + 1], ctx->stream) == hipSuccess;
+    if (a && b) ctx->marks.push_back(cc_ctx::Mark{kind, e, e + 1, n, bytes});
 }
 
 void prof_collect(cc_ctx* ctx) {
@@ -402,15 +403,15 @@ const char* cc_last_error(const cc_ctx* ctx) { return ctx ? ctx->err.c_str() : "
 
 void cc_destroy(cc_ctx* ctx) {
     if (!ctx) return;
-    if (ctx->stream) hipStreamSynchronize(ctx->stream);
-    for (void* p : ctx->allocs) hipFree(p);
-    if (ctx->h_meta) hipHostFree(ctx->h_meta);
-    if (ctx->h_out) hipHostFree(ctx->h_out);
-    if (ctx->h_chain) hipHostFree(ctx->h_chain);
-    if (ctx->ev0) hipEventDestroy(ctx->ev0);
-    if (ctx->ev1) hipEventDestroy(ctx->ev1);
-    for (hipEvent_t e : ctx->pev) hipEventDestroy(e);
-    if (ctx->stream) hipStreamDestroy(ctx->stream);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (void* p : ctx->allocs) (void)hipFree(p);
+    if (ctx->h_meta) (void)hipHostFree(ctx->h_meta);
+    if (ctx->h_out) (void)hipHostFree(ctx->h_out);
+    if (ctx->h_chain) (void)hipHostFree(ctx->h_chain);
+    if (ctx->ev0) (void)hipEventDestroy(ctx->ev0);
+    if (ctx->ev1) (void)hipEventDestroy(ctx->ev1);
+    for (hipEvent_t e : ctx->pev) (void)hipEventDestroy(e);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
 }
 
@@ -821,8 +822,8 @@ cc_status cc_upload(cc_ctx* ctx, int32_t layer, int32_t tensor, const void* data
     HIPCHK(hipMemcpy(ds, sv.data(), sv.size(), hipMemcpyHostToDevice));
     launch_tile_q8(ctx->stream, dc, ds, N, K, *q, row_tile0);
     HIPCHK(hipStreamSynchronize(ctx->stream));
-    hipFree(dc);
-    hipFree(ds);
+    (void)hipFree(dc);
+    (void)hipFree(ds);
     return CC_OK;
 }
 
@@ -996,7 +997,7 @@ static cc_status kv_io(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot, 
         launch_kv_from_ref(ctx->stream, pool, ctx->page_table, slot, head, t0, t1, ctx->geom, which, dbuf);
         HIPCHK(hipStreamSynchronize(ctx->stream));
     }
-    hipFree(dbuf);
+    (void)hipFree(dbuf);
     return CC_OK;
 }
 
@@ -1558,7 +1559,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
     pack_on_device(ctx, ml, njobs, 0, head);
     cc_status ps = take_pages(ctx, want, (int32_t*)(ctx->d_meta + ml.plan), (int32_t*)(hm + ml.plan), status);
     if (ps != CC_OK) {
-        hipStreamSynchronize(st);
+        (void)hipStreamSynchronize(st);   // the refusal is the status reported
         return ps;
     }
     // Embedding (position 0) or the rows handed in.
@@ -1604,7 +1605,7 @@ cc_status cc_step(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_t at, in
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(take_launch_error());
     float ms = 0;
-    hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1);
+    if (hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1) != hipSuccess) ms = 0;
     ctx->last_ms = ms;
     prof_collect(ctx);
     ctx->passes++;
@@ -1768,7 +1769,7 @@ cc_status cc_decode_steps(cc_ctx* ctx, const cc_job* jobs, int32_t njobs, int32_
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(take_launch_error());
     float ms = 0;
-    hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1);
+    if (hipEventElapsedTime(&ms, ctx->ev0, ctx->ev1) != hipSuccess) ms = 0;
     ctx->last_ms = ms;
     ctx->passes += steps;
     ctx->rows += (int64_t)steps * njobs;
@@ -1908,7 +1909,7 @@ cc_status cc_op_matmul_q8(cc_ctx* ctx, const float* X, int32_t M, int32_t K, con
     HIPCHK(take_launch_error());
     HIPCHK(hipMemcpy(Y, dY, (size_t)M * N * 4, hipMemcpyDeviceToHost));
     for (void* v : {(void*)q.codes, (void*)dW, (void*)dS, (void*)dX, (void*)dXp, (void*)dP, (void*)dY})
-        hipFree(v);
+        (void)hipFree(v);
     return CC_OK;
 }
 
@@ -1920,7 +1921,7 @@ cc_status cc_op_round_f16(cc_ctx* ctx, float* a, int64_t n) {
     launch_round_f16(ctx->stream, dA, n);
     HIPCHK(hipStreamSynchronize(ctx->stream));
     HIPCHK(hipMemcpy(a, dA, (size_t)n * 4, hipMemcpyDeviceToHost));
-    hipFree(dA);
+    (void)hipFree(dA);
     return CC_OK;
 }
 
@@ -1939,7 +1940,7 @@ cc_status cc_op_topk(cc_ctx* ctx, const float* logits, int32_t rows, int32_t V, 
     HIPCHK(hipStreamSynchronize(ctx->stream));
     HIPCHK(hipMemcpy(vals, dv, (size_t)rows * M * 4, hipMemcpyDeviceToHost));
     HIPCHK(hipMemcpy(ids, di, (size_t)rows * M * 4, hipMemcpyDeviceToHost));
-    for (void* v : {(void*)dL, (void*)a, (void*)b, (void*)dv, (void*)di}) hipFree(v);
+    for (void* v : {(void*)dL, (void*)a, (void*)b, (void*)dv, (void*)di}) (void)hipFree(v);
     return CC_OK;
 }
 
@@ -1976,7 +1977,7 @@ cc_status cc_op_rmsnorm(cc_ctx* ctx, const float* x, const float* w, int32_t T, 
     HIPCHK(hipStreamSynchronize(ctx->stream));
     HIPCHK(take_launch_error());
     HIPCHK(hipMemcpy(y, dy, (size_t)T * H * 4, hipMemcpyDeviceToHost));
-    for (void* v : {(void*)dx, (void*)dw, (void*)dy}) hipFree(v);
+    for (void* v : {(void*)dx, (void*)dw, (void*)dy}) (void)hipFree(v);
     return CC_OK;
 }
 
@@ -2044,7 +2045,7 @@ cc_status cc_op_store_kv(cc_ctx* ctx, int32_t layer, int32_t which, int32_t slot
                    (const JobDev*)(ctx->d_meta + ml.jobs), d.n_heads, ctx->group, ctx->geom, ctx->tbl, ctx->rot,
                    L.kpool, L.vpool, ctx->page_table, ctx->qp, RowScale{}, 0, 1);
     HIPCHK(hipStreamSynchronize(ctx->stream));
-    hipFree(dr);
+    (void)hipFree(dr);
     for (int h = 0; h < d.n_kv_heads; h++) {
         cc_status r = kv_io(ctx, layer, other, slot, h, T_past, T_past + T_new, nullptr, saved[h].data());
         if (r != CC_OK) return r;
@@ -2087,7 +2088,7 @@ cc_status cc_op_attend(cc_ctx* ctx, int32_t layer, int32_t slot, const float* q,
     HIPCHK(hipStreamSynchronize(st));
     HIPCHK(take_launch_error());
     HIPCHK(hipMemcpy(out, dctx, (size_t)n * qd * 4, hipMemcpyDeviceToHost));
-    for (void* v : {(void*)dr, (void*)dctx, (void*)dXp}) hipFree(v);
+    for (void* v : {(void*)dr, (void*)dctx, (void*)dXp}) (void)hipFree(v);
     return CC_OK;
 }
 

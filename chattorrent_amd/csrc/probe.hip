@@ -63,14 +63,14 @@ int run(int device, size_t bytes, int iters, bool copy, double* gbps) {
     if (hipGetLastError() != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess || ms <= 0.f) goto done;
     *gbps = (copy ? 2.0 : 1.0) * (double)(n16 * 16) * iters / (ms / 1000.0) / 1e9;
     rc = 0;
-done:
-    if (st) hipStreamSynchronize(st);
-    if (e0) hipEventDestroy(e0);
-    if (e1) hipEventDestroy(e1);
-    if (st) hipStreamDestroy(st);
-    if (a) hipFree(a);
-    if (b) hipFree(b);
-    if (sink) hipFree(sink);
+done:   // releases: a failure here leaves rc as it is
+    if (st) (void)hipStreamSynchronize(st);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (st) (void)hipStreamDestroy(st);
+    if (a) (void)hipFree(a);
+    if (b) (void)hipFree(b);
+    if (sink) (void)hipFree(sink);
     return rc;
 }
 
