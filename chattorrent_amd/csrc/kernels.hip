@@ -449,25 +449,33 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm(const uint8_t* __rest
                 bl[h][nt] = lo_weight8(b[h][nt]);
                 scale[h][nt] = rec_scale<F32S>(sv[nt], h);
             }
+        // per half-group, every m-tile's MFMA pair first and the scale FMAs
+        // after them, so no FMA waits on the MFMA issued just before it; each
+        // output's operations and their order are those of k_gemm_lx
 #pragma unroll
-        for (int mt = 0; mt < MTW; mt++) {
-            u32x4 xv[4];
+        for (int h = 0; h < 2; h++) {
+            u32x4 xv[MTW][2];
 #pragma unroll
-            for (int q = 0; q < 4; q++) xv[q] = xs[buf][(mw + mt) * 4 + q][lane];
+            for (int mt = 0; mt < MTW; mt++)
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                float4_t pp[NT];
+                for (int q = 0; q < 2; q++) xv[mt][q] = xs[buf][(mw + mt) * 4 + 2 * h + q][lane];
+            float4_t pp[MTW][NT];
+#pragma unroll
+            for (int mt = 0; mt < MTW; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
-                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h]), b[h][nt], float4_t{0.f, 0.f, 0.f, 0.f});
+                    pp[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[mt][0]), b[h][nt], float4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int mt = 0; mt < MTW; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
-                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h + 1]), bl[h][nt], pp[nt]);
+                    pp[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[mt][1]), bl[h][nt], pp[mt][nt]);
+#pragma unroll
+            for (int mt = 0; mt < MTW; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) seg[mt][nt][e] = __builtin_fmaf(scale[h][nt], pp[nt][e], seg[mt][nt][e]);
-            }
+                    for (int e = 0; e < 4; e++) seg[mt][nt][e] = __builtin_fmaf(scale[h][nt], pp[mt][nt][e], seg[mt][nt][e]);
         }
     };
     int u = 0;
@@ -639,25 +647,33 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm_sum(const uint8_t* __
                 bl[h][nt] = lo_weight8(b[h][nt]);
                 scale[h][nt] = rec_scale<F32S>(sv[nt], h);
             }
+        // per half-group, every m-tile's MFMA pair first and the scale FMAs
+        // after them, so no FMA waits on the MFMA issued just before it; each
+        // output's operations and their order are those of k_gemm_lx
 #pragma unroll
-        for (int mt = 0; mt < MTW; mt++) {
-            u32x4 xv[4];
+        for (int h = 0; h < 2; h++) {
+            u32x4 xv[MTW][2];
 #pragma unroll
-            for (int q = 0; q < 4; q++) xv[q] = xs[buf][(mw + mt) * 4 + q][lane];
+            for (int mt = 0; mt < MTW; mt++)
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                float4_t pp[NT];
+                for (int q = 0; q < 2; q++) xv[mt][q] = xs[buf][(mw + mt) * 4 + 2 * h + q][lane];
+            float4_t pp[MTW][NT];
+#pragma unroll
+            for (int mt = 0; mt < MTW; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
-                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h]), b[h][nt], float4_t{0.f, 0.f, 0.f, 0.f});
+                    pp[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[mt][0]), b[h][nt], float4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int mt = 0; mt < MTW; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
-                    pp[nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[2 * h + 1]), bl[h][nt], pp[nt]);
+                    pp[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[mt][1]), bl[h][nt], pp[mt][nt]);
+#pragma unroll
+            for (int mt = 0; mt < MTW; mt++)
 #pragma unroll
                 for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) seg[mt][nt][e] = __builtin_fmaf(scale[h][nt], pp[nt][e], seg[mt][nt][e]);
-            }
+                    for (int e = 0; e < 4; e++) seg[mt][nt][e] = __builtin_fmaf(scale[h][nt], pp[mt][nt][e], seg[mt][nt][e]);
         }
         if (u + 1 == cend) {   // the plane's value (its last segment folded in) joins the sum
 #pragma unroll
