@@ -170,9 +170,11 @@ __device__ static inline void split_hilo2_x(float x0, float x1, uint32_t& hi, ui
     asm("" : "+v"(x0), "+v"(x1));
     const f2_t x = {x0, x1};
     const half2_t h = __builtin_convertvector(x, half2_t);
-    const f2_t hb = __builtin_convertvector(h, f2_t);
-    const f2_t r = x - hb;
-    const f2_t rs = {r[0] * HILO_LO_SHIFT, r[1] * HILO_LO_SHIFT};
+    // (x - hi) * 2^11 as one FMA from hi's f16 value (v_fma_mix): 2^11 x and
+    // 2^11 x - 2^11 hi are exact in f32, so the bits are those of the
+    // subtraction followed by the scaling
+    const f2_t rs = {__builtin_fmaf((float)h[0], -HILO_LO_SHIFT, x0 * HILO_LO_SHIFT),
+                     __builtin_fmaf((float)h[1], -HILO_LO_SHIFT, x1 * HILO_LO_SHIFT)};
     const half2_t l = __builtin_convertvector(rs, half2_t);
     hi = __builtin_bit_cast(uint32_t, h);
     lo = __builtin_bit_cast(uint32_t, l);
