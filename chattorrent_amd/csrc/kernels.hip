@@ -2112,31 +2112,55 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
             for (int q = 0; q < SCL; q++) sc[q] = __builtin_amdgcn_raw_buffer_load_b128(rv, vso[q], 64 * D, 0);
         }
     };
-    if (p0 < p1) load(p0);
-    for (int p = p0; p < p1; p++) {
-        const int B = (p - p0) & 1;
-        u32x4* kf = kf_s + B * 4 * NG * 64;
-        u32x4* vf = vf_s + B * DT * 2 * 64;
-        float* ksl = ks_s + B * 256 * SCL;
-        float* vsl = vs_s + B * 256 * SCL;
+    // A block with an empty slot (a job of 3 m-tiles or fewer in its last
+    // block, as a verify of 8 rows x 5 heads) gives its idle wave 3 the whole
+    // page: it loads and dequantises everything, the same fragments the four
+    // quarters would be, while the other waves only compute. Its page loop
+    // has the same barriers as theirs.
+    const int mtq = (it0.n * group + 15) >> 4;
+    const bool spare = mtq - it0.mt < 4;
+    if (spare && wv == 3) {
+        u32x4 fk[4][NG / 2], fv[DT], fs[2][SCL];
+        auto load_all = [&](int p) {
+            const auto rk = page_rsrc(kpool, p), rv = page_rsrc(vpool, p);
 #pragma unroll
-        for (int q = 0; q < NG / 2; q++) {
-            kf[(wv * NG + 2 * q) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(kc[q][0], kc[q][1]));
-            kf[(wv * NG + 2 * q + 1) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(kc[q][2], kc[q][3]));
-        }
+            for (int tt = 0; tt < 4; tt++)
 #pragma unroll
-        for (int i = 0; i < DQ; i++) {
-            vf[((wv * DQ + i) * 2) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(vc[i][0], vc[i][1]));
-            vf[((wv * DQ + i) * 2 + 1) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(vc[i][2], vc[i][3]));
-        }
-        if (wv == 0) {
+                for (int q = 0; q < NG / 2; q++)
+                    fk[tt][q] = __builtin_amdgcn_raw_buffer_load_b128(rk, vk, tt * 16 * D + 16 * q, 0);
 #pragma unroll
-            for (int q = 0; q < SCL; q++) *(u32x4*)&ksl[256 * q + lane * 4] = sc[q];
-        } else if (wv == 1) {
+            for (int dt = 0; dt < DT; dt++) fv[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, dt * 256, 0);
 #pragma unroll
             for (int q = 0; q < SCL; q++) {
-                u32x4 v = sc[q];
-                if (p * 64 + 64 > T_act) {   // stale scales past the job's tokens go in as zero
+                fs[0][q] = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16, 64 * D + 1024 * q, 0);
+                fs[1][q] = __builtin_amdgcn_raw_buffer_load_b128(rv, vso[q], 64 * D, 0);
+            }
+        };
+        if (p0 < p1) load_all(p0);
+        for (int p = p0; p < p1; p++) {
+            const int B = (p - p0) & 1;
+            u32x4* kf = kf_s + B * 4 * NG * 64;
+            u32x4* vf = vf_s + B * DT * 2 * 64;
+            float* ksl = ks_s + B * 256 * SCL;
+            float* vsl = vs_s + B * 256 * SCL;
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                for (int q = 0; q < NG / 2; q++) {
+                    kf[(tt * NG + 2 * q) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(fk[tt][q][0], fk[tt][q][1]));
+                    kf[(tt * NG + 2 * q + 1) * 64 + lane] =
+                        __builtin_bit_cast(u32x4, dequant8_biased(fk[tt][q][2], fk[tt][q][3]));
+                }
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) {
+                vf[(dt * 2) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(fv[dt][0], fv[dt][1]));
+                vf[(dt * 2 + 1) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(fv[dt][2], fv[dt][3]));
+            }
+#pragma unroll
+            for (int q = 0; q < SCL; q++) {
+                *(u32x4*)&ksl[256 * q + lane * 4] = fs[0][q];
+                u32x4 v = fs[1][q];
+                if (p * 64 + 64 > T_act) {
                     const int t0 = p * 64 + 16 * (lane & 3) + 4 * (((256 * q + lane * 4) >> 4) & 3);
 #pragma unroll
                     for (int e = 0; e < 4; e++)
@@ -2144,9 +2168,48 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
                 }
                 *(u32x4*)&vsl[256 * q + lane * 4] = v;
             }
+            __syncthreads();
+            if (p + 1 < p1) load_all(p + 1);
+        }
+        return;   // wave 3's slot is empty
+    }
+    if (p0 < p1 && !spare) load(p0);
+    for (int p = p0; p < p1; p++) {
+        const int B = (p - p0) & 1;
+        u32x4* kf = kf_s + B * 4 * NG * 64;
+        u32x4* vf = vf_s + B * DT * 2 * 64;
+        float* ksl = ks_s + B * 256 * SCL;
+        float* vsl = vs_s + B * 256 * SCL;
+        if (!spare) {
+#pragma unroll
+            for (int q = 0; q < NG / 2; q++) {
+                kf[(wv * NG + 2 * q) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(kc[q][0], kc[q][1]));
+                kf[(wv * NG + 2 * q + 1) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(kc[q][2], kc[q][3]));
+            }
+#pragma unroll
+            for (int i = 0; i < DQ; i++) {
+                vf[((wv * DQ + i) * 2) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(vc[i][0], vc[i][1]));
+                vf[((wv * DQ + i) * 2 + 1) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(vc[i][2], vc[i][3]));
+            }
+            if (wv == 0) {
+#pragma unroll
+                for (int q = 0; q < SCL; q++) *(u32x4*)&ksl[256 * q + lane * 4] = sc[q];
+            } else if (wv == 1) {
+#pragma unroll
+                for (int q = 0; q < SCL; q++) {
+                    u32x4 v = sc[q];
+                    if (p * 64 + 64 > T_act) {   // stale scales past the job's tokens go in as zero
+                        const int t0 = p * 64 + 16 * (lane & 3) + 4 * (((256 * q + lane * 4) >> 4) & 3);
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (t0 + e >= T_act) v[e] = 0u;
+                    }
+                    *(u32x4*)&vsl[256 * q + lane * 4] = v;
+                }
+            }
         }
         __syncthreads();
-        if (p + 1 < p1) load(p + 1);   // the registers are free: the next page is on its way
+        if (p + 1 < p1 && !spare) load(p + 1);   // the registers are free: the next page is on its way
         if (!mine) continue;
         float pr[4][4];
         float pm = -INFINITY;
