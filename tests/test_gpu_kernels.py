@@ -258,6 +258,33 @@ def test_attend_verify_rows_equal_one_row_bitwise(gpu, shape):
     finally:
         c.close()
 
+
+@pytest.mark.parametrize("shape", ["27b", "d256"])
+def test_attend_block_with_empty_slot_equals_full_block(gpu, shape):
+    """A verify job of 8 rows (three m-tiles at a GQA group of 5, two at 4)
+    leaves its block's last slot empty, and that idle wave loads and
+    dequantises every page alone; in a job of four m-tiles each wave loads a
+    quarter. The first 8 rows of a four-m-tile job give the bits of the 8-row
+    job at the same position (rows past them only add masked tokens), across
+    a page and chunk boundary (positions 505..)."""
+    base = configs.M27B if shape == "27b" else D256
+    d = configs.with_layers(base, 1)
+    c = _ctx(gpu, d, n_max=1024, t_max=64, slots=2)
+    try:
+        D, nH, nKV = d["head_dim"], d["n_heads"], d["n_kv_heads"]
+        group = nH // nKV
+        full_n, part_n = 64 // group, 8
+        assert -(-full_n * group // 16) == 4 and -(-part_n * group // 16) < 4, (full_n, group)
+        P = 505
+        c.fill_random_kv(1, P + full_n, 5, 9)
+        q = np.random.default_rng(P + 1).standard_normal((full_n, nH * D)).astype(np.float32)
+        full = c.op_attend(0, 1, q, P)
+        part = c.op_attend(0, 1, q[:part_n], P)
+        assert np.array_equal(full[:part_n].view(np.uint32), part.view(np.uint32)), shape
+    finally:
+        c.close()
+
+
 def test_attend_ignores_stale_rows_past_the_context(gpu):
     """The pool rows past a job's tokens hold whatever an earlier session left
     there, NaN and inf included (web/model/kernels.js:1140-1310 never reads
