@@ -1938,13 +1938,23 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
                     for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(ks[r * NG + gg], pp[r], acc[r]);
                 }
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int tok = p * 64 + tt * 16 + 4 * j4 + r;
-                    const bool ok = tok < T_act && tok <= lim;
-                    pr[tt][r] = ok ? acc[r] * score_scale : -INFINITY;
-                    pm = fmaxf(pm, pr[tt][r]);
-                }
+                for (int r = 0; r < 4; r++) pr[tt][r] = acc[r] * score_scale;
             }
+            // every token up to the job's first new position is visible to every
+            // row (and below T_act): only a page past it needs the per-cell mask
+            if (p * 64 + 63 > it.past) {
+#pragma unroll
+                for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int tok = p * 64 + tt * 16 + 4 * j4 + r;
+                        if (!(tok < T_act && tok <= lim)) pr[tt][r] = -INFINITY;
+                    }
+            }
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) pm = fmaxf(pm, pr[tt][r]);
             const auto rvn = page_rsrc(vpool, pn);
             load_k(page_rsrc(kpool, pn), rvn);   // the K registers are free: start the next page
             __builtin_amdgcn_sched_barrier(0);
@@ -2232,13 +2242,23 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
                 for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(ks[r * NG + gg], pp[r], acc[r]);
             }
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int tok = p * 64 + tt * 16 + 4 * j4 + r;
-                const bool ok = tok < T_act && tok <= lim;
-                pr[tt][r] = ok ? acc[r] * score_scale : -INFINITY;
-                pm = fmaxf(pm, pr[tt][r]);
-            }
+            for (int r = 0; r < 4; r++) pr[tt][r] = acc[r] * score_scale;
         }
+        // every token up to the job's first new position is visible to every
+        // row (and below T_act): only a page past it needs the per-cell mask
+        if (p * 64 + 63 > it0.past) {
+#pragma unroll
+            for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int tok = p * 64 + tt * 16 + 4 * j4 + r;
+                    if (!(tok < T_act && tok <= lim)) pr[tt][r] = -INFINITY;
+                }
+        }
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) pm = fmaxf(pm, pr[tt][r]);
         pm = fmaxf(pm, __shfl_xor(pm, 16));
         pm = fmaxf(pm, __shfl_xor(pm, 32));
         const float mnew = fmaxf(mrow, pm);
