@@ -1941,7 +1941,9 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
                 for (int r = 0; r < 4; r++) pr[tt][r] = acc[r] * score_scale;
             }
             // every token up to the job's first new position is visible to every
-            // row (and below T_act): only a page past it needs the per-cell mask
+            // query row (and below T_act): only a page past it needs the per-cell
+            // mask. The m-tile's lanes past the job's rows then carry unmasked
+            // scores; they stay in their own lanes and MFMA columns, never written.
             if (p * 64 + 63 > it.past) {
 #pragma unroll
                 for (int tt = 0; tt < 4; tt++)
@@ -2245,7 +2247,9 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
             for (int r = 0; r < 4; r++) pr[tt][r] = acc[r] * score_scale;
         }
         // every token up to the job's first new position is visible to every
-        // row (and below T_act): only a page past it needs the per-cell mask
+        // query row (and below T_act): only a page past it needs the per-cell
+        // mask. The m-tile's lanes past the job's rows then carry unmasked
+        // scores; they stay in their own lanes and MFMA columns, never written.
         if (p * 64 + 63 > it0.past) {
 #pragma unroll
             for (int tt = 0; tt < 4; tt++)
