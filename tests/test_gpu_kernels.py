@@ -207,11 +207,15 @@ def test_attend_vs_oracle(gpu):
     """qk_scores_gqa + causal_softmax + attn_av_gqa (web/model/kernels.js:
     1140-1310) over random int8 pages: decode rows, a causal verify run, and a
     ragged last page. The GPU softmax is online (max, sum merged per page and
-    chunk); equal to the exact three-pass one within 2e-5 of max |out|."""
+    chunk); equal to the exact three-pass one within 2e-5 of max |out|. The
+    causal mask runs only on pages past the first new position, so the cases
+    put that position at a page's last token (63), at a page's first (64,
+    128) and one before a page boundary with rows across it (127)."""
     from oracle import lib as L
     from oracle import model as Mo
     for base, tokens, n in [(configs.SMOLLM2, 130, 1), (configs.M27B, 700, 1), (configs.M27B, 300, 8),
-                            (configs.SMOLLM2, 64, 37), (D256, 200, 1), (D256, 520, 6)]:
+                            (configs.SMOLLM2, 64, 37), (D256, 200, 1), (D256, 520, 6),
+                            (configs.M27B, 63, 1), (configs.M27B, 128, 1), (configs.SMOLLM2, 127, 3)]:
         d = configs.with_layers(base, 1)
         c = _ctx(gpu, d, n_max=1024, t_max=64, slots=2)
         try:
