@@ -2046,7 +2046,9 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
 // empty slot, mt < 0) and read the same pages. Each wave loads a quarter of
 // a page (K token tile w, V d-tiles w*DT/4 ..), dequantises it once into the
 // workgroup's LDS, and every wave's MFMAs read the fragments from there, so a
-// page is dequantised once instead of once per m-tile. One barrier a page;
+// page is dequantised once instead of once per m-tile; a block with an empty
+// slot has its idle wave 3 load and dequantise the whole page instead, while
+// the other waves only compute. One barrier a page;
 // the fragments are double-buffered (a wave past page p's barrier has
 // finished page p - 1, so page p + 1 may reuse that buffer). Every value and
 // every operation of a row is the one attn_item computes for it.
