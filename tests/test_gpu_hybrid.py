@@ -325,3 +325,49 @@ def test_hybrid_split_over_two_peers_bitwise(gpu):
     finally:
         for c in (whole, a, b):
             c.close()
+
+
+def test_hybrid_qwen38_widths_match_oracle(gpu):
+    """Qwen3.8-27B's own widths through four of its blocks (three Gated DeltaNet,
+    one full attention) against the oracle: hidden 5120, 24 query / 4 kv heads
+    of 256 with a quarter rotary, 16 key / 48 value heads of 128 in the linear
+    blocks, ffn 17408 and the untied 248320-row head. Prefill of two sessions,
+    a decode step, a 4-row verify (snap) beside a decode, its rollback keeping
+    2 rows, then a decode after it (web/model/model.js:411-527,
+    web/model/stage.js:1248-1283)."""
+    from chattorrent_amd import configs
+    d = dict(configs.QWEN38, n_layer=4, layer_types=configs.QWEN38["layer_types"][:4])
+    d.pop("mtp_vocab", None)
+    c, om = _pair(d, slots=2, n_max=512, t_max=64)
+    rng = np.random.default_rng(38)
+    V = d["vocab"]
+    errs = []
+
+    def check(vals, ids, want):
+        logits = _check(vals, ids, want, c)
+        errs.append(float(np.abs(c.read_logits(logits.shape[0]) - logits).max()))
+        return logits
+    try:
+        jobs = [dict(slot=0, past=0, n=20, ids=_ids(rng, 20, V), sampled=1, topk=4),
+                dict(slot=1, past=0, n=9, ids=_ids(rng, 9, V), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        logits = check(vals, ids, om.pass_(jobs))
+        nxt = [int(np.argmax(logits[0])), int(np.argmax(logits[1]))]
+        jobs = [dict(slot=s, past=p, n=1, ids=np.array([nxt[s]], np.int32), sampled=1, topk=4)
+                for s, p in ((0, 20), (1, 9))]
+        vals, ids = c.step(jobs, topk=4)
+        check(vals, ids, om.pass_(jobs))
+        jobs = [dict(slot=0, past=21, n=4, ids=_ids(rng, 4, V), sampled=4, topk=4, snap=True),
+                dict(slot=1, past=10, n=1, ids=_ids(rng, 1, V), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        check(vals, ids, om.pass_(jobs))
+        jobs = [dict(slot=0, past=23, n=1, ids=_ids(rng, 1, V), sampled=1, topk=4, keep=2),
+                dict(slot=1, past=11, n=1, ids=_ids(rng, 1, V), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        check(vals, ids, om.pass_(jobs))
+        jobs = [dict(slot=0, past=24, n=1, ids=_ids(rng, 1, V), sampled=1, topk=4)]
+        vals, ids = c.step(jobs, topk=4)
+        check(vals, ids, om.pass_(jobs))
+        print("qwen3.8 widths, max |logit - oracle| per pass:", [round(e, 5) for e in errs])
+    finally:
+        c.close()
