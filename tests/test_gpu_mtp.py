@@ -91,3 +91,39 @@ def test_mtp_prefill_chunk_keeps_its_last_row(gpu):
         assert _same_drafts(got, mh.draft(1, None, 7, 4, 2)) >= 1
     finally:
         c.close()
+
+
+def test_mtp_qwen38_widths_match_oracle(gpu):
+    """The MTP head at Qwen3.8-27B's widths (hidden 5120, its full-attention
+    block of 24 / 4 heads of 256 with the hybrid extras, the 65536-row draft
+    vocabulary of tools/convert_hf.py:225) over four trunk blocks: fill from a
+    prefill, a 5-draft chain, a verify of the token and four drafts, and a
+    chain from its third row, against the oracle."""
+    from chattorrent_amd import configs
+    from chattorrent_amd.ccdecode import Context
+    vd = configs.QWEN38["mtp_vocab"]
+    d = dict(configs.QWEN38, n_layer=4, layer_types=configs.QWEN38["layer_types"][:4])
+    c = Context(d, n_max=512, t_max=64, slots=2)
+    om = Hy.HybridModel(d, n_slots=2, max_pages=8)
+    om.w = HW.make(d, SEED)
+    HW.upload(c, om.w, d)
+    wm = HW.make_mtp(d, SEED, vd)
+    HW.upload_mtp(c, wm, d)
+    mh = Hy.MtpHead(om, wm, vd)
+    rng = np.random.default_rng(33)
+    try:
+        job = dict(slot=0, past=0, n=12, ids=_ids(rng, 12, vd), sampled=1, topk=4, mtp=True)
+        vals, ids, out = _pass(c, om, mh, [job])
+        _check(vals, ids, out, c)
+        t = int(np.argmax(out[0]["logits"][0])) % vd
+        got = c.mtp_draft(0, 11, t, 12, 5)
+        assert _same_drafts(got, mh.draft(0, out[0]["hidden"][11], t, 12, 5)) >= 3
+        ver = np.array([t] + [int(g) for g in got[:4]], np.int32)
+        job = dict(slot=0, past=12, n=5, ids=ver, sampled=5, topk=4, mtp=True)
+        vals, ids, out = _pass(c, om, mh, [job])
+        _check(vals, ids, out, c)
+        t2 = int(np.argmax(out[0]["logits"][2])) % vd
+        got = c.mtp_draft(0, 2, t2, 15, 4)
+        assert _same_drafts(got, mh.draft(0, out[0]["hidden"][2], t2, 15, 4)) >= 3
+    finally:
+        c.close()
