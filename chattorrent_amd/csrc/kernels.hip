@@ -972,7 +972,10 @@ __device__ static inline float row_scale(const RowScale& rs, int m) { return row
 // thread's 4 values in order, a wave butterfly, the two waves in order) at
 // ssp[m*RW_SMAX + slice]. Workgroup (slice, row): 128 threads, a float4 of
 // the row each. part == nullptr: x as it is. Rows M .. Mpad-1 get zero
-// operand rows. H % 64 == 0, so the operand has no padding columns.
+// operand rows. H % 64 == 0, so the operand has no padding columns. SP plane
+// loads are issued at once (4 when the projection has at most 4 planes, so
+// no load goes out past them; 16 otherwise), the rest in a loop.
+template <int SP>
 __global__ __launch_bounds__(RW_THREADS) void k_resid_w(float* __restrict__ x, const float* __restrict__ part,
                                                       int splits, int M, int H, int round,
                                                       const float* __restrict__ w, int KU, uint4* __restrict__ Xp,
@@ -998,18 +1001,18 @@ __global__ __launch_bounds__(RW_THREADS) void k_resid_w(float* __restrict__ x, c
             // to the planes: a load past the last one reads zero (no branch),
             // and adding +0 leaves the in-order sum as it is
             const auto rp = __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, splits * M * H * 4, 0x00020000);
-            float4 pv[RN_SPLITS];
+            float4 pv[SP];
 #pragma unroll
-            for (int s = 0; s < RN_SPLITS; s++) {
+            for (int s = 0; s < SP; s++) {
                 const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(rp, (int)xoff * 4, s * M * H * 4, 0);
                 pv[s] = make_float4(__uint_as_float(q[0]), __uint_as_float(q[1]), __uint_as_float(q[2]),
                                     __uint_as_float(q[3]));
             }
             float4 pp = pv[0];
 #pragma unroll
-            for (int s = 1; s < RN_SPLITS; s++)
+            for (int s = 1; s < SP; s++)
                 pp = make_float4(pp.x + pv[s].x, pp.y + pv[s].y, pp.z + pv[s].z, pp.w + pv[s].w);
-            for (int s = RN_SPLITS; s < splits; s++) {
+            for (int s = SP; s < splits; s++) {
                 const float4 q = *(const float4*)(part + (size_t)s * M * H + xoff);
                 pp = make_float4(pp.x + q.x, pp.y + q.y, pp.z + q.z, pp.w + q.w);
             }
@@ -1048,8 +1051,12 @@ __global__ __launch_bounds__(RW_THREADS) void k_resid_w(float* __restrict__ x, c
 void launch_resid_w(hipStream_t st, float* x, const float* part, int splits, int M, int Mpad, int H, int round,
                     const float* w, int KU, uint4* Xp, float* ssp) {
     const int nsl = (H / 4 + RW_THREADS - 1) / RW_THREADS;
-    hipLaunchKernelGGL(k_resid_w, dim3(nsl, w ? Mpad : M), dim3(RW_THREADS), 0, st, x, part, splits, M, H, round, w,
-                       KU, Xp, ssp);
+    const dim3 grid(nsl, w ? Mpad : M);
+    if (splits <= 4)
+        hipLaunchKernelGGL(k_resid_w<4>, grid, dim3(RW_THREADS), 0, st, x, part, splits, M, H, round, w, KU, Xp, ssp);
+    else
+        hipLaunchKernelGGL(k_resid_w<RN_SPLITS>, grid, dim3(RW_THREADS), 0, st, x, part, splits, M, H, round, w, KU,
+                           Xp, ssp);
     CHECK_LAUNCH();
 }
 
@@ -1217,7 +1224,7 @@ __device__ static inline float rope_cs(const float* src, int c, int rot, float c
 // workgroup. The head's D values (K splits summed in order) sit in the wave's
 // LDS slice; Q heads are RoPE'd into the attention operand, K heads RoPE'd and
 // quantised into the pool, V heads quantised.
-template <int D>
+template <int D, int SU>
 __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part, int splits, int M,
                                                   const int32_t* __restrict__ row_job,
                                                   const JobDev* __restrict__ jobs, int nH, int group, KVGeom g,
@@ -1235,10 +1242,11 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
     const int hidx = blockIdx.x * 4 + wave;
     const bool live = hidx < nall;
     const int N = nall * D;
-    // every plane's load in flight at once, first, through a resource sized to
-    // the planes: past the last one a load reads zero (no branch), and adding
-    // +0 leaves the in-order sum as it is
-    constexpr int SU = 16, DH = D / 64;
+    // SU planes' loads in flight at once, first (4 when q|k|v has at most 4
+    // planes, else 16), through a resource sized to the planes: past the last
+    // one a load reads zero (no branch), and adding +0 leaves the in-order sum
+    // as it is; planes past SU in a loop
+    constexpr int DH = D / 64;
     float pv[DH][SU];
     if (live) {
         const auto rp = __builtin_amdgcn_make_buffer_rsrc((void*)part, 0, splits * M * N * 4, 0x00020000);
@@ -1366,21 +1374,34 @@ __global__ __launch_bounds__(256) void k_fin_qkv(const float* __restrict__ part,
     }
 }
 
+template <int D>
+static void launch_fin_qkv_d(hipStream_t st, dim3 grid, const float* part, int splits, int M, const int32_t* row_job,
+                             const JobDev* jobs, int nH, int group, const KVGeom& g, const float* tbl, int rot,
+                             uint8_t* kpool, uint8_t* vpool, const uint32_t* page_table, uint4* Qp,
+                             const RowScale& rs, int do_q, int do_kv, const QkExtras& ex) {
+    if (splits <= 4)
+        hipLaunchKernelGGL((k_fin_qkv<D, 4>), grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g,
+                           tbl, rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv, ex);
+    else
+        hipLaunchKernelGGL((k_fin_qkv<D, 16>), grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g,
+                           tbl, rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv, ex);
+}
+
 void launch_fin_qkv(hipStream_t st, const float* part, int splits, int M, const int32_t* row_job,
                     const JobDev* jobs, int nH, int group, const KVGeom& g, const float* tbl, int rot,
                     uint8_t* kpool, uint8_t* vpool, const uint32_t* page_table, uint4* Qp, const RowScale& rs,
                     int do_q, int do_kv, const QkExtras& ex) {
     const int nall = nH + 2 * g.nKV + (ex.gate ? nH : 0);
-    dim3 grid((nall + 3) / 4, M);
+    const dim3 grid((nall + 3) / 4, M);
     if (g.D == 256)
-        hipLaunchKernelGGL(k_fin_qkv<256>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
-                           rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv, ex);
+        launch_fin_qkv_d<256>(st, grid, part, splits, M, row_job, jobs, nH, group, g, tbl, rot, kpool, vpool,
+                              page_table, Qp, rs, do_q, do_kv, ex);
     else if (g.D == 128)
-        hipLaunchKernelGGL(k_fin_qkv<128>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
-                           rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv, ex);
+        launch_fin_qkv_d<128>(st, grid, part, splits, M, row_job, jobs, nH, group, g, tbl, rot, kpool, vpool,
+                              page_table, Qp, rs, do_q, do_kv, ex);
     else
-        hipLaunchKernelGGL(k_fin_qkv<64>, grid, dim3(256), 0, st, part, splits, M, row_job, jobs, nH, group, g, tbl,
-                           rot, kpool, vpool, page_table, Qp, rs, do_q, do_kv, ex);
+        launch_fin_qkv_d<64>(st, grid, part, splits, M, row_job, jobs, nH, group, g, tbl, rot, kpool, vpool,
+                             page_table, Qp, rs, do_q, do_kv, ex);
     CHECK_LAUNCH();
 }
 
