@@ -316,7 +316,7 @@ static void launch_lx(hipStream_t st, const QTensor& w, const uint4* Xp, float* 
 // each record feeds two waves. The activations of one unit of K for the 64
 // rows (16 KiB) are staged through registers into a double-buffered LDS
 // block, one barrier a unit, while each wave streams its pair's records
-// TM_R-1 units ahead. Small enough for four waves a SIMD.
+// TM_R-1 units ahead (144 VGPRs: two waves a SIMD).
 //
 // Bits: a row's result is bit-identical to k_gemm_lx's at any M. Within a
 // plane k_gemm_lx sums a pair's units in order but in segments, cut where
@@ -523,6 +523,186 @@ __global__ __launch_bounds__(64 * TM_WAVES) void k_gemm_tm(const uint8_t* __rest
             for (int e = 0; e < 4; e++)
                 __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(tot[mt][nt][e]), ro,
                                                       vo + (((mt0 + mw + mt) * 16 + e) * N + tile * 16) * 4, 0, 0);
+    }
+}
+
+// k_gemm_tm12: k_gemm_tm at twelve waves a workgroup (three a SIMD), each
+// still one tile pair over the row block's 4 m-tiles, for matrices whose
+// pair groups of twelve still give every CU a workgroup. The running sum of
+// the segments already folded (k_gemm_tm's `tot`) lives in the wave's own
+// LDS slot (8 KiB a wave) instead of 32 registers, which brings the kernel
+// to 160 VGPRs: three waves a SIMD. A fold reads the slot, adds the segment
+// and writes it back: the same additions in the same order, so every output
+// keeps k_gemm_tm's (and k_gemm_lx's) bits. The staged activation blocks of
+// a unit (16) are shared out over the twelve waves, one or two each.
+constexpr int TM12_WAVES = 12;
+template <bool F32S>
+__global__ __launch_bounds__(64 * TM12_WAVES) void k_gemm_tm12(const uint8_t* __restrict__ Wr,
+                                                              const uint4* __restrict__ Xp, int xp_mtiles,
+                                                              float* __restrict__ out, int KU, int M, int N, int Nt,
+                                                              int P, int Gm) {
+    constexpr int NT = 2, R = TM_R, PW = R - 1, MTL = TM_MT, WV = TM12_WAVES;
+    __shared__ u32x4 xs[2][MTL * 4][64];
+    __shared__ float4_t tl[WV][MTL * NT][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int npairs = Nt / NT;
+    const int nrb = (M + 16 * MTL - 1) / (16 * MTL), npg = (npairs + WV - 1) / WV;
+    const int kx = blockIdx.x / 8;
+    const int gx = (kx / nrb) * 8 + blockIdx.x % 8, gy = kx % nrb;
+    if (gx >= P * npg) return;
+    const int r = gx % P, pb = gx / P;
+    const int pair = pb * WV + wave;
+    const bool has = pair < npairs;
+    const int ua = lx_plane_start(r, KU, P), len = lx_plane_start(r + 1, KU, P) - ua;
+    const int mt0 = gy * MTL;
+    const int G2 = 2 * KU;
+    const auto rw = __builtin_amdgcn_make_buffer_rsrc((void*)Wr, 0, 0x7fffffff, 0x00020000);
+    const uint32_t xbytes = (uint32_t)min((unsigned long long)xp_mtiles * G2 * 2048ull, 0xffffffffull);
+    const auto rx = __builtin_amdgcn_make_buffer_rsrc((void*)Xp, 0, xbytes, 0x00020000);
+    const auto ro = __builtin_amdgcn_make_buffer_rsrc((void*)(out + (size_t)r * M * N), 0, M * N * 4, 0x00020000);
+    const int vw = lane * 16, vs = NT * 1024 + (lane & 15) * NT * 4;
+    const int vo = (4 * (lane >> 4) * N + (lane & 15)) * 4;
+    const int rec0 = (ua * npairs + (has ? pair : 0) * len) * LX_REC;
+    const uint32_t cuts = has ? lx_cuts(pair, npairs, Gm, len) : 0u;
+    constexpr int NB = MTL * 4, BPW = (NB + WV - 1) / WV;
+    u32x4 st[BPW];
+    auto load_x = [&](int u) {
+        const int Uk = ua + (u < len ? u : len - 1);
+#pragma unroll
+        for (int k = 0; k < BPW; k++) {
+            const int b = wave + k * WV, mt = b >> 2, q = b & 3;
+            if (b < NB) {
+                const int src = ((mt0 + mt) * G2 + 2 * Uk + (q >> 1)) * 2 + (q & 1);
+                st[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, vw, src * 1024, 0);
+            }
+        }
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int k = 0; k < BPW; k++) {
+            const int b = wave + k * WV;
+            if (b < NB) xs[buf][b][lane] = st[k];
+        }
+    };
+    u32x4 w[R][NT];
+    uint32_t sc[R][NT];
+    auto load_w = [&](int u, u32x4 (&wv)[NT], uint32_t (&sv)[NT]) {
+        const int off = rec0 + (u < len ? u : len - 1) * LX_REC;
+        wv[0] = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, off, 2);
+        wv[1] = __builtin_amdgcn_raw_buffer_load_b128(rw, vw, off + 1024, 2);
+        const auto s2 = __builtin_amdgcn_raw_buffer_load_b64(rw, vs, off, 0);
+        sv[0] = s2[0];
+        sv[1] = s2[1];
+    };
+    float4_t seg[MTL][NT];
+#pragma unroll
+    for (int mt = 0; mt < MTL; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++) seg[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+    bool started = false;
+
+    load_x(0);
+#pragma unroll
+    for (int i = 0; i < PW; i++) load_w(i, w[i], sc[i]);
+    store_x(0);
+    load_x(1);
+    __syncthreads();
+
+    auto fold = [&]() {
+#pragma unroll
+        for (int mt = 0; mt < MTL; mt++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                float4_t t = seg[mt][nt];
+                if (started) {
+                    const float4_t o = tl[wave][mt * NT + nt][lane];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) t[e] = o[e] + seg[mt][nt][e];
+                }
+                tl[wave][mt * NT + nt][lane] = t;
+                seg[mt][nt] = float4_t{0.f, 0.f, 0.f, 0.f};
+            }
+        started = true;
+    };
+    auto unit = [&](int u, const u32x4 (&wc)[NT], const uint32_t (&sv)[NT]) {
+        const int buf = u & 1;
+        if ((cuts >> u) & 1u) fold();
+        half8_t b[2][NT], bl[2][NT];
+        float scale[2][NT];
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                b[h][nt] = h ? dequant8_biased(wc[nt][2], wc[nt][3]) : dequant8_biased(wc[nt][0], wc[nt][1]);
+                bl[h][nt] = lo_weight8(b[h][nt]);
+                scale[h][nt] = rec_scale<F32S>(sv[nt], h);
+            }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            u32x4 xv[MTL][2];
+#pragma unroll
+            for (int mt = 0; mt < MTL; mt++)
+#pragma unroll
+                for (int q = 0; q < 2; q++) xv[mt][q] = xs[buf][mt * 4 + 2 * h + q][lane];
+            float4_t pp[MTL][NT];
+#pragma unroll
+            for (int mt = 0; mt < MTL; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    pp[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[mt][0]), b[h][nt], float4_t{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int mt = 0; mt < MTL; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+                    pp[mt][nt] = mfma16x16x32(__builtin_bit_cast(half8_t, xv[mt][1]), bl[h][nt], pp[mt][nt]);
+#pragma unroll
+            for (int mt = 0; mt < MTL; mt++)
+#pragma unroll
+                for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) seg[mt][nt][e] = __builtin_fmaf(scale[h][nt], pp[mt][nt][e], seg[mt][nt][e]);
+        }
+    };
+    int u = 0;
+    for (; u + R <= len; u += R) {
+#pragma unroll
+        for (int I = 0; I < R; I++) {
+            load_w(u + I + PW, w[(I + PW) % R], sc[(I + PW) % R]);
+            unit(u + I, w[I], sc[I]);
+            store_x((I + 1) & 1);
+            load_x(u + I + 2);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int I = 0; I < PW; I++) {
+        if (u + I < len) {
+            unit(u + I, w[I], sc[I]);
+            store_x((I + 1) & 1);
+            load_x(u + I + 2);
+            __syncthreads();
+        }
+    }
+    if (!has) return;
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int tile = pair * NT + nt;
+        if (tile * 16 >= N) continue;
+        if (tile * 16 + 16 > N && tile * 16 + (lane & 15) >= N) continue;
+#pragma unroll
+        for (int mt = 0; mt < MTL; mt++) {
+            float4_t t = seg[mt][nt];
+            if (started) {
+                const float4_t o = tl[wave][mt * NT + nt][lane];
+#pragma unroll
+                for (int e = 0; e < 4; e++) t[e] = o[e] + seg[mt][nt][e];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(t[e]), ro,
+                                                      vo + (((mt0 + mt) * 16 + e) * N + tile * 16) * 4, 0, 0);
+        }
     }
 }
 
@@ -757,7 +937,23 @@ static void launch_gemm_fmt(hipStream_t st, const QTensor& w, const uint4* Xp, i
         const int Gm = lx_groups(w, ncu) / w.P;
         const int npairs = w.Nt / 2;
         const bool sum = gemm_planes(w, M, ncu) == 1;
-        const int units = (sum ? 1 : w.P) * ((npairs + TM_PAIRS - 1) / TM_PAIRS), nrb = (M + 16 * TM_MT - 1) / (16 * TM_MT);
+        const int nrb = (M + 16 * TM_MT - 1) / (16 * TM_MT);
+        // Twelve pairs a workgroup where that takes fewer rounds of
+        // workgroups over the CUs, counting a round of the twelve-wave kernel
+        // as 1.5 of the eight-wave one's (measured at 128 rows: 39 against
+        // 25 us a round at gate|up, 36 against 25 at down): at 128 rows
+        // gate|up runs 3 rounds instead of 5 and down 2 instead of 3.
+        const int units12 = w.P * ((npairs + TM12_WAVES - 1) / TM12_WAVES);
+        const long long r8 = ((long long)w.P * ((npairs + TM_PAIRS - 1) / TM_PAIRS) * nrb + ncu - 1) / ncu;
+        const long long r12 = ((long long)units12 * nrb + ncu - 1) / ncu;
+        if (!sum && 3 * r12 <= 2 * r8) {
+            dim3 grid(8 * ((units12 + 7) / 8) * nrb);
+            hipLaunchKernelGGL(k_gemm_tm12<F32S>, grid, dim3(64 * TM12_WAVES), 0, st, (const uint8_t*)w.codes, Xp,
+                               xp_mtiles, out, w.KU, M, w.N, w.Nt, w.P, Gm);
+            CHECK_LAUNCH();
+            return;
+        }
+        const int units = (sum ? 1 : w.P) * ((npairs + TM_PAIRS - 1) / TM_PAIRS);
         dim3 grid(8 * ((units + 7) / 8) * nrb);
         if (sum)
             hipLaunchKernelGGL(k_gemm_tm_sum<F32S>, grid, dim3(64 * TM_WAVES), 0, st, (const uint8_t*)w.codes, Xp,

@@ -100,6 +100,28 @@ def test_matmul_many_rows_bitwise(ctx):
         assert np.array_equal(few.view(np.uint32), rows[:32].view(np.uint32)), M
 
 
+def test_matmul_many_rows_twelve_waves_bitwise(ctx):
+    """The many-row matmul runs twelve waves a workgroup (folded segments in
+    LDS) where that takes fewer rounds of workgroups over the CUs, else
+    eight (folds in registers). At N 8240, K 5120 on 256 CUs that is twelve
+    at 70 and 200 rows and eight at 129. Either way every row keeps the bits
+    of the one-row call, so each call equals the first rows of the larger
+    one. N 8240 ends in a partial pair group and a partial tile."""
+    from oracle import lib as L
+    rng = np.random.default_rng(43)
+    K, N = 5120, 8240
+    W = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    S16 = L.to_f16((rng.random((N, K // 32)) * 2 - 1).astype(np.float32))
+    X = (rng.random((200, K), np.float32) * 2 - 1).astype(np.float32)
+    got = {M: ctx.op_matmul_q8(X[:M], W, S16) for M in (70, 129, 200)}
+    for M, rows in got.items():
+        for i in sorted({0, 1, M // 2, M - 2, M - 1}):
+            one = ctx.op_matmul_q8(X[i:i + 1], W, S16)
+            assert np.array_equal(one.view(np.uint32), rows[i:i + 1].view(np.uint32)), (M, i)
+    assert np.array_equal(got[70].view(np.uint32), got[129][:70].view(np.uint32))
+    assert np.array_equal(got[129].view(np.uint32), got[200][:129].view(np.uint32))
+
+
 @pytest.mark.parametrize("K,N", [(2560, 8192), (5120, 8192), (4160, 8240), (2112, 4144)])
 def test_matmul_summed_planes_bitwise(ctx, K, N):
     """With rows enough to fill the GPU without the K split (2048 rows: 32
