@@ -2025,12 +2025,13 @@ void launch_lin_norm(hipStream_t st, const float* core, const float* lraw, const
 // Every page is read through a buffer resource whose base is that page's
 // (page, kv head) block (64-bit address arithmetic, so pools may exceed
 // 4 GB) and whose size is the block: an offset outside it reads zero.
-// The K and V code loads are non-temporal (cache policy nt): a pass reads
-// each page's codes once, and streaming them leaves the L2 to what the
-// kernels after attention read (measured: the whole pass 0.4-1.3% faster at
-// 32 one-row chats and 0.7-0.8% at 16 verify jobs of 8 rows, although the
-// attention launch alone is slower). The 1 KiB scale blocks stay ordinary
-// loads; making them non-temporal as well measured no better.
+// At head_dim <= 128 the K and V code loads are non-temporal (cache policy
+// nt): a pass reads each page's codes once, and streaming them leaves the L2
+// to what the kernels after attention read (measured: the whole pass
+// 0.4-1.3% faster at 32 one-row chats and 0.7-0.8% at 16 verify jobs of 8
+// rows, although the attention launch alone is slower). At head_dim 256 (one
+// wave a SIMD) they measured 2-3% slower for the whole pass and stay
+// ordinary loads, as do the 1 KiB scale blocks (non-temporal: no better).
 //
 // Every lane builds its fragments and rescales O on every page, with no
 // branch on row state: MFMA reads all lanes' operands whatever the execution
@@ -2108,11 +2109,11 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
         for (int tt = 0; tt < 4; tt++)
 #pragma unroll
             for (int q = 0; q < NG / 2; q++)
-                kc[tt][q] = __builtin_amdgcn_raw_buffer_load_b128(rk, vk, tt * 16 * D + 16 * q, 2);
+                kc[tt][q] = __builtin_amdgcn_raw_buffer_load_b128(rk, vk, tt * 16 * D + 16 * q, NG > 4 ? 0 : 2);
     };
     auto load_v = [&](__amdgpu_buffer_rsrc_t rv) {
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) vc[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, dt * 256, 2);
+        for (int dt = 0; dt < DT; dt++) vc[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, dt * 256, NG > 4 ? 0 : 2);
     };
     // One page. Its scale blocks arrived in kst/vst during the previous page;
     // they go to this wave's LDS slice first (a wave's LDS accesses run in
@@ -2338,9 +2339,9 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
     auto load = [&](int p) {
         const auto rk = page_rsrc(kpool, p), rv = page_rsrc(vpool, p);
 #pragma unroll
-        for (int q = 0; q < NG / 2; q++) kc[q] = __builtin_amdgcn_raw_buffer_load_b128(rk, vk, wv * 16 * D + 16 * q, 2);
+        for (int q = 0; q < NG / 2; q++) kc[q] = __builtin_amdgcn_raw_buffer_load_b128(rk, vk, wv * 16 * D + 16 * q, NG > 4 ? 0 : 2);
 #pragma unroll
-        for (int i = 0; i < DQ; i++) vc[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, (wv * DQ + i) * 256, 2);
+        for (int i = 0; i < DQ; i++) vc[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, (wv * DQ + i) * 256, NG > 4 ? 0 : 2);
         if (wv == 0) {
 #pragma unroll
             for (int q = 0; q < SCL; q++) sc[q] = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16, 64 * D + 1024 * q, 0);
@@ -2364,9 +2365,9 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
             for (int tt = 0; tt < 4; tt++)
 #pragma unroll
                 for (int q = 0; q < NG / 2; q++)
-                    fk[tt][q] = __builtin_amdgcn_raw_buffer_load_b128(rk, vk, tt * 16 * D + 16 * q, 2);
+                    fk[tt][q] = __builtin_amdgcn_raw_buffer_load_b128(rk, vk, tt * 16 * D + 16 * q, NG > 4 ? 0 : 2);
 #pragma unroll
-            for (int dt = 0; dt < DT; dt++) fv[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, dt * 256, 2);
+            for (int dt = 0; dt < DT; dt++) fv[dt] = __builtin_amdgcn_raw_buffer_load_b128(rv, vv, dt * 256, NG > 4 ? 0 : 2);
 #pragma unroll
             for (int q = 0; q < SCL; q++) {
                 fs[0][q] = __builtin_amdgcn_raw_buffer_load_b128(rk, lane * 16, 64 * D + 1024 * q, 0);
