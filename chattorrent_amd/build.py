@@ -80,7 +80,7 @@ def build_addon():
 
 
 def build_oracle():
-    _run(["make", "-s", "-C", os.path.join(ROOT, "oracle")])
+    _run(["make", "-s", "-B", "-C", os.path.join(ROOT, "oracle")])
 
 
 def main():
