@@ -127,7 +127,7 @@ __device__ static inline half8_t dequant8_biased(uint32_t lo, uint32_t hi) {
 // while lo stays a normal f16 (|x| >= 2^-3; below that lo's absolute step is
 // 2^-24). Attention's Q operand uses it: its values are of order 1 and its
 // scores are sums of such products, where that step is below f32 rounding.
-// The matmul operands and P.V use split_hilo_x.
+// The matmul operands use split_hilo_x, attention's P.V split_hilo2.
 // x is made opaque first: when x is a product, the compiler may otherwise fold
 // the multiply into the f16 conversion (v_fma_mix, one rounding) for one use
 // of hi and convert the f32 product (two roundings) for another, and the two
@@ -138,13 +138,13 @@ __device__ static inline void split_hilo(float x, _Float16& hi, _Float16& lo) {
     lo = (_Float16)(x - (float)hi);
 }
 
-// The scaled split the matmul operands and attention's P.V use: hi = f16(x)
+// The scaled split the matmul operands use: hi = f16(x)
 // and lo = f16((x - hi) * 2^11). The remainder is below half an f16 step of
 // hi, so lo scaled by 2^11 is of x's own magnitude and stays a normal f16 for
 // every |x| >= 2^-14 (an unscaled lo is subnormal below |x| = 2^-3 and keeps
-// fewer bits). The consumer multiplies lo's products by 2^-11, exactly: the
-// matmuls with the weight fragment scaled by HILO_LO_WEIGHT, attention with
-// its lo accumulator. |x - hi| * 2^11 <= 2^15 for every finite f16 hi.
+// fewer bits). The matmuls multiply lo's products by 2^-11, exactly, with the
+// weight fragment scaled by HILO_LO_WEIGHT. |x - hi| * 2^11 <= 2^15 for every
+// finite f16 hi.
 constexpr float HILO_LO_SHIFT = 2048.0f;
 constexpr float HILO_LO_WEIGHT = 1.0f / 2048.0f;
 __device__ static inline void split_hilo_x(float x, _Float16& hi, _Float16& lo) {
@@ -161,21 +161,29 @@ __device__ static inline half8_t lo_weight8(half8_t b) {
     return b * s;
 }
 
-// Two values at once, as split_hilo_x (nearest-even hi, lo = f16 of the
-// exact remainder times 2^11), returned packed as two f16 pairs. (Truncating
-// the pair with v_cvt_pkrtz saves two instructions but biases every lo toward
-// zero, and the bias adds up over a long softmax sum.)
-__device__ static inline void split_hilo2_x(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+// Attention's P.V operand: two values x = p * s_v as hi = f16(x)
+// (nearest-even) and lo = f16(x - hi), packed as two f16 pairs; x - hi is
+// exact in f32 (one v_fma_mix from hi's f16 value). Attention forms p
+// times 2^PV_SHIFT_LOG2 (2^8, folded into the softmax's exponent, and taken off
+// again, exactly, when a wave writes its partial), so lo is a normal f16 for
+// p * s_v >= 2^-11 (22 significant bits) and below that its absolute step
+// is 2^-32 of p * s_v, under f32 rounding of the page's sum; both halves
+// multiply the same V fragment into one accumulator. A page holding a V
+// scale above PV_SCALE_MAX (|V| > 32385) would overflow the shifted f16, so
+// from that page on the wave drops the shift (its O and running sum times
+// 2^-8, exactly). (Truncating the pair with v_cvt_pkrtz saves two
+// instructions but biases every lo toward zero, and the bias adds up over a
+// long softmax sum.)
+constexpr float PV_SHIFT_LOG2 = 8.0f;
+constexpr float PV_UNSHIFT = 1.0f / 256.0f;
+constexpr float PV_SCALE_MAX = 255.0f;
+__device__ static inline void split_hilo2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
     typedef float f2_t __attribute__((ext_vector_type(2)));
     asm("" : "+v"(x0), "+v"(x1));
     const f2_t x = {x0, x1};
     const half2_t h = __builtin_convertvector(x, half2_t);
-    // (x - hi) * 2^11 as one FMA from hi's f16 value (v_fma_mix): 2^11 x and
-    // 2^11 x - 2^11 hi are exact in f32, so the bits are those of the
-    // subtraction followed by the scaling
-    const f2_t rs = {__builtin_fmaf((float)h[0], -HILO_LO_SHIFT, x0 * HILO_LO_SHIFT),
-                     __builtin_fmaf((float)h[1], -HILO_LO_SHIFT, x1 * HILO_LO_SHIFT)};
-    const half2_t l = __builtin_convertvector(rs, half2_t);
+    const f2_t r = {__builtin_fmaf((float)h[0], -1.0f, x0), __builtin_fmaf((float)h[1], -1.0f, x1)};
+    const half2_t l = __builtin_convertvector(r, half2_t);
     hi = __builtin_bit_cast(uint32_t, h);
     lo = __builtin_bit_cast(uint32_t, l);
 }

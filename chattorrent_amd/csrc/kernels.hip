@@ -2038,6 +2038,15 @@ void launch_lin_norm(hipStream_t st, const float* core, const float* lraw, const
 // mask, and a still fully masked row (max -inf) just takes alpha = 0, p = 0.
 // One work item of a wave: its (job, kv head, m-tile) over the chunk's pages,
 // with the wave's LDS slices for the page's K and V scale blocks.
+// Whether any of four V scales (f32 bits) is too large for the shifted P.V
+// split (p * s * PV_SHIFT would overflow f16) — or not finite.
+__device__ static inline bool pv_big(u32x4 v) {
+    bool b = false;
+#pragma unroll
+    for (int e = 0; e < 4; e++) b = b || !(__uint_as_float(v[e]) <= PV_SCALE_MAX);
+    return b;
+}
+
 template <int NG>
 __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __restrict__ Qp,
                                           const uint8_t* __restrict__ kpool, const uint8_t* __restrict__ vpool,
@@ -2092,6 +2101,7 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
     }
 
     float mrow = -INFINITY, lsum = 0.0f;
+    bool shifted = true;   // p carries 2^PV_SHIFT_LOG2 (O and lsum too) until a page's V scales forbid it
     float4_t o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -2125,6 +2135,7 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
     auto page = [&](int p) {
         // the last page reloads itself instead of branching (an L2 hit)
         const int pn = p + 1 < p1 ? p + 1 : p;
+        bool big = false;
 #pragma unroll
         for (int q = 0; q < SCL; q++) {
             *(u32x4*)&ksl_w[256 * q + lane * 4] = kst[q];
@@ -2137,8 +2148,10 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
                 for (int e = 0; e < 4; e++)
                     if (t0 + e >= T_act) v[e] = 0u;
             }
+            big = big || pv_big(v);
             *(u32x4*)&vsl_w[256 * q + lane * 4] = v;
         }
+        const bool pbig = __builtin_amdgcn_ballot_w64(big) != 0;
         {
             float pr[4][4];
             float pm = -INFINITY;
@@ -2187,13 +2200,15 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
             pm = fmaxf(pm, __shfl_xor(pm, 16));
             pm = fmaxf(pm, __shfl_xor(pm, 32));
             const float mnew = fmaxf(mrow, pm);
-            const float alpha = mrow == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrow - mnew);
+            const float shrink = pbig && shifted ? PV_UNSHIFT : 1.0f;
+            shifted = shifted && !pbig;
+            const float alpha = (mrow == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrow - mnew)) * shrink;
             lsum *= alpha;
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) o[dt][r] *= alpha;
-            const float msub = mnew == -INFINITY ? 0.0f : mnew;
+            const float msub = (mnew == -INFINITY ? 0.0f : mnew) - (shifted ? PV_SHIFT_LOG2 : 0.0f);
 #pragma unroll
             for (int tt = 0; tt < 4; tt++)
 #pragma unroll
@@ -2203,9 +2218,7 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
                     lsum += e;
                 }
             __builtin_amdgcn_sched_barrier(0);
-            // p * s as hi + 2^-11 lo (split_hilo2_x): the lo products gather in
-            // ol over the page and join O once, times 2^-11
-            float4_t ol[DT];
+            // p * s (p times 2^PV_SHIFT_LOG2 while shifted) as hi + lo (split_hilo2), both into O
 #pragma unroll
             for (int b = 0; b < NG; b++) {
                 float sv[16];   // the lane's 16 tokens of 32-block b
@@ -2223,7 +2236,7 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
                         const float p0 = pr[tt][r] * sv[4 * tt + r];
                         const float p1 = pr[tt][r + 1] * sv[4 * tt + r + 1];
                         uint32_t h, l;
-                        split_hilo2_x(p0, p1, h, l);
+                        split_hilo2(p0, p1, h, l);
                         phw[ii >> 1] = h;
                         plw[ii >> 1] = l;
                     }
@@ -2234,14 +2247,10 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
                         const u32x4 c = vc[dt];
                         const half8_t vf = ks ? dequant8_biased(c[2], c[3]) : dequant8_biased(c[0], c[1]);
                         o[dt] = mfma16x16x32(vf, ph, o[dt]);
-                        ol[dt] = mfma16x16x32(vf, pl, ks ? ol[dt] : float4_t{0.f, 0.f, 0.f, 0.f});
+                        o[dt] = mfma16x16x32(vf, pl, o[dt]);
                     }
                 }
             }
-#pragma unroll
-            for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) o[dt][r] = __builtin_fmaf(HILO_LO_WEIGHT, ol[dt][r], o[dt][r]);
             mrow = mnew;
             load_v(rvn);
         }
@@ -2254,13 +2263,15 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
     }
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
-    // partial row: max, sum, two pad floats, then O (16-byte aligned); rows
-    // past the job's R query rows are neither written nor read
+    // partial row: max, sum, two pad floats, then O (16-byte aligned), the
+    // shift taken off; rows past the job's R query rows are neither written
+    // nor read
     if (rho < R) {
+        const float un = shifted ? PV_UNSHIFT : 1.0f;
         float* dst = part + it.part + (size_t)l16 * (D + 4);
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) *(float4_t*)(dst + 4 + dt * 16 + 4 * j4) = o[dt];
-        if (j4 == 0) *(float2*)dst = make_float2(mrow, lsum);
+        for (int dt = 0; dt < DT; dt++) *(float4_t*)(dst + 4 + dt * 16 + 4 * j4) = o[dt] * un;
+        if (j4 == 0) *(float2*)dst = make_float2(mrow, lsum * un);
     }
 }
 
@@ -2286,11 +2297,12 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
     constexpr int DT = D / 16, DQ = DT / 4;
     constexpr int SCL = NG > 4 ? NG / 4 : 1;
     // LDS: K fragments [2][4 tt][NG gg][64], V fragments [2][DT][2 ks][64], then the
-    // K and V scale blocks [2][256 * SCL] floats each
+    // K and V scale blocks [2][256 * SCL] floats each, then the pages' range flags [2]
     u32x4* kf_s = lds;
     u32x4* vf_s = kf_s + 2 * 4 * NG * 64;
     float* ks_s = (float*)(vf_s + 2 * DT * 2 * 64);
     float* vs_s = ks_s + 2 * 256 * SCL;
+    int* big_s = (int*)(vs_s + 2 * 256 * SCL);   // [2]: the page's V scales forbid the P.V shift
     const int lane = threadIdx.x & 63, j4 = lane >> 4, l16 = lane & 15;
     const int T_act = it0.past + it0.n;
     const int R = it0.n * group;
@@ -2329,6 +2341,7 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
     }
 
     float mrow = -INFINITY, lsum = 0.0f;
+    bool shifted = true;   // as in attn_item
     float4_t o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -2394,6 +2407,7 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
                 vf[(dt * 2) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(fv[dt][0], fv[dt][1]));
                 vf[(dt * 2 + 1) * 64 + lane] = __builtin_bit_cast(u32x4, dequant8_biased(fv[dt][2], fv[dt][3]));
             }
+            bool big = false;
 #pragma unroll
             for (int q = 0; q < SCL; q++) {
                 *(u32x4*)&ksl[256 * q + lane * 4] = fs[0][q];
@@ -2404,8 +2418,11 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
                     for (int e = 0; e < 4; e++)
                         if (t0 + e >= T_act) v[e] = 0u;
                 }
+                big = big || pv_big(v);
                 *(u32x4*)&vsl[256 * q + lane * 4] = v;
             }
+            const bool pbig = __builtin_amdgcn_ballot_w64(big) != 0;
+            if (lane == 0) big_s[B] = pbig ? 1 : 0;
             __syncthreads();
             if (p + 1 < p1) load_all(p + 1);
         }
@@ -2433,6 +2450,7 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
 #pragma unroll
                 for (int q = 0; q < SCL; q++) *(u32x4*)&ksl[256 * q + lane * 4] = sc[q];
             } else if (wv == 1) {
+                bool big = false;
 #pragma unroll
                 for (int q = 0; q < SCL; q++) {
                     u32x4 v = sc[q];
@@ -2442,8 +2460,11 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
                         for (int e = 0; e < 4; e++)
                             if (t0 + e >= T_act) v[e] = 0u;
                     }
+                    big = big || pv_big(v);
                     *(u32x4*)&vsl[256 * q + lane * 4] = v;
                 }
+                const bool pbig = __builtin_amdgcn_ballot_w64(big) != 0;
+                if (lane == 0) big_s[B] = pbig ? 1 : 0;
             }
         }
         __syncthreads();
@@ -2492,13 +2513,16 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
         pm = fmaxf(pm, __shfl_xor(pm, 16));
         pm = fmaxf(pm, __shfl_xor(pm, 32));
         const float mnew = fmaxf(mrow, pm);
-        const float alpha = mrow == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrow - mnew);
+        const bool pbig = __builtin_amdgcn_readfirstlane(big_s[B]) != 0;
+        const float shrink = pbig && shifted ? PV_UNSHIFT : 1.0f;
+        shifted = shifted && !pbig;
+        const float alpha = (mrow == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrow - mnew)) * shrink;
         lsum *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; dt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) o[dt][r] *= alpha;
-        const float msub = mnew == -INFINITY ? 0.0f : mnew;
+        const float msub = (mnew == -INFINITY ? 0.0f : mnew) - (shifted ? PV_SHIFT_LOG2 : 0.0f);
 #pragma unroll
         for (int tt = 0; tt < 4; tt++)
 #pragma unroll
@@ -2507,7 +2531,6 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
                 pr[tt][r] = e;
                 lsum += e;
             }
-        float4_t ol[DT];   // the page's lo-half products (split_hilo2_x), 2^11 x
 #pragma unroll
         for (int b = 0; b < NG; b++) {
             float sv[16];
@@ -2523,7 +2546,7 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
                 for (int ii = 0; ii < 8; ii += 2) {
                     const int tt = 2 * ks + (ii >> 2), r = ii & 3;
                     uint32_t h, l;
-                    split_hilo2_x(pr[tt][r] * sv[4 * tt + r], pr[tt][r + 1] * sv[4 * tt + r + 1], h, l);
+                    split_hilo2(pr[tt][r] * sv[4 * tt + r], pr[tt][r + 1] * sv[4 * tt + r + 1], h, l);
                     phw[ii >> 1] = h;
                     plw[ii >> 1] = l;
                 }
@@ -2533,24 +2556,21 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
                     const int dt = 2 * b + dd;
                     const half8_t vfr = __builtin_bit_cast(half8_t, vf[(dt * 2 + ks) * 64 + lane]);
                     o[dt] = mfma16x16x32(vfr, ph, o[dt]);
-                    ol[dt] = mfma16x16x32(vfr, pl, ks ? ol[dt] : float4_t{0.f, 0.f, 0.f, 0.f});
+                    o[dt] = mfma16x16x32(vfr, pl, o[dt]);
                 }
             }
         }
-#pragma unroll
-        for (int dt = 0; dt < DT; dt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) o[dt][r] = __builtin_fmaf(HILO_LO_WEIGHT, ol[dt][r], o[dt][r]);
         mrow = mnew;
     }
     if (!mine) return;
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
     if (rho < R) {
+        const float un = shifted ? PV_UNSHIFT : 1.0f;
         float* dst = part + it.part + (size_t)l16 * (D + 4);
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) *(float4_t*)(dst + 4 + dt * 16 + 4 * j4) = o[dt];
-        if (j4 == 0) *(float2*)dst = make_float2(mrow, lsum);
+        for (int dt = 0; dt < DT; dt++) *(float4_t*)(dst + 4 + dt * 16 + 4 * j4) = o[dt] * un;
+        if (j4 == 0) *(float2*)dst = make_float2(mrow, lsum * un);
     }
 }
 
@@ -2561,7 +2581,7 @@ template <int NG>
 constexpr size_t attn_lds_bytes() {
     constexpr size_t SCL = NG > 4 ? NG / 4 : 1, DT = 2 * NG;
     constexpr size_t single = 8 * 256 * SCL * 4;
-    constexpr size_t block = (2 * 4 * NG * 64 + 2 * DT * 2 * 64) * 16 + 2 * 2 * 256 * SCL * 4;
+    constexpr size_t block = (2 * 4 * NG * 64 + 2 * DT * 2 * 64) * 16 + 2 * 2 * 256 * SCL * 4 + 16;
     return single > block ? single : block;
 }
 

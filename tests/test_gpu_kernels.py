@@ -338,3 +338,58 @@ def test_attend_ignores_stale_rows_past_the_context(gpu):
             assert np.array_equal(clean.view(np.uint32), poisoned.view(np.uint32)), (tokens, n)
         finally:
             c.close()
+
+
+def test_attend_with_v_scales_beyond_the_shifted_split(gpu):
+    """The P.V operand is p * s_v with p carried times 2^8 through the softmax,
+    so that its f16 lo half stays normal; a page holding a V scale above 255
+    (|V| > 32385 in its 32-channel group) would overflow that f16, and the
+    wave drops the shift from that page on. V scales of 300-5000 put on
+    tokens of a page in the middle of a work item (page 1), on the first page
+    of the next item (page 8) and on a later one (page 10): the output still
+    matches the oracle (web/model/kernels.js:1255-1310 attn_av_gqa, f32 for
+    any scale) within 2e-5 of max |out|, decode rows through each wave's own
+    dequantisation and verify rows through the shared-page blocks, and each
+    verify row keeps the bits of the same row attended alone."""
+    from oracle import lib as L
+    from oracle import model as Mo
+    for base in (configs.M27B, D256):
+        d = configs.with_layers(base, 1)
+        D, nH, nKV = d["head_dim"], d["n_heads"], d["n_kv_heads"]
+        group = nH // nKV
+        tokens, nv = 700, 8
+        c = _ctx(gpu, d, n_max=1024, t_max=64, slots=2)
+        try:
+            om = Mo.Model(d, n_slots=2, max_pages=16)
+            c.fill_random_kv(1, tokens + nv, 11, 3)
+            om.fill_random_kv(1, tokens + nv, 11, 3)
+            big = {100: 300.0, 101: 5000.0, 103: 1000.0, 512: 700.0, 650: 2000.0}
+            for h in range(nKV):
+                rows = c.read_kv(0, 1, 1, h, 0, tokens + nv)
+                assert np.array_equal(rows, om.kv_rows(0, 1, 1, 0, tokens + nv, h))
+                for t, s in big.items():
+                    sc = rows[t, D // 4:].view(np.float32)
+                    sc[h % (D // 32)] = np.float32(s)
+                c.write_kv(0, 1, 1, h, 0, rows)
+                pg = om.frames[1]["pages"]
+                t = np.arange(tokens + nv)
+                at = ((pg[t // 64].astype(np.int64) * nKV + h) * 64 + t % 64) * om.rw
+                om.V[0][at[:, None] + np.arange(om.rw)[None, :]] = rows
+            pages = om.frames[1]["pages"]
+            for n in (1, nv):
+                q = np.random.default_rng(tokens + n).standard_normal((n, nH * D)).astype(np.float32)
+                got = c.op_attend(0, 1, q, tokens)
+                Qh = np.ascontiguousarray(q.reshape(n, nH, D).transpose(1, 0, 2))
+                L.rope(Qh, D, tokens, om.tbl)
+                s = L.qk_scores(Qh, om.K[0], n, tokens + n, 64, D, nH, group, pages)
+                p = L.causal_softmax(s, tokens)
+                want = L.attn_av(p, om.V[0], D, 64, group, pages).transpose(1, 0, 2).reshape(n, nH * D)
+                assert np.isfinite(got).all(), (base["hidden"], n)
+                err = np.abs(got - want).max()
+                assert err <= 2e-5 * max(1.0, np.abs(want).max()), (base["hidden"], n, err)
+                if n > 1:
+                    for i in range(n):
+                        one = c.op_attend(0, 1, q[i:i + 1], tokens + i)
+                        assert np.array_equal(one.view(np.uint32), got[i:i + 1].view(np.uint32)), (base["hidden"], i)
+        finally:
+            c.close()
