@@ -168,15 +168,18 @@ __device__ static inline half8_t lo_weight8(half8_t b) {
 // again, exactly, when a wave writes its partial), so lo is a normal f16 for
 // p * s_v >= 2^-11 (22 significant bits) and below that its absolute step
 // is 2^-32 of p * s_v, under f32 rounding of the page's sum; both halves
-// multiply the same V fragment into one accumulator. A page holding a V
-// scale above PV_SCALE_MAX (|V| > 32385) would overflow the shifted f16, so
-// from that page on the wave drops the shift (its O and running sum times
-// 2^-8, exactly). (Truncating the pair with v_cvt_pkrtz saves two
-// instructions but biases every lo toward zero, and the bias adds up over a
-// long softmax sum.)
+// multiply the same V fragment into one accumulator. p is formed as
+// exp2(s - (max - 8)); with |max| < PV_MAX_SCORE (log2 units) the rounding
+// of max - 8 keeps p below 256.1, so p * s stays in the f16 range for V
+// scales up to PV_SCALE_MAX (|V| <= 32385). A row meeting a page with a
+// larger (or non-finite) V scale, or a running max beyond that bound, drops
+// the shift from that page on (its O and running sum times 2^-8, exactly).
+// (Truncating the pair with v_cvt_pkrtz saves two instructions but biases
+// every lo toward zero, and the bias adds up over a long softmax sum.)
 constexpr float PV_SHIFT_LOG2 = 8.0f;
 constexpr float PV_UNSHIFT = 1.0f / 256.0f;
 constexpr float PV_SCALE_MAX = 255.0f;
+constexpr float PV_MAX_SCORE = 4096.0f;
 __device__ static inline void split_hilo2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
     typedef float f2_t __attribute__((ext_vector_type(2)));
     asm("" : "+v"(x0), "+v"(x1));

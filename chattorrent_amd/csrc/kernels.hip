@@ -2101,7 +2101,7 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
     }
 
     float mrow = -INFINITY, lsum = 0.0f;
-    bool shifted = true;   // p carries 2^PV_SHIFT_LOG2 (O and lsum too) until a page's V scales forbid it
+    bool shifted = true;   // this row's p carries 2^PV_SHIFT_LOG2 (its O and lsum too) until dropped
     float4_t o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) o[dt] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -2200,8 +2200,11 @@ __device__ __forceinline__ void attn_item(const AttnItem& it, const uint4* __res
             pm = fmaxf(pm, __shfl_xor(pm, 16));
             pm = fmaxf(pm, __shfl_xor(pm, 32));
             const float mnew = fmaxf(mrow, pm);
-            const float shrink = pbig && shifted ? PV_UNSHIFT : 1.0f;
-            shifted = shifted && !pbig;
+            // the row drops the shift for good on a page whose V scales or its own
+            // running max (in log2 units) leave no f16 room for p * s
+            const bool drop = pbig || !(fabsf(mnew) < PV_MAX_SCORE);
+            const float shrink = drop && shifted ? PV_UNSHIFT : 1.0f;
+            shifted = shifted && !drop;
             const float alpha = (mrow == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrow - mnew)) * shrink;
             lsum *= alpha;
 #pragma unroll
@@ -2514,8 +2517,9 @@ __device__ __forceinline__ void attn_block4(const AttnItem& it, const AttnItem& 
         pm = fmaxf(pm, __shfl_xor(pm, 32));
         const float mnew = fmaxf(mrow, pm);
         const bool pbig = __builtin_amdgcn_readfirstlane(big_s[B]) != 0;
-        const float shrink = pbig && shifted ? PV_UNSHIFT : 1.0f;
-        shifted = shifted && !pbig;
+        const bool drop = pbig || !(fabsf(mnew) < PV_MAX_SCORE);   // as in attn_item
+        const float shrink = drop && shifted ? PV_UNSHIFT : 1.0f;
+        shifted = shifted && !drop;
         const float alpha = (mrow == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mrow - mnew)) * shrink;
         lsum *= alpha;
 #pragma unroll

@@ -340,7 +340,7 @@ def test_attend_ignores_stale_rows_past_the_context(gpu):
             c.close()
 
 
-def test_attend_with_v_scales_beyond_the_shifted_split(gpu):
+def test_attend_beyond_the_shifted_split(gpu):
     """The P.V operand is p * s_v with p carried times 2^8 through the softmax,
     so that its f16 lo half stays normal; a page holding a V scale above 255
     (|V| > 32385 in its 32-channel group) would overflow that f16, and the
@@ -350,7 +350,13 @@ def test_attend_with_v_scales_beyond_the_shifted_split(gpu):
     matches the oracle (web/model/kernels.js:1255-1310 attn_av_gqa, f32 for
     any scale) within 2e-5 of max |out|, decode rows through each wave's own
     dequantisation and verify rows through the shared-page blocks, and each
-    verify row keeps the bits of the same row attended alone."""
+    verify row keeps the bits of the same row attended alone. Then the other
+    bound of the shift: rows whose scores reach past 4096 in log2 units
+    (queries times 5000) drop it on their own, so they stay finite and near
+    the oracle (within 1e-2 of max |out|: at such scores the softmax is one
+    token, and the f32 rounding of the scores themselves moves the rest),
+    while the rows beside them in the same verify job keep 2e-5 and every
+    row keeps the bits of the same row alone."""
     from oracle import lib as L
     from oracle import model as Mo
     for base in (configs.M27B, D256):
@@ -391,5 +397,25 @@ def test_attend_with_v_scales_beyond_the_shifted_split(gpu):
                     for i in range(n):
                         one = c.op_attend(0, 1, q[i:i + 1], tokens + i)
                         assert np.array_equal(one.view(np.uint32), got[i:i + 1].view(np.uint32)), (base["hidden"], i)
+            hot = [2, 5]
+            q = np.random.default_rng(tokens + 99).standard_normal((nv, nH * D)).astype(np.float32)
+            q[hot] *= 5000.0
+            got = c.op_attend(0, 1, q, tokens)
+            Qh = np.ascontiguousarray(q.reshape(nv, nH, D).transpose(1, 0, 2))
+            L.rope(Qh, D, tokens, om.tbl)
+            s = L.qk_scores(Qh, om.K[0], nv, tokens + nv, 64, D, nH, group, pages)
+            assert np.abs(s[:, hot]).max() * 1.4426950408889634 > 2 * 4096, "scores short of the bound"
+            p = L.causal_softmax(s, tokens)
+            want = L.attn_av(p, om.V[0], D, 64, group, pages).transpose(1, 0, 2).reshape(nv, nH * D)
+            assert np.isfinite(got).all(), base["hidden"]
+            cold = [i for i in range(nv) if i not in hot]
+            scale = max(1.0, np.abs(want).max())
+            err_hot = np.abs(got[hot] - want[hot]).max()
+            err_cold = np.abs(got[cold] - want[cold]).max()
+            assert err_hot <= 1e-2 * scale, (base["hidden"], err_hot)
+            assert err_cold <= 2e-5 * scale, (base["hidden"], err_cold)
+            for i in range(nv):
+                one = c.op_attend(0, 1, q[i:i + 1], tokens + i)
+                assert np.array_equal(one.view(np.uint32), got[i:i + 1].view(np.uint32)), (base["hidden"], "hot", i)
         finally:
             c.close()
