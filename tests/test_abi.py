@@ -45,3 +45,16 @@ def test_no_gpu_is_an_error_not_a_fallback():
     with pytest.raises(CCError) as e:
         Context(configs.with_layers(configs.SMOLLM2, 1), n_max=128, t_max=4, slots=1)
     assert e.value.status == 8   # CC_EDEVICE
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one MI355X: asked for more GPUs it exits with a
+    message (status 2) before touching any device, rather than reporting a
+    one-GPU figure under an N-GPU label."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], cwd=ROOT,
+                       stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=120)
+    assert r.returncode == 2, (r.returncode, r.stderr)
+    assert r.stdout == ""
+    assert "one MI355X" in r.stderr
